@@ -1,0 +1,120 @@
+"""Numpy writer of random-valid Pingala-8 native tensor slots (test infrastructure).
+
+Byte layout follows the reference's in-memory contract (patches/llama_cpu_vs_7ac59a6.patch:8-51 and
+:3817-3824): header A|B|c|NS|TRL|0, tile words M, fp16 scales S[b][r], 16-aligned payload D, then the
+side regions placed top-down from the slot end (delta, c16, prm, pinv, signs, trailer).
+Random payload words are always valid codes (every 8-bit index and every label bit is legal), as in the
+reference's timing arm (CPU.patch:4391-4458).
+"""
+import os
+
+import numpy as np
+
+NW = [0, 4, 6, 8, 10, 12, 16, 24]
+MAGIC0, MAGIC1 = 0x4E525656, 0x31354952
+HERE = os.path.dirname(os.path.abspath(__file__))
+TABLES = os.path.join(HERE, "golden", "tables_vrc.bin")
+
+
+def a16(n):
+    return (n + 15) & ~15
+
+
+def need(kbytes, rows, K, nd):
+    return a16(kbytes) + a16(8 * nd) + a16(2 * K) + 2 * a16(2 * rows) + 256 + 32 + 64
+
+
+def offsets(n, rows, K, nd):
+    t = n - 32
+    sg = t - 256
+    q = (sg - 2 * rows) & ~15
+    p = (q - 2 * rows) & ~15
+    c = (p - 2 * K) & ~15
+    e = (c - 8 * nd) & ~15
+    return dict(E=e, C=c, P=p, Q=q, SG=sg, T=t)
+
+
+def shipped_tables():
+    """(A uint32[256], c uint32): the shipped codebook, as raw little-endian int8 (tests/golden/tables_vrc.bin)."""
+    raw = np.fromfile(TABLES, np.int8)
+    A = raw[:1024].view(np.uint32).copy()
+    c = int(raw[1024:1028].view(np.uint32)[0])
+    return A, c
+
+
+def random_tables(rng):
+    """A in [-64, 64], c in [-16, 16] (the reference's random-valid arm, CPU.patch:4211-4220)."""
+    A = rng.integers(-64, 65, size=(256, 4)).astype(np.int8).view(np.uint32).reshape(256).copy()
+    c = int(rng.integers(-16, 17, size=4).astype(np.int8).view(np.uint32)[0])
+    return A, c
+
+
+def build_slot(A, cs, cls, payload, S, c16, prm, sg, drow=None, dcol=None, dval=None, extra=0):
+    """cls int[ng, nb]; payload uint32 in tile order (tile i = g*nb + b has 64*NW(cls) words);
+    S uint16 [nb, rows]; c16 uint16 [K]; prm int16 [rows]; sg int8 [256]; delta arrays (original indices)."""
+    ng, nb = cls.shape
+    rows, K = 32 * ng, 256 * nb
+    nt = ng * nb
+    nd = 0 if drow is None else len(drow)
+    M = np.zeros(nt, np.uint32)
+    off = 0
+    for i, c in enumerate(cls.reshape(-1)):
+        M[i] = off | (int(c) << 29)
+        off += 64 * NW[int(c)]
+    assert off == payload.size and off < (1 << 29)
+    offD = a16(2064 + 68 * nt)
+    kbytes = offD + 4 * payload.size
+    n = need(kbytes, rows, K, nd) + extra
+    buf = np.zeros(n, np.uint8)
+    w = buf[:2064].view(np.uint32)
+    w[0:256] = A
+    w[256:512] = A
+    w[512] = cs
+    w[513] = 108
+    w[514] = 2
+    w[515] = 0
+    buf[2064:2064 + 4 * nt] = M.view(np.uint8)
+    buf[2064 + 4 * nt:2064 + 68 * nt] = np.ascontiguousarray(S, np.uint16).reshape(-1).view(np.uint8)
+    buf[offD:kbytes] = payload.view(np.uint8)
+    o = offsets(n, rows, K, nd)
+    assert kbytes <= o["E"]
+    if nd:
+        buf[o["E"]:o["E"] + 2 * nd] = np.asarray(drow, np.uint16).view(np.uint8)
+        buf[o["E"] + 2 * nd:o["E"] + 4 * nd] = np.asarray(dcol, np.uint16).view(np.uint8)
+        buf[o["E"] + 4 * nd:o["E"] + 8 * nd] = np.asarray(dval, np.float32).view(np.uint8)
+    buf[o["C"]:o["C"] + 2 * K] = np.ascontiguousarray(c16, np.uint16).view(np.uint8)
+    prm = np.asarray(prm, np.int16)
+    pinv = np.empty(rows, np.int16)
+    pinv[prm.astype(np.int64)] = np.arange(rows, dtype=np.int16)
+    buf[o["P"]:o["P"] + 2 * rows] = prm.view(np.uint8)
+    buf[o["Q"]:o["Q"] + 2 * rows] = pinv.view(np.uint8)
+    buf[o["SG"]:o["SG"] + 256] = np.asarray(sg, np.int8).view(np.uint8)
+    buf[o["T"]:o["T"] + 32] = np.array([MAGIC0, MAGIC1, kbytes, nd, rows, K, 108, 1], np.uint32).view(np.uint8)
+    return buf
+
+
+def random_slot(rng, rows, K, classes=(3,), class_p=None, tables="shipped", nd=0, permute=True,
+                c16="random", scale_range=(2e-4, 3e-4), extra=0):
+    """A random-valid tensor. classes: classes drawn per tile (with probabilities class_p)."""
+    ng, nb = rows // 32, K // 256
+    A, cs = shipped_tables() if tables == "shipped" else random_tables(rng)
+    cls = rng.choice(np.asarray(classes), size=(ng, nb), p=class_p).astype(np.int64)
+    nwords = int(sum(64 * NW[c] for c in cls.reshape(-1)))
+    payload = rng.integers(0, 1 << 32, size=nwords, dtype=np.uint64).astype(np.uint32)
+    S = rng.uniform(*scale_range, size=(nb, rows)).astype(np.float16).view(np.uint16)
+    S[np.repeat(cls.T == 0, 32, axis=1)] = 0
+    if c16 == "random":
+        c16v = rng.uniform(0.5, 2.0, size=K).astype(np.float16).view(np.uint16)
+    else:
+        c16v = np.full(K, 0x3C00, np.uint16)
+    prm = rng.permutation(rows).astype(np.int16) if permute else np.arange(rows, dtype=np.int16)
+    sg = np.where(rng.integers(0, 2, 256) == 1, 1, -1).astype(np.int8)
+    drow = dcol = dval = None
+    if nd:
+        flat = rng.choice(rows * K, size=nd, replace=False)
+        order = np.argsort(flat)
+        flat = flat[order]
+        drow = (flat // K).astype(np.uint16)
+        dcol = (flat % K).astype(np.uint16)
+        dval = rng.uniform(-0.05, 0.05, size=nd).astype(np.float32)
+    return build_slot(A, cs, cls, payload, S, c16v, prm, sg, drow, dcol, dval, extra=extra)
