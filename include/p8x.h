@@ -1,0 +1,131 @@
+/*
+ * p8x.h -- C ABI of the MI355X (gfx950) Pingala-8 hot path: block decode of the 2-bit coset-trellis
+ * weight tiles and the fused decode x activation products that consume them.
+ *
+ * Reference interfaces replaced (patches/llama_cpu_vs_7ac59a6.patch, "CPU.patch"):
+ *   tensor contract ......... ggml/include/ggml-vr-native.h (CPU.patch:1-51)
+ *   probe / prepare ......... vrc_probe, vrc_init (CPU.patch:234-275); vr_native_probe,
+ *                             vr_prepare_native (CPU.patch:1955-1965, :4335-4390)
+ *   dequantize_row .......... vrc_dequant_f32 (CPU.patch:1012-1027), vrc_decode_tile_int (:992-1010)
+ *   dequant to fp16 ......... ggml_cuda_f44_to_fp16/_fp32 hooks (CPU.patch:1351-1365); for VR tensors
+ *                             the role of k_r51_k1 (CPU.patch:2176-2235)
+ *   activation quantization . vrc_prep_block (CPU.patch:559-571), k_vr_qx_real (:4292-4307);
+ *                             ggml quantize_q8_1 (stock llama.cpp, called at CPU.patch:1576)
+ *   vec_dot ................. vrc_tile / vrc_dot128 (CPU.patch:617-668)
+ *   mul_mat_vec ............. vr_mul_mat_vec + k_vr (CPU.patch:4466-4521, :3951-4016), vrc_tg (:1161-1199),
+ *                             ggml_cuda_f44_mul_mat_vec (:2615-2631)
+ *   mul_mat (prompt) ........ ggml_cuda_f44_mul_mat_q8 (CPU.patch:2303-2343)
+ *
+ * Conventions (as the reference): weights W are [rows][K] (ggml ne0 = K); y[rows] = W x. Tiles are
+ * 32 sorted rows x 256 columns; outputs are written in ORIGINAL row order (prm un-permute) and the sparse
+ * clamp delta is applied on the original activations. Differences: status codes instead of aborts,
+ * explicit handles instead of a global registry, deterministic reductions instead of float atomics.
+ *
+ * Every function returns P8X_OK (0) or a P8X_ERR_* code; p8x_last_error() gives a thread-local message.
+ * Device entry points take device pointers and a hipStream_t passed as void* (NULL = null stream); they
+ * are asynchronous. Calls that share one p8x_tensor use its workspace and must be ordered on one stream.
+ */
+#ifndef P8X_H
+#define P8X_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    P8X_OK = 0,
+    P8X_ERR_ARG = 1,          /* bad argument (null pointer, shape, out of range) */
+    P8X_ERR_FORMAT = 2,       /* slot bytes fail the tensor contract checks */
+    P8X_ERR_HIP = 3,          /* a HIP runtime call failed */
+    P8X_ERR_UNSUPPORTED = 4,  /* valid request this build does not serve */
+    P8X_ERR_NOMEM = 5
+};
+
+enum { P8X_F32 = 0, P8X_F16 = 1, P8X_BF16 = 2, P8X_I16 = 3 };
+enum { P8X_DOMAIN_ORIGINAL = 0, P8X_DOMAIN_ROTATED = 1 };
+enum { P8X_ACT_Q8_128 = 0, P8X_ACT_Q8_1 = 1 };
+
+#define P8X_MAX_COLS 8
+
+typedef struct p8x_tensor p8x_tensor;
+
+typedef struct p8x_info {
+    int rows, K, nd, ng, nb;
+    size_t n;               /* slot bytes */
+    size_t kbytes;          /* kernel bytes (header + M + S + D) */
+    size_t stream_bytes;    /* packed weight stream read by a GEMV: M words + S + D payload */
+    size_t class_tiles[8];  /* tiles per class 0..7 */
+    const void *dev_base;   /* device address of the slot bytes */
+} p8x_info;
+
+const char *p8x_version(void);
+const char *p8x_error_string(int code);
+const char *p8x_last_error(void);
+
+/* ---- tensor contract (CPU.patch:25-51) ------------------------------------------------------------ */
+/* bytes a slot needs: vrn_need (CPU.patch:27-29) */
+size_t p8x_need(size_t kbytes, int rows, int K, int nd);
+/* 1 if the host bytes carry a native trailer for this shape, else 0: vrc_probe (CPU.patch:234-238) */
+int p8x_probe(const void *slot, size_t n, int rows, int K);
+
+/* Validate a slot and build its device-side metadata: vrc_init + vr_prepare_native (CPU.patch:240-275,
+ * :4335-4390). on_device = 0: `slot` is host memory and is copied to a device allocation the handle owns;
+ * on_device = 1: `slot` is device memory that must outlive the handle. The only allocating call. */
+int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_tensor **out);
+void p8x_release(p8x_tensor *t);
+int p8x_tensor_info(const p8x_tensor *t, p8x_info *out);
+
+/* ---- decode / dequantize_row ---------------------------------------------------------------------- */
+/* Original-domain weights of the whole tensor, row r of `out` = ORIGINAL row r, row stride `ld` elements,
+ * dtype P8X_F32 | P8X_F16 | P8X_BF16. F32 is bit-exact to vrc_dequant_f32 (CPU.patch:1012-1027); F16/BF16
+ * are that F32 rounded to nearest even. */
+int p8x_dequantize(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream);
+/* Rotated-domain sorted-row weights: P8X_I16 = exact tile ints (vrc_decode_tile_int, CPU.patch:992-1010),
+ * P8X_F32 = int * S (vr_wint * vr_wscale, CPU.patch:4030-4071). out is [rows][ld]. */
+int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream);
+
+/* ---- activations ------------------------------------------------------------------------------------ */
+/* x' = FWHT256(x * sg / c) / 16, 8-bit per 128-column half-slice: q [ncols][K] int8, d [ncols][K/128]
+ * (d = amax/127), sum [ncols][K/128] (sum of q; may be NULL). Bit-exact to vrc_prep_block / k_vr_qx_real. */
+int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx,
+                        int8_t *q, float *d, int32_t *sum, void *stream);
+/* x' quantized to ggml block_q8_1 (36 B: fp16 d, fp16 s, 32 x int8), [ncols][K/32] blocks. */
+int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, void *stream);
+
+/* ---- products --------------------------------------------------------------------------------------- */
+/* vec_dot against pre-quantized activations (vrc_tile, CPU.patch:617-668): act = P8X_ACT_Q8_128 (q, d from
+ * p8x_quantize_q8_128, `d` required) or P8X_ACT_Q8_1 (q = block_q8_1 array, d ignored). Writes y [ncols][ldy]
+ * in ORIGINAL rows WITHOUT the clamp delta (it needs the unquantized x). partials (optional, sorted rows):
+ * int32 [ncols][rows][K/128] for Q8_128 or [ncols][rows][K/32] for Q8_1, the exact integer dot of each row
+ * with each quantization block. */
+int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols,
+                float *y, size_t ldy, int32_t *partials, void *stream);
+/* y = W x for 1..8 columns (vr_mul_mat_vec, CPU.patch:4466-4521): activation prep + fused decode-GEMV +
+ * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. */
+int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
+int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
+/* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T with X in
+ * P8X_F32 or P8X_BF16. Weight tiles are decoded to fp16 in LDS and fed to MFMA with fp32 accumulation. */
+int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream);
+
+/* ---- host-side producers (not on the hot path) -------------------------------------------------------- */
+/* Random valid tensor slot (the reference's random-valid timing arm, CPU.patch:4391-4458). class_p[8] are
+ * tile-class probabilities; codebook 0 = the shipped table (research/work/r48k3/tables_vrc.pt), 1 = random
+ * A in [-64,64], c in [-16,16]. Writes at most cap bytes into out; *n_out = slot size. */
+int p8x_synth_random(uint64_t seed, int rows, int K, const double *class_p, int codebook, int nd,
+                     int permute_rows, void *out, size_t cap, size_t *n_out);
+/* Quantize f32 weights W [rows][K] to a class-3 slot with the plain-MSE 8-state Viterbi (the identity-Hessian
+ * case of the reference encoder, research/detail/r59_sourcecoding.py:39-98, r48k.py:213-239): S = fp16(1.05
+ * rms/23.557) per 256 block of the rotated row, c16 per column, seeded Hadamard signs, clamp delta for
+ * |W| > fp16(1.001 max|W|). c16 may be NULL (all ones). */
+int p8x_quantize_tensor(const float *W, int rows, int K, const uint16_t *c16, uint64_t sign_seed,
+                        void *out, size_t cap, size_t *n_out);
+/* bytes the two producers need */
+size_t p8x_slot_bytes(int rows, int K, const size_t class_tiles[8], int nd);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

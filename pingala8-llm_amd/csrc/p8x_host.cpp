@@ -1,0 +1,309 @@
+// p8x_host.cpp -- host side of the C ABI: slot validation, device metadata, argument checks.
+//
+// p8x_prepare restates the reference's load-time checks and derived data: trailer/header checks and
+// ic = sg / c (vrc_init, CPU.patch:240-275), kbytes against the M words and the delta CSR by original row
+// (vr_prepare_native, CPU.patch:4335-4390). Failures return P8X_ERR_FORMAT instead of aborting.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "p8x_internal.h"
+
+namespace p8x {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return P8X_OK;
+    return set_error(P8X_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int num_cus() {
+    static int cus = -1;
+    if (cus < 0) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess) cus = prop.multiProcessorCount;
+        else cus = 256;
+    }
+    return cus;
+}
+
+static int nw_tile(uint32_t m) { return nw_of((int)(m >> 29)); }
+
+}  // namespace p8x
+
+using namespace p8x;
+
+extern "C" {
+
+const char *p8x_version(void) { return "p8x 0.1 (gfx950)"; }
+
+const char *p8x_error_string(int code) {
+    switch (code) {
+        case P8X_OK: return "ok";
+        case P8X_ERR_ARG: return "invalid argument";
+        case P8X_ERR_FORMAT: return "slot bytes fail the tensor contract";
+        case P8X_ERR_HIP: return "HIP runtime error";
+        case P8X_ERR_UNSUPPORTED: return "unsupported request";
+        case P8X_ERR_NOMEM: return "out of memory";
+        default: return "unknown error";
+    }
+}
+
+const char *p8x_last_error(void) { return g_err; }
+
+size_t p8x_need(size_t kbytes, int rows, int K, int nd) {
+    return align16(kbytes) + align16(8 * (size_t)nd) + align16(2 * (size_t)K) + 2 * align16(2 * (size_t)rows) + 256 + 32 + 64;
+}
+
+int p8x_probe(const void *slot, size_t n, int rows, int K) {
+    if (!slot || n < 4096) return 0;
+    uint32_t tr[8];
+    memcpy(tr, (const uint8_t *)slot + n - 32, 32);
+    return tr[0] == kMagic0 && tr[1] == kMagic1 && tr[4] == (uint32_t)rows && tr[5] == (uint32_t)K && tr[6] == kNS;
+}
+
+static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]) {
+    const size_t t = n - 32, sg = t - 256;
+    const size_t q = (sg - 2 * rows) & ~(size_t)15;
+    const size_t p = (q - 2 * rows) & ~(size_t)15;
+    const size_t c = (p - 2 * K) & ~(size_t)15;
+    const size_t e = (c - 8 * nd) & ~(size_t)15;
+    off[0] = e; off[1] = c; off[2] = p; off[3] = q; off[4] = sg; off[5] = t;
+}
+
+void p8x_release(p8x_tensor *t) {
+    if (!t) return;
+    for (void *p : {(void *)t->owned, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->wx16})
+        if (p) (void)hipFree(p);
+    delete t;
+}
+
+int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_tensor **out) {
+    if (!slot || !out) return set_error(P8X_ERR_ARG, "p8x_prepare: null pointer");
+    *out = nullptr;
+    if (rows <= 0 || K <= 0 || K % 256 || rows % 32 || rows >= 32768)
+        return set_error(P8X_ERR_ARG, "p8x_prepare: shape %d x %d (need K %% 256 == 0, rows %% 32 == 0, rows < 32768)", rows, K);
+    if (n < 4096) return set_error(P8X_ERR_FORMAT, "p8x_prepare: slot of %zu bytes is too small", n);
+    const uint8_t *src = (const uint8_t *)slot;
+    auto fetch = [&](size_t off, size_t len, void *dst) -> int {
+        if (off + len > n) return set_error(P8X_ERR_FORMAT, "p8x_prepare: region [%zu, %zu) beyond the slot", off, off + len);
+        if (!len) return P8X_OK;
+        if (on_device) return hip_check(hipMemcpy(dst, src + off, len, hipMemcpyDeviceToHost), "p8x_prepare: read slot");
+        memcpy(dst, src + off, len);
+        return P8X_OK;
+    };
+    int rc;
+    uint32_t tr[8];
+    if ((rc = fetch(n - 32, 32, tr))) return rc;
+    if (tr[0] != kMagic0 || tr[1] != kMagic1)
+        return set_error(P8X_ERR_FORMAT, "p8x_prepare: bad trailer magic %08x %08x", tr[0], tr[1]);
+    if (tr[4] != (uint32_t)rows || tr[5] != (uint32_t)K || tr[6] != kNS)
+        return set_error(P8X_ERR_FORMAT, "p8x_prepare: trailer rows %u K %u ns %u, expected %d %d %u", tr[4], tr[5], tr[6], rows, K, kNS);
+    const int nb = K / 256, ng = rows / 32, nsl = K / 128, nd = (int)tr[3];
+    const size_t nt = (size_t)ng * nb, kbytes = tr[2];
+    std::vector<uint32_t> hdr(516), M(nt);
+    if ((rc = fetch(0, 2064, hdr.data()))) return rc;
+    if (hdr[513] != kNS || hdr[514] != kTRL)
+        return set_error(P8X_ERR_FORMAT, "p8x_prepare: header NS %u TRL %u (need %u, %u)", hdr[513], hdr[514], kNS, kTRL);
+    if ((rc = fetch(kHeaderBytes, 4 * nt, M.data()))) return rc;
+    size_t off[6];
+    if ((size_t)nd > n / 8) return set_error(P8X_ERR_FORMAT, "p8x_prepare: delta count %d too large", nd);
+    side_offsets(n, (size_t)rows, (size_t)K, (size_t)nd, off);
+    if (off[0] > n || kbytes > off[0]) return set_error(P8X_ERR_FORMAT, "p8x_prepare: kbytes %zu overlaps the side regions", kbytes);
+    size_t words = 0, hist[8] = {0};
+    for (size_t i = 0; i < nt; ++i) { words += (size_t)64 * nw_tile(M[i]); hist[M[i] >> 29]++; }
+    if (offset_D(nt) + 4 * words != kbytes)
+        return set_error(P8X_ERR_FORMAT, "p8x_prepare: kbytes %zu != M-implied %zu", kbytes, offset_D(nt) + 4 * words);
+    for (size_t i = 0; i < nt; ++i) {   // every tile's payload must lie inside D
+        const size_t o = M[i] & 0x1FFFFFFFu;
+        if (o + (size_t)64 * nw_tile(M[i]) > words)
+            return set_error(P8X_ERR_FORMAT, "p8x_prepare: tile %zu payload offset %zu out of range", i, o);
+    }
+    std::vector<uint16_t> c16(K);
+    std::vector<int16_t> prm(rows);
+    std::vector<int8_t> sg(256);
+    std::vector<uint16_t> drow(nd), dcol(nd);
+    std::vector<float> dval(nd);
+    if ((rc = fetch(off[1], 2 * (size_t)K, c16.data()))) return rc;
+    if ((rc = fetch(off[2], 2 * (size_t)rows, prm.data()))) return rc;
+    if ((rc = fetch(off[4], 256, sg.data()))) return rc;
+    if (nd) {
+        if ((rc = fetch(off[0], 2 * (size_t)nd, drow.data()))) return rc;
+        if ((rc = fetch(off[0] + 2 * (size_t)nd, 2 * (size_t)nd, dcol.data()))) return rc;
+        if ((rc = fetch(off[0] + 4 * (size_t)nd, 4 * (size_t)nd, dval.data()))) return rc;
+    }
+    {   // prm must be a permutation (CPU.patch:4852-4857)
+        std::vector<char> seen(rows, 0);
+        for (int r = 0; r < rows; ++r) {
+            if (prm[r] < 0 || prm[r] >= rows || seen[prm[r]]) return set_error(P8X_ERR_FORMAT, "p8x_prepare: prm is not a permutation (row %d)", r);
+            seen[prm[r]] = 1;
+        }
+    }
+    for (int e = 0; e < nd; ++e)
+        if (drow[e] >= rows || dcol[e] >= K) return set_error(P8X_ERR_FORMAT, "p8x_prepare: delta entry %d out of range", e);
+    for (int i = 0; i < 256; ++i)
+        if (sg[i] != 1 && sg[i] != -1) return set_error(P8X_ERR_FORMAT, "p8x_prepare: Hadamard sign %d is %d", i, sg[i]);
+
+    // derived host data
+    std::vector<uint32_t> a2(512);
+    bool wrap_free = true;
+    for (int f = 0; f < 256; ++f) {
+        a2[f] = hdr[f];
+        a2[256 + f] = add_bytes(hdr[f], hdr[512]);
+        for (int e = 0; e < 4; ++e) {
+            const int s = (int)(int8_t)(hdr[f] >> (8 * e)) + (int)(int8_t)(hdr[512] >> (8 * e));
+            if (s < -128 || s > 127) wrap_free = false;
+        }
+    }
+    std::vector<float> ic(K);
+    for (int k = 0; k < K; ++k) ic[k] = (float)sg[k & 255] / half_to_float(c16[k]);
+    std::vector<int> cp(rows + 1, 0);
+    std::vector<uint16_t> cc(nd);
+    std::vector<float> cv(nd);
+    for (int e = 0; e < nd; ++e) cp[drow[e] + 1]++;
+    for (int r = 0; r < rows; ++r) cp[r + 1] += cp[r];
+    {
+        std::vector<int> fill(cp.begin(), cp.end() - 1);
+        for (int e = 0; e < nd; ++e) { const int q = fill[drow[e]]++; cc[q] = dcol[e]; cv[q] = dval[e]; }
+    }
+
+    p8x_tensor *t = new p8x_tensor();
+    t->rows = rows; t->K = K; t->nb = nb; t->ng = ng; t->nsl = nsl; t->nd = nd;
+    t->n = n; t->nt = nt; t->kbytes = kbytes;
+    t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
+    for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
+    t->wrap_free = wrap_free;
+    (void)hipGetDevice(&t->device);
+    auto fail = [&](int code) { p8x_release(t); return code; };
+    auto alloc = [&](void **p, size_t bytes, const char *what) -> int {
+        if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return set_error(P8X_ERR_NOMEM, "p8x_prepare: hipMalloc %s (%zu B)", what, bytes);
+        return P8X_OK;
+    };
+    if (on_device) {
+        t->base = src;
+    } else {
+        if ((rc = alloc((void **)&t->owned, n, "slot"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->owned, src, n, hipMemcpyHostToDevice), "p8x_prepare: upload slot"))) return fail(rc);
+        t->base = t->owned;
+    }
+    t->M = (const uint32_t *)(t->base + kHeaderBytes);
+    t->S = (const uint16_t *)(t->base + offset_S(nt));
+    t->D = (const uint32_t *)(t->base + offset_D(nt));
+    t->prm = (const int16_t *)(t->base + off[2]);
+    const GemvPlan plan = gemv_plan(t, 1);
+    t->gemv_bpk = plan.bpk; t->gemv_nks = plan.nks;
+    if ((rc = alloc((void **)&t->a2, 512 * 4, "tables"))) return fail(rc);
+    if ((rc = alloc((void **)&t->ic, 4 * (size_t)K, "ic"))) return fail(rc);
+    if ((rc = alloc((void **)&t->cp, 4 * (size_t)(rows + 1), "delta rows"))) return fail(rc);
+    if ((rc = alloc((void **)&t->cc, 2 * (size_t)nd, "delta cols"))) return fail(rc);
+    if ((rc = alloc((void **)&t->cv, 4 * (size_t)nd, "delta values"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wq, (size_t)P8X_MAX_COLS * K, "q"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wd, 4 * (size_t)P8X_MAX_COLS * nsl, "d"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wsum, 4 * (size_t)P8X_MAX_COLS * nsl, "sum"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wpart, 4 * (size_t)t->gemv_nks * P8X_MAX_COLS * rows, "partials"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
+    if ((rc = hip_check(hipMemcpy(t->a2, a2.data(), 512 * 4, hipMemcpyHostToDevice), "p8x_prepare: tables"))) return fail(rc);
+    if ((rc = hip_check(hipMemcpy(t->ic, ic.data(), 4 * (size_t)K, hipMemcpyHostToDevice), "p8x_prepare: ic"))) return fail(rc);
+    if ((rc = hip_check(hipMemcpy(t->cp, cp.data(), 4 * (size_t)(rows + 1), hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);
+    if (nd) {
+        if ((rc = hip_check(hipMemcpy(t->cc, cc.data(), 2 * (size_t)nd, hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->cv, cv.data(), 4 * (size_t)nd, hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);
+    }
+    if ((rc = hip_check(hipMemset(t->wcnt, 0, 4 * (size_t)ng), "p8x_prepare: counters"))) return fail(rc);
+    if ((rc = hip_check(hipDeviceSynchronize(), "p8x_prepare: sync"))) return fail(rc);
+    *out = t;
+    return P8X_OK;
+}
+
+int p8x_tensor_info(const p8x_tensor *t, p8x_info *o) {
+    if (!t || !o) return set_error(P8X_ERR_ARG, "p8x_tensor_info: null pointer");
+    o->rows = t->rows; o->K = t->K; o->nd = t->nd; o->ng = t->ng; o->nb = t->nb;
+    o->n = t->n; o->kbytes = t->kbytes; o->stream_bytes = t->stream_bytes;
+    for (int c = 0; c < 8; ++c) o->class_tiles[c] = t->class_tiles[c];
+    o->dev_base = t->base;
+    return P8X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------- device entry points
+int p8x_dequantize(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream) {
+    if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_dequantize: null pointer");
+    if (dtype != P8X_F32 && dtype != P8X_F16 && dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_dequantize: dtype %d", dtype);
+    if (ld < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_dequantize: ld %zu < K %d", ld, t->K);
+    return launch_dequant(t, dtype, out, ld, (hipStream_t)stream);
+}
+
+int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream) {
+    if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: null pointer");
+    if (dtype != P8X_I16 && dtype != P8X_F32) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: dtype %d", dtype);
+    if (ld < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: ld %zu < K %d", ld, t->K);
+    return launch_decode_rotated(t, dtype, out, ld, (hipStream_t)stream);
+}
+
+int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, void *stream) {
+    if (!t || !x || !q || !d) return set_error(P8X_ERR_ARG, "p8x_quantize_q8_128: null pointer");
+    if (ncols < 1 || ldx < (size_t)t->K || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "p8x_quantize_q8_128: ncols %d ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", ncols, ldx);
+    return launch_act_q8_128(t, x, ncols, ldx, q, d, sum, (hipStream_t)stream);
+}
+
+int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, void *stream) {
+    if (!t || !x || !blocks) return set_error(P8X_ERR_ARG, "p8x_quantize_q8_1: null pointer");
+    if (ncols < 1 || ldx < (size_t)t->K || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "p8x_quantize_q8_1: ncols %d ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", ncols, ldx);
+    return launch_act_q8_1(t, x, ncols, ldx, blocks, (hipStream_t)stream);
+}
+
+int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, float *y, size_t ldy, int32_t *partials, void *stream) {
+    if (!t || !q || !y) return set_error(P8X_ERR_ARG, "p8x_vec_dot: null pointer");
+    if (act != P8X_ACT_Q8_128 && act != P8X_ACT_Q8_1) return set_error(P8X_ERR_ARG, "p8x_vec_dot: act %d", act);
+    if (act == P8X_ACT_Q8_128 && !d) return set_error(P8X_ERR_ARG, "p8x_vec_dot: Q8_128 needs d");
+    if (ncols < 1 || ncols > P8X_MAX_COLS || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_vec_dot: ncols %d ldy %zu", ncols, ldy);
+    return launch_gemv(t, act, q, d, ncols, nullptr, 0, y, ldy, partials, (hipStream_t)stream);
+}
+
+int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream) {
+    if (!t || !x || !y) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: null pointer");
+    if (ncols < 1 || ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: ncols %d (1..%d)", ncols, P8X_MAX_COLS);
+    if (ldx < (size_t)t->K || ldy < (size_t)t->rows || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: ldx %zu ldy %zu (x 16-byte aligned, ldx %% 4 == 0)", ldx, ldy);
+    hipStream_t st = (hipStream_t)stream;
+    int rc;
+    if (act == P8X_ACT_Q8_128) {
+        if ((rc = launch_act_q8_128(t, x, ncols, ldx, t->wq, t->wd, nullptr, st))) return rc;
+        return launch_gemv(t, act, t->wq, t->wd, ncols, x, ldx, y, ldy, nullptr, st);
+    }
+    if (act == P8X_ACT_Q8_1) {
+        if ((rc = launch_act_q8_1(t, x, ncols, ldx, t->wq81, st))) return rc;
+        return launch_gemv(t, act, t->wq81, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
+    }
+    return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: act %d", act);
+}
+
+int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream) {
+    return p8x_mul_mat_vec_act(t, P8X_ACT_Q8_128, x, ncols, ldx, y, ldy, stream);
+}
+
+int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream) {
+    if (!t || !x || !y) return set_error(P8X_ERR_ARG, "p8x_mul_mat: null pointer");
+    if (x_dtype != P8X_F32 && x_dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x dtype %d", x_dtype);
+    if (N < 1 || ldx < (size_t)t->K || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat: N %d ldx %zu ldy %zu", N, ldx, ldy);
+    return launch_mul_mat(t, x, x_dtype, N, ldx, y, ldy, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// p8x_internal.h -- library-internal types shared by the host code and the kernel launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/p8x.h"
+#include "p8x_format.h"
+
+struct p8x_tensor {
+    int rows = 0, K = 0, nb = 0, ng = 0, nsl = 0, nd = 0;
+    size_t n = 0, nt = 0, kbytes = 0, stream_bytes = 0;
+    size_t class_tiles[8] = {0};
+    int device = 0;
+    const uint8_t *base = nullptr;   // device slot bytes
+    uint8_t *owned = nullptr;        // set when the library copied host bytes
+    // views into the slot (device)
+    const uint32_t *M = nullptr;
+    const uint16_t *S = nullptr;
+    const uint32_t *D = nullptr;
+    const int16_t *prm = nullptr;
+    // device metadata built at prepare
+    uint32_t *a2 = nullptr;          // [2][256]: A[f] + h c (bytewise), h-major
+    float *ic = nullptr;             // sg / c per column [K]
+    int *cp = nullptr;               // delta CSR by original row [rows + 1]
+    uint16_t *cc = nullptr;          // [nd]
+    float *cv = nullptr;             // [nd]
+    // workspace (stream-ordered use)
+    int8_t *wq = nullptr;            // q8_128 activations [P8X_MAX_COLS][K]
+    float *wd = nullptr;             // [P8X_MAX_COLS][nsl]
+    int32_t *wsum = nullptr;         // [P8X_MAX_COLS][nsl]
+    uint8_t *wq81 = nullptr;         // block_q8_1 [P8X_MAX_COLS][K / 32]
+    float *wpart = nullptr;          // split-K partial rows [nks][P8X_MAX_COLS][rows]
+    unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
+    uint16_t *wx16 = nullptr;        // rotated fp16 activations for the prompt GEMM (grown on demand)
+    size_t wx16_elems = 0;
+    int gemv_bpk = 8, gemv_nks = 1;  // GEMV work split: blocks per item, items per row group
+    bool wrap_free = true;           // |A + c| <= 127 bytewise
+};
+
+namespace p8x {
+
+int set_error(int code, const char *fmt, ...);
+int hip_check(hipError_t e, const char *what);
+
+struct GemvPlan {
+    int bpk, nks, grid, items;
+};
+GemvPlan gemv_plan(const p8x_tensor *t, int ncols);
+
+// launchers (p8x_gemv.hip, p8x_decode.hip, p8x_gemm.hip)
+int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st);
+int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, hipStream_t st);
+int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
+                float *y, size_t ldy, int32_t *partials, hipStream_t st);
+int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
+int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
+int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st);
+
+int num_cus();
+
+}  // namespace p8x

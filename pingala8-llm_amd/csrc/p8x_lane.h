@@ -1,0 +1,153 @@
+// p8x_lane.h -- gfx950 lane-slice decoder shared by every kernel.
+//
+// One wave64 owns one tile (g, b): lane L decodes half-slice hs = L >> 5 of sorted row 32g + (L & 31).
+// A lane-slice is NW(c) payload words holding 32 fields per stage; step k of lane j encodes chunk
+// t = (j + k) & 31 (CPU.patch:155-158). Here every lane loads its words already rotated by j fields
+// (per-lane load addresses plus one v_alignbit per word), so field t of the rotated registers IS chunk t
+// for every lane: all later indexing is compile-time and the activation chunk is the same for all 32
+// lanes of a half-wave (an LDS broadcast).
+//
+// Coset table in LDS: entry (f, h) = A[f] + h * c (bytewise, CPU.patch:221/:255), replicated across the
+// 32 LDS banks: byte address (f << 8) | (h << 7) | (bank << 2) with bank = lane & 31, so the 32 lanes of a
+// half-wave never conflict. One v_perm_b32 builds that address from the 8-bit field and a per-lane byte
+// holding (h << 7) | (bank << 2).
+//
+// Trellis (CPU.patch:159-160, :277-283): labels z_t in chunk order -> u_t = z_t ^ u_{t-1} ^ u_{t-3},
+// h_t = u_{t-2}; computed in closed form on the 32-bit label word.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "p8x_format.h"
+
+namespace p8x {
+
+constexpr int kTabWords = 256 * 64;   // 64 KB coset table
+constexpr int kTabBytes = kTabWords * 4;
+
+// Fill the replicated table from a2 = [h][256] words (h-major), all threads of the block.
+__device__ __forceinline__ void build_coset_table(uint32_t *tab, const uint32_t *__restrict__ a2, int tid, int nthreads) {
+    uint4 *t4 = reinterpret_cast<uint4 *>(tab);
+    for (int i = tid; i < kTabWords / 4; i += nthreads) {
+        const int f = i >> 4, h = (i >> 3) & 1;
+        const uint32_t v = a2[h * 256 + f];
+        t4[i] = make_uint4(v, v, v, v);
+    }
+}
+
+__device__ __forceinline__ uint32_t lds_word(const uint32_t *tab, uint32_t byte_addr) {
+    return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(tab) + byte_addr);
+}
+
+// closed form of the 8-state trellis over one 32-chunk label word (chunk order in, chunk order out)
+__device__ __forceinline__ uint32_t trellis_coset_bits(uint32_t z) {
+    uint32_t u = z;
+    u ^= (u << 1) ^ (u << 3);
+    u ^= (u << 2) ^ (u << 6);
+    u ^= (u << 4) ^ (u << 12);
+    u ^= (u << 8) ^ (u << 24);
+    u ^= u << 16;
+    return u << 2;
+}
+
+// address of word i of lane j inside a half-slice: [i >> 1][j][i & 1] (CPU.patch:292-297)
+__device__ __forceinline__ int lane_word_offset(int i, int j) { return ((i >> 1) << 6) + 2 * j + (i & 1); }
+
+// Load a region of W words (32 fields of W bits) starting at lane word WB, rotated so field t = chunk t.
+// R = original rotated right by r = W * (32 - j) bits (mod 32 W).
+template <int W, int WB>
+__device__ __forceinline__ void load_region(const uint32_t *__restrict__ p, int j, uint32_t (&R)[W]) {
+    const int r = ((32 - j) & 31) * W;
+    const int wr = r >> 5, br = r & 31;
+    uint32_t L[W];
+#pragma unroll
+    for (int m = 0; m < W; ++m) {
+        const int i = WB + (m + wr) % W;
+        L[m] = __builtin_nontemporal_load(p + lane_word_offset(i, j));
+    }
+#pragma unroll
+    for (int i = 0; i < W; ++i) R[i] = __builtin_amdgcn_alignbit(L[(i + 1) % W], L[i], br);
+}
+
+template <int W, int N>
+__device__ __forceinline__ uint32_t field_of(const uint32_t (&R)[N], int t) {
+    const int pos = W * t, wi = pos >> 5, bb = pos & 31;
+    if (bb + W <= 32) return __builtin_amdgcn_ubfe(R[wi], bb, W);
+    return __builtin_amdgcn_alignbit(R[(wi + 1) % N], R[wi], bb) & ((1u << W) - 1u);
+}
+
+// chunk-order labels of a W1 = 8 stage-1 region: bit t = bit 7 of byte t
+__device__ __forceinline__ uint32_t labels_from_bytes(const uint32_t (&R)[8]) {
+    uint32_t n[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = __builtin_amdgcn_udot4(R[2 * q] & 0x80808080u, 0x08040201u, 0u, false);
+        n[q] = __builtin_amdgcn_udot4(R[2 * q + 1] & 0x80808080u, 0x80402010u, lo, false);   // bits 7..14
+    }
+    return (n[0] >> 7) | (n[1] << 1) | (n[2] << 9) | (n[3] << 17);
+}
+
+// per-lane address bytes for 4 chunks: byte e = (h_{4q+e} << 7) | (bank << 2)
+__device__ __forceinline__ void coset_bytes(uint32_t H, uint32_t bankbytes, uint32_t (&hb)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const uint32_t nib = __builtin_amdgcn_ubfe(H, 4 * q, 4);
+        const uint32_t spread = (nib * 0x00204081u) & 0x01010101u;
+        hb[q] = (spread << 7) | bankbytes;
+    }
+}
+
+// Decoded state of one lane-slice of class C.
+template <int C>
+struct LaneSlice {
+    static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
+    static constexpr int NR1 = W1 == 8 ? 8 : (W1 > 0 ? W1 - 1 : 1);
+    static constexpr int NR2 = W2 ? W2 : 1, NR3 = W3 ? W3 : 1;
+    uint32_t r0;           // W1 < 8: label word, chunk order
+    uint32_t r1[NR1];
+    uint32_t r2[NR2];
+    uint32_t r3[NR3];
+    uint32_t hb[8];
+
+    // p = half-slice base (tile payload + hs * NW * 32), j = lane row
+    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j) {
+        if constexpr (W1 == 8) {
+            load_region<8, 0>(p, j, r1);
+        } else {
+            const uint32_t w0 = __builtin_nontemporal_load(p + lane_word_offset(0, j));
+            r0 = __builtin_amdgcn_alignbit(w0, w0, (32 - j) & 31);
+            load_region<W1 - 1, 1>(p, j, r1);
+        }
+        if constexpr (W2 > 0) load_region<W2, W1>(p, j, r2);
+        if constexpr (W3 > 0) load_region<W3, W1 + W2>(p, j, r3);
+    }
+
+    __device__ __forceinline__ void prepare(uint32_t bankbytes) {
+        uint32_t z;
+        if constexpr (W1 == 8) z = labels_from_bytes(r1);
+        else z = r0;
+        coset_bytes(trellis_coset_bits(z), bankbytes, hb);
+    }
+
+    // LDS byte address of stage S (0..2) at chunk t
+    template <int S>
+    __device__ __forceinline__ uint32_t addr(int t) const {
+        const int e = t & 3;
+        const uint32_t hq = hb[t >> 2];
+        if constexpr (S == 0) {
+            if constexpr (W1 == 8) return __builtin_amdgcn_perm(r1[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else {
+                const uint32_t f = field_of<W1 - 1>(r1, t) | (__builtin_amdgcn_ubfe(r0, t, 1) << (W1 - 1));
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
+            }
+        } else if constexpr (S == 1) {
+            if constexpr (W2 == 8) return __builtin_amdgcn_perm(r2[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else return __builtin_amdgcn_perm(field_of<W2>(r2, t), hq, 0x0c0c0400u | e);
+        } else {
+            return __builtin_amdgcn_perm(r3[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+        }
+    }
+};
+
+__device__ __forceinline__ int sext8(uint32_t w, int e) { return (int)(int8_t)(w >> (8 * e)); }
+
+}  // namespace p8x

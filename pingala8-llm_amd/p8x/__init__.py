@@ -1,0 +1,361 @@
+"""ctypes harness for libp8x (the MI355X Pingala-8 hot path) and a minimal HIP runtime binding.
+
+No torch: device memory, streams and events come straight from libamdhip64. The product library must be
+built (`make -C pingala8-llm_amd/csrc`); loading fails loudly when it is missing.
+"""
+import ctypes
+import ctypes.util
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libp8x.so")
+
+P8X_OK, P8X_ERR_ARG, P8X_ERR_FORMAT, P8X_ERR_HIP, P8X_ERR_UNSUPPORTED, P8X_ERR_NOMEM = range(6)
+F32, F16, BF16, I16 = 0, 1, 2, 3
+ACT_Q8_128, ACT_Q8_1 = 0, 1
+MAX_COLS = 8
+
+EXPORTS = [
+    "p8x_version", "p8x_error_string", "p8x_last_error", "p8x_need", "p8x_probe", "p8x_prepare", "p8x_release",
+    "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
+    "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_synth_random",
+    "p8x_quantize_tensor", "p8x_slot_bytes",
+]
+
+
+class P8xError(RuntimeError):
+    pass
+
+
+class Info(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int), ("K", ctypes.c_int), ("nd", ctypes.c_int), ("ng", ctypes.c_int), ("nb", ctypes.c_int),
+                ("n", ctypes.c_size_t), ("kbytes", ctypes.c_size_t), ("stream_bytes", ctypes.c_size_t),
+                ("class_tiles", ctypes.c_size_t * 8), ("dev_base", ctypes.c_void_p)]
+
+
+_lib = None
+
+
+def lib():
+    """libp8x.so with argtypes set; raises when the build is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise P8xError(f"libp8x.so not built: {LIB_PATH} (run make -C pingala8-llm_amd/csrc)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i, sz, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_uint64
+    L.p8x_version.restype = ctypes.c_char_p
+    L.p8x_error_string.restype = ctypes.c_char_p
+    L.p8x_error_string.argtypes = [i]
+    L.p8x_last_error.restype = ctypes.c_char_p
+    L.p8x_need.argtypes = [sz, i, i, i]; L.p8x_need.restype = sz
+    L.p8x_probe.argtypes = [vp, sz, i, i]
+    L.p8x_prepare.argtypes = [vp, sz, i, i, i, ctypes.POINTER(vp)]
+    L.p8x_release.argtypes = [vp]; L.p8x_release.restype = None
+    L.p8x_tensor_info.argtypes = [vp, ctypes.POINTER(Info)]
+    L.p8x_dequantize.argtypes = [vp, i, vp, sz, vp]
+    L.p8x_decode_rotated.argtypes = [vp, i, vp, sz, vp]
+    L.p8x_quantize_q8_128.argtypes = [vp, vp, i, sz, vp, vp, vp, vp]
+    L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
+    L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, vp]
+    L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
+    L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
+    L.p8x_mul_mat.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
+    L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
+    L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
+    L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
+    _lib = L
+    return L
+
+
+def check(rc, what=""):
+    if rc != P8X_OK:
+        L = lib()
+        raise P8xError(f"{what}: {L.p8x_error_string(rc).decode()} ({L.p8x_last_error().decode()})")
+
+
+# --------------------------------------------------------------------------------------------------- HIP runtime
+_hip = None
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        path = None
+        for cand in ("/opt/rocm/lib/libamdhip64.so", ctypes.util.find_library("amdhip64")):
+            if cand and (os.path.exists(cand) or not cand.startswith("/")):
+                path = cand
+                break
+        H = ctypes.CDLL(path)
+        vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        H.hipMalloc.argtypes = [ctypes.POINTER(vp), sz]
+        H.hipFree.argtypes = [vp]
+        H.hipMemcpy.argtypes = [vp, vp, sz, i]
+        H.hipMemset.argtypes = [vp, i, sz]
+        H.hipDeviceSynchronize.argtypes = []
+        H.hipGetErrorString.restype = ctypes.c_char_p
+        H.hipGetErrorString.argtypes = [i]
+        H.hipStreamCreate.argtypes = [ctypes.POINTER(vp)]
+        H.hipStreamDestroy.argtypes = [vp]
+        H.hipStreamSynchronize.argtypes = [vp]
+        H.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        H.hipEventDestroy.argtypes = [vp]
+        H.hipEventRecord.argtypes = [vp, vp]
+        H.hipEventSynchronize.argtypes = [vp]
+        H.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        H.hipGetDeviceCount.argtypes = [ctypes.POINTER(i)]
+        H.hipStreamBeginCapture.argtypes = [vp, i]
+        H.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        H.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, sz]
+        H.hipGraphLaunch.argtypes = [vp, vp]
+        H.hipGraphExecDestroy.argtypes = [vp]
+        H.hipGraphDestroy.argtypes = [vp]
+        _hip = H
+    return _hip
+
+
+def hip_check(rc, what=""):
+    if rc != 0:
+        raise P8xError(f"{what}: HIP error {rc} {hip().hipGetErrorString(rc).decode()}")
+
+
+def device_count():
+    n = ctypes.c_int(0)
+    try:
+        if hip().hipGetDeviceCount(ctypes.byref(n)) != 0:
+            return 0
+    except OSError:
+        return 0
+    return n.value
+
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+class DeviceBuffer:
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = ctypes.c_void_p()
+        hip_check(hip().hipMalloc(ctypes.byref(self.ptr), max(self.nbytes, 16)), "hipMalloc")
+
+    @classmethod
+    def from_numpy(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        if a.nbytes:
+            hip_check(hip().hipMemcpy(b.ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes, H2D), "hipMemcpy H2D")
+        return b
+
+    def to_numpy(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        if out.nbytes:
+            hip_check(hip().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), self.ptr, out.nbytes, D2H), "hipMemcpy D2H")
+        return out
+
+    def fill(self, byte):
+        hip_check(hip().hipMemset(self.ptr, byte, self.nbytes), "hipMemset")
+
+    @property
+    def addr(self):
+        return self.ptr.value
+
+    def free(self):
+        if self.ptr:
+            hip().hipFree(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize():
+    hip_check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Stream:
+    def __init__(self):
+        self.h = ctypes.c_void_p()
+        hip_check(hip().hipStreamCreate(ctypes.byref(self.h)), "hipStreamCreate")
+
+    def sync(self):
+        hip_check(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
+
+
+class Event:
+    def __init__(self):
+        self.h = ctypes.c_void_p()
+        hip_check(hip().hipEventCreate(ctypes.byref(self.h)), "hipEventCreate")
+
+    def record(self, stream=None):
+        hip_check(hip().hipEventRecord(self.h, stream.h if stream else None), "hipEventRecord")
+
+    def elapsed_ms(self, later):
+        ms = ctypes.c_float(0)
+        hip_check(hip().hipEventSynchronize(later.h), "hipEventSynchronize")
+        hip_check(hip().hipEventElapsedTime(ctypes.byref(ms), self.h, later.h), "hipEventElapsedTime")
+        return ms.value
+
+
+# --------------------------------------------------------------------------------------------------- host producers
+CLASS_P_C3 = (0, 0, 0, 1, 0, 0, 0, 0)
+
+
+def synth_random(seed, rows, K, class_p=CLASS_P_C3, codebook=0, nd=0, permute=True):
+    """random valid slot bytes (numpy uint8)"""
+    L = lib()
+    cp = (ctypes.c_double * 8)(*class_p)
+    n = ctypes.c_size_t(0)
+    L.p8x_synth_random(seed, rows, K, cp, codebook, nd, int(permute), None, 0, ctypes.byref(n))
+    buf = np.empty(n.value, np.uint8)
+    check(L.p8x_synth_random(seed, rows, K, cp, codebook, nd, int(permute), buf.ctypes.data, buf.size, ctypes.byref(n)), "synth_random")
+    return buf
+
+
+def quantize_tensor(W, c16=None, sign_seed=0):
+    """class-3 slot bytes from f32 weights [rows][K] (plain-MSE Viterbi)"""
+    L = lib()
+    W = np.ascontiguousarray(W, np.float32)
+    rows, K = W.shape
+    c = None if c16 is None else np.ascontiguousarray(c16, np.uint16)
+    cptr = None if c is None else c.ctypes.data
+    n = ctypes.c_size_t(0)
+    L.p8x_quantize_tensor(W.ctypes.data, rows, K, cptr, sign_seed, None, 0, ctypes.byref(n))
+    buf = np.empty(n.value + 64, np.uint8)
+    check(L.p8x_quantize_tensor(W.ctypes.data, rows, K, cptr, sign_seed, buf.ctypes.data, buf.size, ctypes.byref(n)), "quantize_tensor")
+    return buf[:n.value].copy()
+
+
+# --------------------------------------------------------------------------------------------------- tensors
+def _vp(x):
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    if isinstance(x, int):
+        return ctypes.c_void_p(x)
+    return x
+
+
+class Tensor:
+    """A prepared tensor slot (device-resident)."""
+
+    def __init__(self, slot, rows, K, device_slot=None):
+        L = lib()
+        self.rows, self.K = rows, K
+        self.h = ctypes.c_void_p()
+        if device_slot is not None:
+            check(L.p8x_prepare(device_slot.ptr, device_slot.nbytes, rows, K, 1, ctypes.byref(self.h)), "p8x_prepare")
+            self._keep = device_slot
+        else:
+            slot = np.ascontiguousarray(slot, np.uint8)
+            check(L.p8x_prepare(slot.ctypes.data, slot.size, rows, K, 0, ctypes.byref(self.h)), "p8x_prepare")
+        inf = Info()
+        check(L.p8x_tensor_info(self.h, ctypes.byref(inf)), "p8x_tensor_info")
+        self.info = inf
+        self.nsl = K // 128
+
+    @property
+    def stream_bytes(self):
+        return self.info.stream_bytes
+
+    def release(self):
+        if self.h:
+            lib().p8x_release(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    # ---- device-pointer entry points
+    def dequantize_dev(self, dtype, out, ld=None, stream=None):
+        check(lib().p8x_dequantize(self.h, dtype, _vp(out), ld or self.K, stream.h if stream else None), "p8x_dequantize")
+
+    def decode_rotated_dev(self, dtype, out, ld=None, stream=None):
+        check(lib().p8x_decode_rotated(self.h, dtype, _vp(out), ld or self.K, stream.h if stream else None), "p8x_decode_rotated")
+
+    def mul_mat_vec_dev(self, x, y, ncols=1, ldx=None, ldy=None, act=ACT_Q8_128, stream=None):
+        check(lib().p8x_mul_mat_vec_act(self.h, act, _vp(x), ncols, ldx or self.K, _vp(y), ldy or self.rows,
+                                        stream.h if stream else None), "p8x_mul_mat_vec")
+
+    def mul_mat_dev(self, x, x_dtype, N, y, ldx=None, ldy=None, stream=None):
+        check(lib().p8x_mul_mat(self.h, _vp(x), x_dtype, N, ldx or self.K, _vp(y), ldy or self.rows,
+                                stream.h if stream else None), "p8x_mul_mat")
+
+    # ---- numpy conveniences (copy in / out, synchronous)
+    def dequantize(self, dtype=F32):
+        npdt = {F32: np.float32, F16: np.uint16, BF16: np.uint16}[dtype]
+        out = DeviceBuffer(self.rows * self.K * np.dtype(npdt).itemsize)
+        self.dequantize_dev(dtype, out)
+        synchronize()
+        return out.to_numpy(npdt, (self.rows, self.K))
+
+    def decode_rotated(self, dtype=I16):
+        npdt = {I16: np.int16, F32: np.float32}[dtype]
+        out = DeviceBuffer(self.rows * self.K * np.dtype(npdt).itemsize)
+        self.decode_rotated_dev(dtype, out)
+        synchronize()
+        return out.to_numpy(npdt, (self.rows, self.K))
+
+    def quantize_q8_128(self, x):
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        ncols = x.shape[0]
+        xd = DeviceBuffer.from_numpy(x)
+        q = DeviceBuffer(ncols * self.K); d = DeviceBuffer(4 * ncols * self.nsl); s = DeviceBuffer(4 * ncols * self.nsl)
+        check(lib().p8x_quantize_q8_128(self.h, xd.ptr, ncols, self.K, q.ptr, d.ptr, s.ptr, None), "p8x_quantize_q8_128")
+        synchronize()
+        return (q.to_numpy(np.int8, (ncols, self.K)), d.to_numpy(np.float32, (ncols, self.nsl)),
+                s.to_numpy(np.int32, (ncols, self.nsl)))
+
+    def quantize_q8_1(self, x):
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        ncols = x.shape[0]
+        xd = DeviceBuffer.from_numpy(x)
+        blk = DeviceBuffer(ncols * 36 * (self.K // 32))
+        check(lib().p8x_quantize_q8_1(self.h, xd.ptr, ncols, self.K, blk.ptr, None), "p8x_quantize_q8_1")
+        synchronize()
+        return blk.to_numpy(np.uint8, (ncols, 36 * (self.K // 32)))
+
+    def vec_dot(self, act, q, d=None, partials=False):
+        """y (no delta) and optionally the integer partials, from host-quantized activations"""
+        q = np.ascontiguousarray(q)
+        ncols = q.shape[0]
+        qd = DeviceBuffer.from_numpy(q)
+        dd = DeviceBuffer.from_numpy(np.ascontiguousarray(d, np.float32)) if d is not None else None
+        y = DeviceBuffer(4 * ncols * self.rows)
+        nblk = self.nsl if act == ACT_Q8_128 else self.K // 32
+        p = DeviceBuffer(4 * ncols * self.rows * nblk) if partials else None
+        check(lib().p8x_vec_dot(self.h, act, qd.ptr, dd.ptr if dd else None, ncols, y.ptr, self.rows,
+                                p.ptr if p else None, None), "p8x_vec_dot")
+        synchronize()
+        yo = y.to_numpy(np.float32, (ncols, self.rows))
+        if partials:
+            return yo, p.to_numpy(np.int32, (ncols, self.rows, nblk))
+        return yo
+
+    def mul_mat_vec(self, x, act=ACT_Q8_128):
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        ncols = x.shape[0]
+        xd = DeviceBuffer.from_numpy(x)
+        y = DeviceBuffer(4 * ncols * self.rows)
+        self.mul_mat_vec_dev(xd, y, ncols=ncols, act=act)
+        synchronize()
+        return y.to_numpy(np.float32, (ncols, self.rows))
+
+    def mul_mat(self, X, dtype=F32):
+        X = np.ascontiguousarray(X)
+        N = X.shape[0]
+        xd = DeviceBuffer.from_numpy(X)
+        y = DeviceBuffer(4 * N * self.rows)
+        self.mul_mat_dev(xd, dtype, N, y)
+        synchronize()
+        return y.to_numpy(np.float32, (N, self.rows))
