@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark: batch-1 fused decode + GEMV over the Llama-3.1-8B-shaped Pingala-8 linear stack on one MI355X.
+
+Workload (one step): 32 layers x (q 4096x4096, k 1024x4096, v 1024x4096, o 4096x4096, gate 14336x4096,
+up 14336x4096, down 4096x14336) + lm_head 128256x4096 as 4 row-shards of 32064 rows (the format keeps
+rows < 32768). Every linear runs the reference's GEMV path: activation prep (x' = FWHT(x sg / c) / 16,
+8-bit per 128 columns) then the fused decode + GEMV kernel with un-permute and clamp delta. Random-valid
+class-3 weights (the reference's timing arm) on synthetic N(0, 1) activations, all resident in HBM before
+the timed region. value = packed weight stream bytes (M + S + D) per step x steps / wall time.
+
+roofline: the fused GEMV kernel, algorithmic bytes = the packed stream of each launch, durations from HIP
+events bracketing every GEMV launch on the stream it runs on. cpu_baseline: the reference's own CPU core
+(oracle/_ref, built from its patch) running its two-phase GEMV driver on a bounded sample (one layer).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "pingala8-llm_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+
+import p8x  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+LLAMA_LAYER = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096), ("attn_output", 4096, 4096),
+               ("ffn_gate", 14336, 4096), ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
+HEAD_SHARDS = [("lm_head", 32064, 4096)] * 4
+CLASS_C3 = (0, 0, 0, 1, 0, 0, 0, 0)
+# B4 class mix per tensor kind (logs/cs_lfull_transcode.log): attn_v class 6, ffn_down 78.1% c3 / 12.5% c4 / 9.4% c2
+CLASS_B4 = {"attn_v": (0, 0, 0, 0, 0, 0, 1, 0), "ffn_down": (0, 0, 0.094, 0.781, 0.125, 0, 0, 0)}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_stack(layers, mix, keep_host_layer0):
+    tensors, kinds, host0 = [], [], []
+    seed = 1
+    plan = [(f"blk.{l}.{k}", r, K) for l in range(layers) for (k, r, K) in LLAMA_LAYER] + \
+           [(f"output.{i}", r, K) for i, (_, r, K) in enumerate(HEAD_SHARDS)]
+    for name, rows, K in plan:
+        kind = name.split(".")[-1] if name.startswith("blk") else "lm_head"
+        cp = CLASS_B4.get(kind, CLASS_C3) if mix == "b4" else CLASS_C3
+        slot = p8x.synth_random(seed, rows, K, class_p=cp, nd=1)
+        seed += 1
+        tensors.append(p8x.Tensor(slot, rows, K))
+        kinds.append(kind)
+        if keep_host_layer0 and name.startswith("blk.0."):
+            host0.append((slot, rows, K))
+    return tensors, kinds, host0
+
+
+def cpu_baseline(host0, seconds, threads):
+    import oracle as O
+    variant = O.best_ref_variant()
+    if not O.ref_available(variant):
+        return None
+    core = O.RefCore(variant)
+    pool = O.RefPool(core, threads)
+    refs = [core.open(s, r, K) for (s, r, K) in host0]
+    rng = np.random.default_rng(7)
+    xs = [rng.standard_normal(K).astype(np.float32) for (_, _, K) in host0]
+    ys = [np.zeros(r, np.float32) for (_, r, _) in host0]
+    nbytes = 0
+    for (s, r, K) in host0:
+        nt = (r // 32) * (K // 256)
+        kb = int(np.frombuffer(s[-32:].tobytes(), np.uint32)[2])
+        nbytes += kb - ((2064 + 68 * nt + 15) & ~15) + 68 * nt   # payload + S + M
+    pool.gemv_seq(refs, xs, ys, planes=1)   # warm
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        pool.gemv_seq(refs, xs, ys, planes=1)
+        n += 1
+    dt = time.perf_counter() - t0
+    pool.close()
+    for r in refs:
+        r.close()
+    return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"layer 0 of the stack (7 linears, {nbytes / 1e6:.1f} MB packed), {n} passes in {dt:.1f} s, "
+                      f"q8 activations, reference core vr-native-cpu-core.h built {core.isa}"}
+
+
+def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
+    q = p8x.DeviceBuffer(max(t.K for t in tensors))
+    d = p8x.DeviceBuffer(4 * (max(t.K for t in tensors) // 128))
+
+    def step_linear(events=None):
+        for i, t in enumerate(tensors):
+            t.quantize_q8_128_dev(xs[t.K], q, d, stream=stream)
+            if events is not None:
+                events[2 * i].record(stream)
+            t.vec_dot_dev(p8x.ACT_Q8_128, q, d, ybufs[i], x=xs[t.K], stream=stream)
+            if events is not None:
+                events[2 * i + 1].record(stream)
+
+    step_linear()
+    stream.sync()
+    evs = [[p8x.Event() for _ in range(2 * len(tensors))] for _ in range(pl_steps)]
+    p8x.synchronize()
+    e0, e1 = p8x.Event(), p8x.Event()
+    e0.record(stream)
+    for s_ in range(pl_steps):
+        step_linear(evs[s_])
+    e1.record(stream)
+    stream.sync()
+    pl_ms = e0.elapsed_ms(e1) / pl_steps
+    kern_ms = np.zeros(len(tensors))
+    for s_ in range(pl_steps):
+        for i in range(len(tensors)):
+            kern_ms[i] += evs[s_][2 * i].elapsed_ms(evs[s_][2 * i + 1])
+    kern_ms /= pl_steps
+    bytes_per = np.array([t.stream_bytes for t in tensors], np.float64)
+    per_kind = {}
+    for k in dict.fromkeys(kinds):
+        idx = [i for i, kk in enumerate(kinds) if kk == k]
+        per_kind[k] = {"GB/s": round(bytes_per[idx].sum() / (kern_ms[idx].sum() * 1e-3) / 1e9, 1),
+                       "us_per_launch": round(float(kern_ms[idx].mean() * 1e3), 2),
+                       "MB_per_launch": round(float(bytes_per[idx].mean() / 1e6), 3)}
+    log("per-linear launches, per kind:", json.dumps(per_kind))
+    per_linear = {"GB/s": round(step_bytes / (pl_ms * 1e-3) / 1e9, 1), "ms_per_step": round(pl_ms, 4),
+                  "launches_per_step": 2 * len(tensors), "per_kind": per_kind}
+    return per_linear
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--mix", choices=("c3", "b4"), default="c3")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by rows across GPUs, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    if p8x.device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+
+    t_build = time.perf_counter()
+    tensors, kinds, host0 = build_stack(args.layers, args.mix, not args.no_cpu)
+    log(f"built {len(tensors)} tensors in {time.perf_counter() - t_build:.1f} s")
+    step_bytes = sum(t.stream_bytes for t in tensors)
+    rng = np.random.default_rng(0)
+    xs = {K: p8x.DeviceBuffer.from_numpy(rng.standard_normal(K).astype(np.float32)) for K in sorted({t.K for t in tensors})}
+    ybufs = [p8x.DeviceBuffer(4 * t.rows) for t in tensors]
+    stream = p8x.Stream()
+
+    # ---- streaming: one grouped launch (activation prep + fused decode-GEMV) over every linear per step
+    batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ybufs)
+    for _ in range(args.warmup):
+        batch.run(stream)
+    stream.sync()
+    ev = [(p8x.Event(), p8x.Event()) for _ in range(args.steps)]
+    e0, e1 = p8x.Event(), p8x.Event()
+    p8x.synchronize()
+    e0.record(stream)
+    t0 = time.perf_counter()
+    for s_ in range(args.steps):
+        batch.run_stage(0, stream)
+        ev[s_][0].record(stream)
+        batch.run_stage(1, stream)
+        ev[s_][1].record(stream)
+    e1.record(stream)
+    stream.sync()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_ms(e1) / args.steps
+    gemv_ms = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
+    log(f"stream: {ms_per_step * 1e3:.1f} us/step, GEMV kernel {gemv_ms * 1e3:.1f} us -> {achieved:.0f} GB/s")
+
+    # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
+    per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
+    cpu = None
+    if not args.no_cpu and host0:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        cpu = cpu_baseline(host0, args.cpu_seconds, threads)
+    out = {
+        "metric": "bs=1 dequant-GEMV HBM GB/s (% of peak), Llama-3.1-8B linear shapes",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (random-valid class-3 codes, N(0,1) activations)",
+        "config": {"workload": "llama3.1-8b linear stack, batch 1: 32 x (q,k,v,o,gate,up,down) + lm_head as 4 x 32064 rows, "
+                               "streamed by one grouped launch per step",
+                   "layers": args.layers, "class_mix": args.mix, "linears": len(tensors), "launches_per_step": 2,
+                   "stream_bytes_per_step": int(step_bytes), "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+                   "activations": "q8 per 128 columns (k_vr_qx_real semantics)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv<1,Q8_128,class 3> (fused decode + GEMV, grouped launch)", "launches": args.steps,
+                     "bytes_per_launch": int(step_bytes)},
+        "cpu_baseline": cpu,
+        "per_linear_launches": per_linear,
+        "host_wall_s": round(wall, 3),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

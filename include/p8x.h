@@ -97,10 +97,10 @@ int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx
 /* ---- products --------------------------------------------------------------------------------------- */
 /* vec_dot against pre-quantized activations (vrc_tile, CPU.patch:617-668): act = P8X_ACT_Q8_128 (q, d from
  * p8x_quantize_q8_128, `d` required) or P8X_ACT_Q8_1 (q = block_q8_1 array, d ignored). Writes y [ncols][ldy]
- * in ORIGINAL rows WITHOUT the clamp delta (it needs the unquantized x). partials (optional, sorted rows):
- * int32 [ncols][rows][K/128] for Q8_128 or [ncols][rows][K/32] for Q8_1, the exact integer dot of each row
- * with each quantization block. */
-int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols,
+ * in ORIGINAL rows. The clamp delta needs the unquantized activations: it is added when x ([ncols][ldx] f32)
+ * is given and skipped when x is NULL. partials (optional, sorted rows): int32 [ncols][rows][K/128] for
+ * Q8_128 or [ncols][rows][K/32] for Q8_1, the exact integer dot of each row with each quantization block. */
+int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, void *stream);
 /* y = W x for 1..8 columns (vr_mul_mat_vec, CPU.patch:4466-4521): activation prep + fused decode-GEMV +
  * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. */
@@ -109,6 +109,20 @@ int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols,
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T with X in
  * P8X_F32 or P8X_BF16. Weight tiles are decoded to fp16 in LDS and fed to MFMA with fp32 accumulation. */
 int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream);
+
+/* ---- grouped GEMV ------------------------------------------------------------------------------------- */
+/* No counterpart in the reference (ggml issues one mul_mat per graph node). A fixed list of independent
+ * GEMVs y_i = W_i x_i (8-bit-per-128 activations, the same ncols 1..8 for all) run as one batched
+ * activation-prep launch plus one fused decode + GEMV launch, so the packed weights of many linears stream
+ * through a single persistent grid (e.g. q/k/v, or gate/up, of a layer). All tensors must share the codebook
+ * and coset vector. x/y are device pointers fixed at creation; create allocates the batch's workspace. */
+typedef struct p8x_gemv_batch p8x_gemv_batch;
+int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                          float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out);
+int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
+/* the two launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV */
+int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream);
+void p8x_gemv_batch_release(p8x_gemv_batch *b);
 
 /* ---- host-side producers (not on the hot path) -------------------------------------------------------- */
 /* Random valid tensor slot (the reference's random-valid timing arm, CPU.patch:4391-4458). class_p[8] are

@@ -34,10 +34,11 @@ __device__ __forceinline__ void lane_ints(const uint32_t *tab, const uint32_t *_
     ls.prepare(bankbytes);
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
-        const uint32_t w0 = lds_word(tab, ls.template addr<0>(t));
+        const uint32_t hq = ls.group_bytes(t >> 2);
+        const uint32_t w0 = lds_word(tab, ls.template addr<0>(t, hq));
         uint32_t w1 = 0, w2 = 0;
-        if constexpr (NST > 1) w1 = lds_word(tab, ls.template addr<1>(t));
-        if constexpr (NST > 2) w2 = lds_word(tab, ls.template addr<2>(t));
+        if constexpr (NST > 1) w1 = lds_word(tab, ls.template addr<1>(t, hq));
+        if constexpr (NST > 2) w2 = lds_word(tab, ls.template addr<2>(t, hq));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             int x = sext8(w0, e) * (1 << SH1);

@@ -1,0 +1,293 @@
+// p8x_gemv.h -- fused decode + GEMV kernel templates (instantiated in p8x_gemv_q8.hip / p8x_gemv_q8b.hip /
+// p8x_gemv_q81.hip so the builds run in parallel).
+//
+// Persistent workgroups of 8 waves build the 64 KB replicated coset table once, then walk tasks
+// (job, octet of 8 row groups, K-chunk). Each wave owns one row group over the task's K-chunk: no
+// barrier or cross-wave reduction inside the main loop. Per tile, the wave decodes (p8x_lane.h) and takes
+// v_dot4 products of the looked-up int8x4 codewords (coset folded in) with the activation chunk, an LDS
+// broadcast because chunk order is the same in every lane. Per lane-slice: isum = sum_s dot_s << SH_s
+// (CPU.patch:646-662); y_row += float(isum) * d * S. The next tile's payload is in flight while the
+// current one is decoded. The two half-slices of a row meet through one cross-lane add; the K-chunks of a
+// row group through a fixed-order fix-up by the last-arriving wave, so results are deterministic (the
+// reference accumulates with float atomics, CPU.patch:4014).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "p8x_internal.h"
+#include "p8x_lane.h"
+
+namespace p8x {
+
+constexpr int kGemvWaves = 8;
+constexpr int kGemvThreads = 64 * kGemvWaves;
+
+// ------------------------------------------------------------------------------------------------ fused decode + GEMV
+// One GEMV of a launch. A launch walks a list of these (one entry for p8x_mul_mat_vec, many for a grouped
+// launch); tasks are numbered across the list: task = (job, octet of 8 row groups, K-chunk).
+struct GemvJob {
+    const uint32_t *M; const uint16_t *S; const uint32_t *D; const int16_t *prm;
+    const int *cp; const uint16_t *cc; const float *cv;
+    const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32]
+    const float *x; unsigned ldx;    // original activations for the clamp delta (nullptr: no delta)
+    float *y; unsigned ldy;
+    int32_t *partials;               // optional integer partials (sorted rows)
+    float *wpart; unsigned *wcnt;    // K-chunk partial rows [nks][ncol][rows] and arrival counters [ng]
+    int rows, K, nb, ng, nsl;
+    int kchunk, nks, task0, ntasks;
+};
+
+constexpr int kXBytes = 14336;   // LDS activation bytes per task: ncol x kchunk x 256
+
+__host__ __device__ constexpr int kchunk_max(int ncol) { return kXBytes / (256 * ncol); }
+
+template <int NCOL, int ACT>
+struct GemvSmem {
+    static constexpr int kScales = NCOL * (ACT == P8X_ACT_Q8_128 ? 2 : 8) * kchunk_max(NCOL);
+    uint32_t tab[kTabWords];   // first member: LDS address 0, so table addresses need no base add
+    uint32_t xq[kXBytes / 4];  // [ncol][kchunk * 256 bytes]
+    float xd[kScales];         // [ncol][scales of the chunk]
+};
+
+template <int NCOL, int ACT>
+struct TaskCtx {
+    GemvJob J;   // by value: fields live in SGPRs
+    int g, b0, nbl, hs, j;
+    uint32_t bankbytes;
+};
+
+template <int NCOL, int ACT, bool PARTIALS, int C>
+__device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, const RawSlice<C> &raw,
+                                          int b, float (&yacc)[NCOL]) {
+    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
+    constexpr int NSUB = ACT == P8X_ACT_Q8_128 ? 1 : 4;   // integer sums per lane-slice
+    constexpr int XW = kXBytes / 4 / NCOL;                 // LDS words per column
+    constexpr int NSC = GemvSmem<NCOL, ACT>::kScales / NCOL;
+    LaneSlice<C> ls;
+    ls.from_raw(raw, c.j);
+    ls.prepare(c.bankbytes);
+    const int bl = b - c.b0;
+    int acc[NST][NCOL][NSUB];
+#pragma unroll
+    for (int s = 0; s < NST; ++s)
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n)
+#pragma unroll
+            for (int u = 0; u < NSUB; ++u) acc[s][n][u] = 0;
+    const uint32_t *xbase = sm.xq + (bl * 256 + c.hs * 128) / 4;
+#pragma unroll
+    for (int t4 = 0; t4 < 8; ++t4) {
+        uint4 xv[NCOL];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) xv[n] = *reinterpret_cast<const uint4 *>(xbase + n * XW + 4 * t4);
+        const uint32_t hq = ls.group_bytes(t4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 4 * t4 + e;
+            const int u = NSUB == 1 ? 0 : (t >> 3);
+            uint32_t w[3];
+            w[0] = lds_word(sm.tab, ls.template addr<0>(t, hq));
+            if constexpr (NST > 1) w[1] = lds_word(sm.tab, ls.template addr<1>(t, hq));
+            if constexpr (NST > 2) w[2] = lds_word(sm.tab, ls.template addr<2>(t, hq));
+#pragma unroll
+            for (int n = 0; n < NCOL; ++n) {
+                const uint32_t xc = e == 0 ? xv[n].x : e == 1 ? xv[n].y : e == 2 ? xv[n].z : xv[n].w;
+#pragma unroll
+                for (int s = 0; s < NST; ++s) acc[s][n][u] = __builtin_amdgcn_sdot4((int)w[s], (int)xc, acc[s][n][u], false);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // bound the live ranges: one group of 4 chunks at a time
+    }
+    const float sc = half_to_float(raw.s);
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+            int isum = acc[0][n][u] * (1 << SH1);
+            if constexpr (NST > 1) isum += acc[1][n][u] * (1 << SH2);
+            if constexpr (NST > 2) isum += acc[2][n][u];
+            if constexpr (PARTIALS) {
+                const int r = 32 * c.g + c.j;
+                if constexpr (ACT == P8X_ACT_Q8_128) c.J.partials[((size_t)n * c.J.rows + r) * c.J.nsl + 2 * b + c.hs] = isum;
+                else c.J.partials[((size_t)n * c.J.rows + r) * (c.J.K / 32) + 8 * b + 4 * c.hs + u] = isum;
+            }
+            const float dsc = ACT == P8X_ACT_Q8_128 ? sm.xd[n * NSC + 2 * bl + c.hs] : sm.xd[n * NSC + 8 * bl + 4 * c.hs + u];
+            yacc[n] += ((float)isum * dsc) * sc;
+        }
+    }
+}
+
+// A run of consecutive tiles of class C in row group g: the next tile's words are in flight while the
+// current one is decoded (two register buffers, alternating). Returns the first block not consumed.
+template <int NCOL, int ACT, bool PARTIALS, int C>
+__device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, int b, int bend, float (&yacc)[NCOL]) {
+    constexpr int NW = nw_of(C);
+    const GemvJob &J = c.J;
+    const gptr<const uint32_t> mrow = as_global(J.M) + (size_t)c.g * J.nb;
+    const gptr<const uint32_t> D = as_global(J.D) + c.hs * NW * 32;
+    const gptr<const uint16_t> S = as_global(J.S) + 32 * c.g;
+    RawSlice<C> A, B;
+    A.load(D + (mrow[b] & 0x1FFFFFFFu), S + (size_t)b * J.rows, c.j);
+    for (;;) {
+        int bn = b + 1;
+        uint32_t mn = bn < bend ? mrow[bn] : 0u;
+        bool more = (mn >> 29) == (uint32_t)C;
+        if (more) B.load(D + (mn & 0x1FFFFFFFu), S + (size_t)bn * J.rows, c.j);
+        gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, A, b, yacc);
+        if (!more) return bn;
+        b = bn++;
+        mn = bn < bend ? mrow[bn] : 0u;
+        more = (mn >> 29) == (uint32_t)C;
+        if (more) A.load(D + (mn & 0x1FFFFFFFu), S + (size_t)bn * J.rows, c.j);
+        gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, B, b, yacc);
+        if (!more) return bn;
+        b = bn;
+    }
+}
+
+// waves per SIMD the register budget is sized for: 4 (<= 128 VGPRs) where the kernel fits without spills
+// (one column, class-3 tiles), else 2
+__host__ __device__ constexpr int gemv_waves_per_eu(int ncol, int cm) { return ncol == 1 && cm == (1 << 3) ? 4 : 2; }
+
+template <int NCOL, int ACT, bool PARTIALS, int CM>
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu(NCOL, CM), gemv_waves_per_eu(NCOL, CM))))
+void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_tasks, const uint32_t *__restrict__ a2) {
+    __shared__ GemvSmem<NCOL, ACT> sm;   // static: the table sits at LDS address 0 at compile time
+    constexpr int NSC = GemvSmem<NCOL, ACT>::kScales / NCOL;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    TaskCtx<NCOL, ACT> c;
+    c.hs = lane >> 5; c.j = lane & 31;
+    c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
+    build_coset_table(sm.tab, a2, tid, kGemvThreads);
+    int jc = 0;
+    for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
+        if (jobs) {
+            while (task >= jobs[jc].task0 + jobs[jc].ntasks) ++jc;
+            c.J = jobs[jc];
+        } else {
+            c.J = job0;
+        }
+        const GemvJob *J = &c.J;
+        const int local = task - J->task0, oct = local / J->nks, ks = local % J->nks;
+        c.b0 = ks * J->kchunk;
+        c.nbl = min(J->kchunk, J->nb - c.b0);
+        c.g = 8 * oct + w;
+        // stage this task's activations and scales
+        __syncthreads();
+        for (int i = tid; i < NCOL * c.nbl * 64; i += kGemvThreads) {
+            const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
+            uint32_t v;
+            if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J->q + (size_t)n * J->K + 256 * c.b0)[wi];
+            else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J->q + ((size_t)n * (J->K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
+            sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
+        }
+        {
+            constexpr int PER = ACT == P8X_ACT_Q8_128 ? 2 : 8;
+            for (int i = tid; i < NCOL * PER * c.nbl; i += kGemvThreads) {
+                const int n = i / (PER * c.nbl), si = i % (PER * c.nbl);
+                float v;
+                if constexpr (ACT == P8X_ACT_Q8_128) v = J->d[(size_t)n * J->nsl + 2 * c.b0 + si];
+                else v = half_to_float(*reinterpret_cast<const uint16_t *>((const uint8_t *)J->q + ((size_t)n * (J->K / 32) + 8 * c.b0 + si) * 36));
+                sm.xd[n * NSC + si] = v;
+            }
+        }
+        __syncthreads();
+        if (c.g >= J->ng) continue;
+        float yacc[NCOL];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
+        const int bend = c.b0 + c.nbl;
+        for (int b = c.b0; b < bend;) {
+            const uint32_t mt = J->M[(size_t)c.g * J->nb + b];
+            // CM: the tile classes this instantiation decodes (chosen from the tensor's class histogram)
+            switch (mt >> 29) {
+                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 1>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 2>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 3>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 4>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 5>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 6>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 7>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                default:
+                    if constexpr (PARTIALS) {   // class 0: zero weights
+                        const int r = 32 * c.g + c.j;
+                        for (int n = 0; n < NCOL; ++n) {
+                            if constexpr (ACT == P8X_ACT_Q8_128) J->partials[((size_t)n * J->rows + r) * J->nsl + 2 * b + c.hs] = 0;
+                            else for (int u = 0; u < 4; ++u) J->partials[((size_t)n * J->rows + r) * (J->K / 32) + 8 * b + 4 * c.hs + u] = 0;
+                        }
+                    }
+                    ++b;
+                    break;
+            }
+        }
+        // half-slice 1 joins half-slice 0; lanes 0..31 hold the 32 rows
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) yacc[n] += __shfl_xor(yacc[n], 32);
+        bool final_rows = J->nks == 1;
+        if (J->nks > 1) {
+            // K-chunk fix-up, no agent-scope fences (on gfx950 those write back and invalidate the XCD's whole L2):
+            // partial rows are agent-coherent stores; the wave waits for them, then bumps the row group's arrival
+            // counter; the last arrival reads the partials with agent-coherent loads and sums them in chunk order.
+            if (lane < 32)
+#pragma unroll
+                for (int n = 0; n < NCOL; ++n)
+                    __hip_atomic_store(&J->wpart[((size_t)ks * NCOL + n) * J->rows + 32 * c.g + c.j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            unsigned old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(&J->wcnt[c.g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __builtin_amdgcn_readfirstlane(old);
+            final_rows = old == (unsigned)(J->nks - 1);
+            if (final_rows) {
+                if (lane < 32)
+#pragma unroll
+                    for (int n = 0; n < NCOL; ++n) {
+                        // issue 8 partial loads at a time (one memory round trip per 8 chunks), sum in chunk order
+                        float sacc = 0.f;
+                        for (int k0 = 0; k0 < J->nks; k0 += 8) {
+                            float pv[8];
+#pragma unroll
+                            for (int i = 0; i < 8; ++i)
+                                pv[i] = k0 + i < J->nks ? __hip_atomic_load(&J->wpart[((size_t)(k0 + i) * NCOL + n) * J->rows + 32 * c.g + c.j],
+                                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+                            for (int i = 0; i < 8; ++i)
+                                if (k0 + i < J->nks) sacc += pv[i];
+                        }
+                        yacc[n] = sacc;
+                    }
+                if (lane == 0) __hip_atomic_store(&J->wcnt[c.g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (final_rows && lane < 32) {
+            const int ro = J->prm[32 * c.g + c.j];
+#pragma unroll
+            for (int n = 0; n < NCOL; ++n) {
+                float v = yacc[n];
+                if (J->x) {
+                    const float *xr = J->x + (size_t)n * J->ldx;
+                    for (int e = J->cp[ro]; e < J->cp[ro + 1]; ++e) v += J->cv[e] * xr[J->cc[e]];
+                }
+                J->y[(size_t)n * J->ldy + ro] = v;
+            }
+        }
+    }
+}
+
+
+// class sets with their own instantiations: class 3 only (the 2-bit bulk), class 6 only (4-bit attn_v),
+// classes 2-4 (mixed ffn_down), everything
+constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmAll = 0xFE;
+
+template <int NCOL, int ACT, bool PARTIALS, int CM>
+static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+    const int per_cu = gemv_waves_per_eu(NCOL, CM) >= 4 ? 2 : 1;   // 8-wave workgroups resident per CU
+    const int grid = std::min(tasks, per_cu * num_cus());
+    hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
+    return hip_check(hipGetLastError(), "k_gemv launch");
+}
+
+// defined in the instantiation units
+int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
+int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
+int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
+
+}  // namespace p8x

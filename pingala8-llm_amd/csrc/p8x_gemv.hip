@@ -15,13 +15,12 @@
 // accumulates with float atomics, CPU.patch:4014).
 #include <hip/hip_runtime.h>
 
-#include "p8x_internal.h"
-#include "p8x_lane.h"
+#include <cstring>
+#include <vector>
+
+#include "p8x_gemv.h"
 
 namespace p8x {
-
-constexpr int kGemvWaves = 8;
-constexpr int kGemvThreads = 64 * kGemvWaves;
 
 // ------------------------------------------------------------------------------------------------ activation prep
 // correctly rounded f32 quotient via f64 (53 >= 2*24 + 2 bits: no double-rounding error)
@@ -109,251 +108,207 @@ __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, si
     }
 }
 
-// ------------------------------------------------------------------------------------------------ fused decode + GEMV
-struct GemvArgs {
-    const uint32_t *M; const uint16_t *S; const uint32_t *D; const uint32_t *a2; const int16_t *prm;
-    const int *cp; const uint16_t *cc; const float *cv;
-    const int8_t *q;          // Q8_128: [ncol][K] int8
-    const float *d;           // Q8_128: [ncol][nsl]
-    const uint8_t *q81;       // Q8_1: [ncol][K/32] blocks
-    const float *x; size_t ldx;   // original activations for the clamp delta (nullptr: no delta)
-    float *y; size_t ldy;
-    int32_t *partials;        // optional integer partials (sorted rows)
-    float *wpart; unsigned *wcnt;
-    int rows, K, nb, ng, nsl, bpk, nks, items;
-};
-
-template <int NCOL, int ACT>
-struct GemvSmem {
-    static constexpr int kXBytes = NCOL * 8 * 256;   // activation bytes of one item (bpk <= 8)
-    static constexpr int kScales = ACT == P8X_ACT_Q8_128 ? 16 : 64;   // scales per column per item
-    uint32_t tab[kTabWords];
-    uint32_t xq[kXBytes / 4];
-    float xd[NCOL * kScales];
-    float red[kGemvWaves * NCOL * 32];
-};
-
-template <int NCOL, int ACT, bool PARTIALS, int C>
-__device__ __forceinline__ void gemv_tile(const GemvArgs &a, const GemvSmem<NCOL, ACT> &sm, const uint32_t *__restrict__ payload,
-                                          int lane, int bl, int b, int g, uint32_t bankbytes, float (&yacc)[NCOL]) {
-    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C), NW = nw_of(C);
-    const int hs = lane >> 5, j = lane & 31;
-    LaneSlice<C> ls;
-    ls.load(payload + hs * NW * 32, j);
-    const float sc = half_to_float(a.S[(size_t)b * a.rows + 32 * g + j]);
-    ls.prepare(bankbytes);
-    constexpr int NSUB = ACT == P8X_ACT_Q8_128 ? 1 : 4;   // integer sums per lane-slice
-    int acc[NST][NCOL][NSUB];
-#pragma unroll
-    for (int s = 0; s < NST; ++s)
-#pragma unroll
-        for (int n = 0; n < NCOL; ++n)
-#pragma unroll
-            for (int u = 0; u < NSUB; ++u) acc[s][n][u] = 0;
-    const uint32_t *xbase = sm.xq + (bl * 256 + hs * 128) / 4;
-#pragma unroll
-    for (int t4 = 0; t4 < 8; ++t4) {
-        uint4 xv[NCOL];
-#pragma unroll
-        for (int n = 0; n < NCOL; ++n) xv[n] = *reinterpret_cast<const uint4 *>(xbase + n * (GemvSmem<NCOL, ACT>::kXBytes / 4 / NCOL) + 4 * t4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 4 * t4 + e;
-            constexpr int dummy = 0; (void)dummy;
-            const int u = NSUB == 1 ? 0 : (t >> 3);
-            uint32_t w[3];
-            w[0] = lds_word(sm.tab, ls.template addr<0>(t));
-            if constexpr (NST > 1) w[1] = lds_word(sm.tab, ls.template addr<1>(t));
-            if constexpr (NST > 2) w[2] = lds_word(sm.tab, ls.template addr<2>(t));
-#pragma unroll
-            for (int n = 0; n < NCOL; ++n) {
-                const uint32_t xc = e == 0 ? xv[n].x : e == 1 ? xv[n].y : e == 2 ? xv[n].z : xv[n].w;
-#pragma unroll
-                for (int s = 0; s < NST; ++s) acc[s][n][u] = __builtin_amdgcn_sdot4((int)w[s], (int)xc, acc[s][n][u], false);
-            }
-        }
-    }
-#pragma unroll
-    for (int n = 0; n < NCOL; ++n) {
-#pragma unroll
-        for (int u = 0; u < NSUB; ++u) {
-            int isum = acc[0][n][u] * (1 << SH1);
-            if constexpr (NST > 1) isum += acc[1][n][u] * (1 << SH2);
-            if constexpr (NST > 2) isum += acc[2][n][u];
-            if constexpr (PARTIALS) {
-                const int r = 32 * g + j;
-                if constexpr (ACT == P8X_ACT_Q8_128) a.partials[((size_t)n * a.rows + r) * a.nsl + 2 * b + hs] = isum;
-                else a.partials[((size_t)n * a.rows + r) * (a.K / 32) + 8 * b + 4 * hs + u] = isum;
-            }
-            const float dsc = ACT == P8X_ACT_Q8_128 ? sm.xd[n * GemvSmem<NCOL, ACT>::kScales + 2 * bl + hs]
-                                                    : sm.xd[n * GemvSmem<NCOL, ACT>::kScales + 8 * bl + 4 * hs + u];
-            yacc[n] += ((float)isum * dsc) * sc;
-        }
-    }
-}
-
-template <int NCOL, int ACT, bool PARTIALS>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv(const GemvArgs a) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    auto &sm = *reinterpret_cast<GemvSmem<NCOL, ACT> *>(smem_raw);
-    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t bankbytes = (uint32_t)((lane & 31) << 2) * 0x01010101u;
-    build_coset_table(sm.tab, a.a2, tid, kGemvThreads);
-    for (int item = blockIdx.x; item < a.items; item += gridDim.x) {
-        const int g = item / a.nks, ks = item % a.nks;
-        const int b0 = ks * a.bpk, nbl = min(a.bpk, a.nb - b0);
-        // stage this item's activations (NCOL x nbl blocks of 256 bytes) and scales
-        __syncthreads();
-        constexpr int XW = GemvSmem<NCOL, ACT>::kXBytes / 4 / NCOL;   // words per column
-        if constexpr (ACT == P8X_ACT_Q8_128) {
-            for (int i = tid; i < NCOL * nbl * 64; i += kGemvThreads) {
-                const int n = i / (nbl * 64), wi = i % (nbl * 64);
-                sm.xq[n * XW + wi] = reinterpret_cast<const uint32_t *>(a.q + (size_t)n * a.K + 256 * b0)[wi];
-            }
-            for (int i = tid; i < NCOL * 2 * nbl; i += kGemvThreads) {
-                const int n = i / (2 * nbl), si = i % (2 * nbl);
-                sm.xd[n * GemvSmem<NCOL, ACT>::kScales + si] = a.d[(size_t)n * a.nsl + 2 * b0 + si];
-            }
-        } else {
-            const int nq = a.K / 32;
-            for (int i = tid; i < NCOL * nbl * 64; i += kGemvThreads) {
-                const int n = i / (nbl * 64), wi = i % (nbl * 64);   // word wi: block wi / 8, word wi % 8 of its 32 ints
-                const uint8_t *blk = a.q81 + ((size_t)n * nq + 8 * b0 + wi / 8) * 36;
-                sm.xq[n * XW + wi] = reinterpret_cast<const uint32_t *>(blk + 4)[wi % 8];
-            }
-            for (int i = tid; i < NCOL * 8 * nbl; i += kGemvThreads) {
-                const int n = i / (8 * nbl), si = i % (8 * nbl);
-                const uint8_t *blk = a.q81 + ((size_t)n * nq + 8 * b0 + si) * 36;
-                sm.xd[n * GemvSmem<NCOL, ACT>::kScales + si] = half_to_float(*reinterpret_cast<const uint16_t *>(blk));
-            }
-        }
-        __syncthreads();
-        float yacc[NCOL];
-#pragma unroll
-        for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
-        for (int bl = w; bl < nbl; bl += kGemvWaves) {
-            const int b = b0 + bl;
-            const uint32_t mt = a.M[(size_t)g * a.nb + b];
-            const uint32_t *payload = a.D + (mt & 0x1FFFFFFFu);
-            switch (mt >> 29) {
-                case 1: gemv_tile<NCOL, ACT, PARTIALS, 1>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 2: gemv_tile<NCOL, ACT, PARTIALS, 2>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 3: gemv_tile<NCOL, ACT, PARTIALS, 3>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 4: gemv_tile<NCOL, ACT, PARTIALS, 4>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 5: gemv_tile<NCOL, ACT, PARTIALS, 5>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 6: gemv_tile<NCOL, ACT, PARTIALS, 6>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                case 7: gemv_tile<NCOL, ACT, PARTIALS, 7>(a, sm, payload, lane, bl, b, g, bankbytes, yacc); break;
-                default:
-                    if constexpr (PARTIALS) {   // class 0: zero weights
-                        const int r = 32 * g + (lane & 31), hs = lane >> 5;
-                        for (int n = 0; n < NCOL; ++n) {
-                            if constexpr (ACT == P8X_ACT_Q8_128) a.partials[((size_t)n * a.rows + r) * a.nsl + 2 * b + hs] = 0;
-                            else for (int u = 0; u < 4; ++u) a.partials[((size_t)n * a.rows + r) * (a.K / 32) + 8 * b + 4 * hs + u] = 0;
-                        }
-                    }
-                    break;
-            }
-        }
-        // half-slice 1 joins half-slice 0, then the waves meet in LDS
-#pragma unroll
-        for (int n = 0; n < NCOL; ++n) {
-            const float o = __shfl_xor(yacc[n], 32);
-            if (lane < 32) sm.red[(w * NCOL + n) * 32 + lane] = yacc[n] + o;
-        }
-        __syncthreads();
-        float ysum = 0.f;
-        int n = 0, j = 0;
-        if (tid < 32 * NCOL) {
-            n = tid >> 5; j = tid & 31;
-            for (int ww = 0; ww < kGemvWaves; ++ww) ysum += sm.red[(ww * NCOL + n) * 32 + j];
-        }
-        bool final_rows = a.nks == 1;
-        if (a.nks > 1) {
-            if (tid < 32 * NCOL) a.wpart[((size_t)ks * NCOL + n) * a.rows + 32 * g + j] = ysum;
-            __threadfence();
-            __syncthreads();
-            __shared__ unsigned last;
-            if (tid == 0) last = atomicAdd(&a.wcnt[g], 1u) == (unsigned)(a.nks - 1);
-            __syncthreads();
-            final_rows = last != 0;
-            if (final_rows) {
-                __threadfence();
-                if (tid < 32 * NCOL) {
-                    ysum = 0.f;
-                    for (int k2 = 0; k2 < a.nks; ++k2)
-                        ysum += __hip_atomic_load(&a.wpart[((size_t)k2 * NCOL + n) * a.rows + 32 * g + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                if (tid == 0) a.wcnt[g] = 0u;
-            }
-        }
-        if (final_rows && tid < 32 * NCOL) {
-            const int ro = a.prm[32 * g + j];
-            if (a.x) {
-                const float *xr = a.x + (size_t)n * a.ldx;
-                for (int e = a.cp[ro]; e < a.cp[ro + 1]; ++e) ysum += a.cv[e] * xr[a.cc[e]];
-            }
-            a.y[(size_t)n * a.ldy + ro] = ysum;
-        }
-    }
-}
-
+// K-split of a single-GEMV launch: about one task per workgroup slot, at least two tiles per wave, chunks no
+// larger than the LDS activation buffer allows.
 GemvPlan gemv_plan(const p8x_tensor *t, int ncols) {
-    (void)ncols;
     GemvPlan p;
-    p.bpk = t->nb < 8 ? t->nb : 8;
+    const int octets = (t->ng + 7) / 8;
+    const int slots = 2 * num_cus();
+    int nks = (slots + octets - 1) / octets;
+    nks = std::min(nks, std::max(1, t->nb / 2));
+    nks = std::max(nks, (t->nb + kchunk_max(ncols) - 1) / kchunk_max(ncols));
+    nks = std::min(nks, t->nb);
+    p.bpk = (t->nb + nks - 1) / nks;
     p.nks = (t->nb + p.bpk - 1) / p.bpk;
-    p.items = t->ng * p.nks;
-    p.grid = p.items;
+    p.items = octets * p.nks;
+    p.grid = std::min(p.items, slots);
     return p;
 }
 
-template <int NCOL, int ACT, bool PARTIALS>
-static int launch_gemv_t(const GemvArgs &a, int items, hipStream_t st) {
-    const size_t smem = sizeof(GemvSmem<NCOL, ACT>);
-    auto kern = k_gemv<NCOL, ACT, PARTIALS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        int rc = hip_check(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem), "gemv smem attribute");
-        if (rc) return rc;
-        attr_set = true;
-    }
-    const int per_cu = smem <= 80 * 1024 ? 2 : 1;
-    const int grid = std::min(items, num_cus() * per_cu);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kGemvThreads), smem, st, a);
-    return hip_check(hipGetLastError(), "k_gemv launch");
+int class_set(const size_t hist[8]) {
+    int m = 0;
+    for (int c = 1; c < 8; ++c) if (hist[c]) m |= 1 << c;
+    for (int cm : {kCmC3, kCmC6, kCmC234})
+        if ((m & ~cm) == 0) return cm;
+    return kCmAll;
 }
 
-template <int ACT, bool PARTIALS>
-static int launch_gemv_cols(const GemvArgs &a, int ncols, int items, hipStream_t st) {
-    switch (ncols) {
-        case 1: return launch_gemv_t<1, ACT, PARTIALS>(a, items, st);
-        case 2: return launch_gemv_t<2, ACT, PARTIALS>(a, items, st);
-        case 3: return launch_gemv_t<3, ACT, PARTIALS>(a, items, st);
-        case 4: return launch_gemv_t<4, ACT, PARTIALS>(a, items, st);
-        case 5: return launch_gemv_t<5, ACT, PARTIALS>(a, items, st);
-        case 6: return launch_gemv_t<6, ACT, PARTIALS>(a, items, st);
-        case 7: return launch_gemv_t<7, ACT, PARTIALS>(a, items, st);
-        case 8: return launch_gemv_t<8, ACT, PARTIALS>(a, items, st);
-        default: return set_error(P8X_ERR_ARG, "gemv: ncols %d", ncols);
-    }
+static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
+                     float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int task0) {
+    g = GemvJob{};
+    g.M = t->M; g.S = t->S; g.D = t->D; g.prm = t->prm;
+    g.cp = t->cp; g.cc = t->cc; g.cv = t->cv;
+    g.q = q; g.d = d; g.x = x; g.ldx = (unsigned)ldx; g.y = y; g.ldy = (unsigned)ldy; g.partials = partials;
+    g.wpart = t->wpart; g.wcnt = t->wcnt;
+    g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl;
+    g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + 7) / 8) * nks;
 }
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st) {
-    GemvArgs a{};
-    a.M = t->M; a.S = t->S; a.D = t->D; a.a2 = t->a2; a.prm = t->prm;
-    a.cp = t->cp; a.cc = t->cc; a.cv = t->cv;
-    if (act == P8X_ACT_Q8_128) { a.q = (const int8_t *)q; a.d = d; }
-    else a.q81 = (const uint8_t *)q;
-    a.x = x; a.ldx = ldx; a.y = y; a.ldy = ldy; a.partials = partials;
-    a.wpart = t->wpart; a.wcnt = t->wcnt;
-    a.rows = t->rows; a.K = t->K; a.nb = t->nb; a.ng = t->ng; a.nsl = t->nsl;
-    a.bpk = t->gemv_bpk; a.nks = t->gemv_nks; a.items = t->ng * t->gemv_nks;
-    if (act == P8X_ACT_Q8_128) {
-        return partials ? launch_gemv_cols<P8X_ACT_Q8_128, true>(a, ncols, a.items, st) : launch_gemv_cols<P8X_ACT_Q8_128, false>(a, ncols, a.items, st);
+    const GemvPlan p = gemv_plan(t, ncols);
+    if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
+    GemvJob job0;
+    fill_job(job0, t, q, d, x, ldx, y, ldy, partials, p.nks, p.bpk, 0);
+    const int cm = class_set(t->class_tiles);
+    if (partials) {   // integer partials: one column per launch
+        for (int n = 0; n < ncols; ++n) {
+            GemvJob jn = job0;
+            const size_t qcol = act == P8X_ACT_Q8_128 ? (size_t)t->K : (size_t)36 * (t->K / 32);
+            jn.q = (const uint8_t *)q + n * qcol;
+            if (d) jn.d = d + (size_t)n * t->nsl;
+            if (x) jn.x = x + (size_t)n * ldx;
+            jn.y = y + (size_t)n * ldy;
+            jn.partials = partials + (size_t)n * t->rows * (act == P8X_ACT_Q8_128 ? t->nsl : t->K / 32);
+            const GemvPlan p1 = gemv_plan(t, 1);
+            jn.nks = p1.nks; jn.kchunk = p1.bpk; jn.ntasks = ((t->ng + 7) / 8) * p1.nks;
+            const int rc = launch_gemv_partials(act, jn, t->a2, st);
+            if (rc) return rc;
+        }
+        return P8X_OK;
     }
-    return partials ? launch_gemv_cols<P8X_ACT_Q8_1, true>(a, ncols, a.items, st) : launch_gemv_cols<P8X_ACT_Q8_1, false>(a, ncols, a.items, st);
+    if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, nullptr, job0, 1, job0.ntasks, t->a2, st);
+    return launch_gemv_q81(ncols, nullptr, job0, 1, job0.ntasks, t->a2, st);
 }
+
+// ------------------------------------------------------------------------------------------------ grouped launches
+struct ActJob {
+    const float *x; unsigned ldx; const float *ic; int K;
+    int8_t *q; float *d;   // [ncols][K], [ncols][K / 128]
+    int blk0;              // first 256-block of this job in the launch
+};
+
+// grid (total blocks, ncols), block 64: the k_act_q8_128 body for a list of jobs
+__global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restrict__ jobs, int njobs) {
+    const int gb = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    int lo = 0, hi = njobs - 1;   // last job with blk0 <= gb
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].blk0 <= gb) lo = mid; else hi = mid - 1;
+    }
+    const ActJob J = jobs[lo];
+    const int b = gb - J.blk0;
+    float v[4];
+    rotate_block_lane(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane, v);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = half_wave_max(am);
+    const float dd = div_rn(am, 127.f);
+    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
+    int qi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qi[e] = __float2int_rn(v[e] * id);
+    const uint32_t packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+    reinterpret_cast<uint32_t *>(J.q + (size_t)n * J.K + 256 * b)[lane] = packed;
+    if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
+}
+
+}  // namespace p8x
+
+struct p8x_gemv_batch {
+    int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
+    const uint32_t *a2 = nullptr;
+    p8x::GemvJob *d_jobs = nullptr;
+    p8x::ActJob *d_act = nullptr;
+    void *work = nullptr;   // activations, partial rows and counters of every job
+};
+
+using namespace p8x;
+
+extern "C" {
+
+void p8x_gemv_batch_release(p8x_gemv_batch *b) {
+    if (!b) return;
+    if (b->d_jobs) (void)hipFree(b->d_jobs);
+    if (b->d_act) (void)hipFree(b->d_act);
+    if (b->work) (void)hipFree(b->work);
+    delete b;
+}
+
+int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                          float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out) {
+    if (!tensors || !x || !ldx || !y || !ldy || !out || njobs < 1) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: bad arguments");
+    if (ncols < 1 || ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: ncols %d", ncols);
+    *out = nullptr;
+    size_t hist[8] = {0};
+    for (int i = 0; i < njobs; ++i) {
+        const p8x_tensor *t = tensors[i];
+        if (!t || !x[i] || !y[i]) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: job %d has a null pointer", i);
+        if (ldx[i] < (size_t)t->K || ldx[i] % 4 || ((uintptr_t)x[i] & 15) || ldy[i] < (size_t)t->rows)
+            return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: job %d strides/alignment", i);
+        if (memcmp(t->a2_host, tensors[0]->a2_host, sizeof t->a2_host))
+            return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: job %d has a different codebook", i);
+        for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
+    }
+    // workspace layout per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows] | counters [ng]
+    std::vector<GemvJob> jobs(njobs);
+    std::vector<ActJob> act(njobs);
+    std::vector<size_t> off_q(njobs), off_d(njobs), off_p(njobs), off_c(njobs);
+    size_t bytes = 0;
+    auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
+    int task0 = 0, blk0 = 0;
+    for (int i = 0; i < njobs; ++i) {
+        const p8x_tensor *t = tensors[i];
+        const int kc = std::min(t->nb, kchunk_max(ncols));
+        const int nks = (t->nb + kc - 1) / kc;
+        off_q[i] = take((size_t)ncols * t->K);
+        off_d[i] = take(4 * (size_t)ncols * t->nsl);
+        off_p[i] = nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
+        off_c[i] = nks > 1 ? take(4 * (size_t)t->ng) : 0;
+        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, task0);
+        task0 += jobs[i].ntasks;
+        act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
+        blk0 += t->nb;
+    }
+    p8x_gemv_batch *b = new p8x_gemv_batch();
+    b->njobs = njobs; b->ncols = ncols; b->cm = class_set(hist); b->total_tasks = task0; b->total_blocks = blk0;
+    b->a2 = tensors[0]->a2;
+    int rc;
+    if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||
+        hipMalloc((void **)&b->d_act, sizeof(ActJob) * njobs) != hipSuccess) {
+        p8x_gemv_batch_release(b);
+        return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: hipMalloc");
+    }
+    uint8_t *w = (uint8_t *)b->work;
+    for (int i = 0; i < njobs; ++i) {
+        jobs[i].q = w + off_q[i];
+        jobs[i].d = (const float *)(w + off_d[i]);
+        act[i].q = (int8_t *)(w + off_q[i]);
+        act[i].d = (float *)(w + off_d[i]);
+        if (jobs[i].nks > 1) { jobs[i].wpart = (float *)(w + off_p[i]); jobs[i].wcnt = (unsigned *)(w + off_c[i]); }
+        else { jobs[i].wpart = nullptr; jobs[i].wcnt = nullptr; }
+    }
+    if ((rc = hip_check(hipMemset(b->work, 0, bytes), "p8x_gemv_batch_create: clear")) ||
+        (rc = hip_check(hipMemcpy(b->d_jobs, jobs.data(), sizeof(GemvJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: jobs")) ||
+        (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs"))) {
+        p8x_gemv_batch_release(b);
+        return rc;
+    }
+    *out = b;
+    return P8X_OK;
+}
+
+int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
+    if (!b) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run: null batch");
+    hipStream_t st = (hipStream_t)stream;
+    if (stage == 0) {
+        hipLaunchKernelGGL(k_act_q8_128_batch, dim3(b->total_blocks, b->ncols), dim3(64), 0, st, (const ActJob *)b->d_act, b->njobs);
+        return hip_check(hipGetLastError(), "k_act_q8_128_batch launch");
+    }
+    if (stage == 1) {
+        GemvJob none{};
+        return launch_gemv_q8(b->ncols, b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->a2, st);
+    }
+    return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
+}
+
+int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream) {
+    int rc = p8x_gemv_batch_run_stage(b, 0, stream);
+    return rc ? rc : p8x_gemv_batch_run_stage(b, 1, stream);
+}
+
+}  // extern "C"
+
+namespace p8x {
 
 int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st) {
     hipLaunchKernelGGL(k_act_q8_128, dim3(t->nb, ncols), dim3(64), 0, st, x, ldx, (const float *)t->ic, t->K, q, d, sum);

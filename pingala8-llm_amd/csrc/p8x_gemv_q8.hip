@@ -1,0 +1,23 @@
+// p8x_gemv_q8.hip -- GEMV instantiations, 8-bit-per-128 activations, 1..4 columns
+#include "p8x_gemv.h"
+
+namespace p8x {
+
+template <int NCOL>
+static int q8_cm(int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+    if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(jobs, job0, njobs, tasks, a2, st);
+    if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(jobs, job0, njobs, tasks, a2, st);
+    if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(jobs, job0, njobs, tasks, a2, st);
+    return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
+}
+
+int launch_gemv_q8_lo(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+    switch (ncols) {
+        case 1: return q8_cm<1>(cm, jobs, job0, njobs, tasks, a2, st);
+        case 2: return q8_cm<2>(cm, jobs, job0, njobs, tasks, a2, st);
+        case 3: return q8_cm<3>(cm, jobs, job0, njobs, tasks, a2, st);
+        default: return q8_cm<4>(cm, jobs, job0, njobs, tasks, a2, st);
+    }
+}
+
+}  // namespace p8x

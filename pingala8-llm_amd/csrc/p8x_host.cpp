@@ -188,6 +188,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
     t->wrap_free = wrap_free;
+    memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
     auto fail = [&](int code) { p8x_release(t); return code; };
     auto alloc = [&](void **p, size_t bytes, const char *what) -> int {
@@ -205,8 +206,10 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->S = (const uint16_t *)(t->base + offset_S(nt));
     t->D = (const uint32_t *)(t->base + offset_D(nt));
     t->prm = (const int16_t *)(t->base + off[2]);
-    const GemvPlan plan = gemv_plan(t, 1);
-    t->gemv_bpk = plan.bpk; t->gemv_nks = plan.nks;
+    for (int nc = 1; nc <= P8X_MAX_COLS; ++nc) {   // partial rows of the largest single-GEMV plan
+        const GemvPlan plan = gemv_plan(t, nc);
+        if (plan.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)plan.nks * nc * rows);
+    }
     if ((rc = alloc((void **)&t->a2, 512 * 4, "tables"))) return fail(rc);
     if ((rc = alloc((void **)&t->ic, 4 * (size_t)K, "ic"))) return fail(rc);
     if ((rc = alloc((void **)&t->cp, 4 * (size_t)(rows + 1), "delta rows"))) return fail(rc);
@@ -216,7 +219,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wd, 4 * (size_t)P8X_MAX_COLS * nsl, "d"))) return fail(rc);
     if ((rc = alloc((void **)&t->wsum, 4 * (size_t)P8X_MAX_COLS * nsl, "sum"))) return fail(rc);
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
-    if ((rc = alloc((void **)&t->wpart, 4 * (size_t)t->gemv_nks * P8X_MAX_COLS * rows, "partials"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->a2, a2.data(), 512 * 4, hipMemcpyHostToDevice), "p8x_prepare: tables"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->ic, ic.data(), 4 * (size_t)K, hipMemcpyHostToDevice), "p8x_prepare: ic"))) return fail(rc);
@@ -269,12 +272,14 @@ int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx
     return launch_act_q8_1(t, x, ncols, ldx, blocks, (hipStream_t)stream);
 }
 
-int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, float *y, size_t ldy, int32_t *partials, void *stream) {
+int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
+                float *y, size_t ldy, int32_t *partials, void *stream) {
     if (!t || !q || !y) return set_error(P8X_ERR_ARG, "p8x_vec_dot: null pointer");
     if (act != P8X_ACT_Q8_128 && act != P8X_ACT_Q8_1) return set_error(P8X_ERR_ARG, "p8x_vec_dot: act %d", act);
     if (act == P8X_ACT_Q8_128 && !d) return set_error(P8X_ERR_ARG, "p8x_vec_dot: Q8_128 needs d");
     if (ncols < 1 || ncols > P8X_MAX_COLS || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_vec_dot: ncols %d ldy %zu", ncols, ldy);
-    return launch_gemv(t, act, q, d, ncols, nullptr, 0, y, ldy, partials, (hipStream_t)stream);
+    if (x && ldx < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_vec_dot: ldx %zu < K %d", ldx, t->K);
+    return launch_gemv(t, act, q, d, ncols, x, ldx, y, ldy, partials, (hipStream_t)stream);
 }
 
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream) {

@@ -32,12 +32,13 @@ struct p8x_tensor {
     float *wd = nullptr;             // [P8X_MAX_COLS][nsl]
     int32_t *wsum = nullptr;         // [P8X_MAX_COLS][nsl]
     uint8_t *wq81 = nullptr;         // block_q8_1 [P8X_MAX_COLS][K / 32]
-    float *wpart = nullptr;          // split-K partial rows [nks][P8X_MAX_COLS][rows]
+    float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan
+    size_t wpart_floats = 0;
     unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
     uint16_t *wx16 = nullptr;        // rotated fp16 activations for the prompt GEMM (grown on demand)
     size_t wx16_elems = 0;
-    int gemv_bpk = 8, gemv_nks = 1;  // GEMV work split: blocks per item, items per row group
     bool wrap_free = true;           // |A + c| <= 127 bytewise
+    uint32_t a2_host[512];           // host copy of a2 (batches check that tensors share the tables)
 };
 
 namespace p8x {

@@ -34,6 +34,13 @@ __device__ __forceinline__ void build_coset_table(uint32_t *tab, const uint32_t 
     }
 }
 
+// global address-space views: pointers read out of descriptors are generic; these make loads global_load
+// with an SGPR base and a 32-bit lane offset instead of FLAT loads with 64-bit per-lane addresses
+template <typename T>
+using gptr = __attribute__((address_space(1))) T *;
+template <typename T>
+__device__ __forceinline__ gptr<const T> as_global(const T *p) { return (gptr<const T>)p; }
+
 __device__ __forceinline__ uint32_t lds_word(const uint32_t *tab, uint32_t byte_addr) {
     return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(tab) + byte_addr);
 }
@@ -86,14 +93,48 @@ __device__ __forceinline__ uint32_t labels_from_bytes(const uint32_t (&R)[8]) {
     return (n[0] >> 7) | (n[1] << 1) | (n[2] << 9) | (n[3] << 17);
 }
 
-// per-lane address bytes for 4 chunks: byte e = (h_{4q+e} << 7) | (bank << 2)
-__device__ __forceinline__ void coset_bytes(uint32_t H, uint32_t bankbytes, uint32_t (&hb)[8]) {
+// per-lane address bytes for chunks 4q .. 4q+3: byte e = (h_{4q+e} << 7) | (bank << 2). The nibble is first
+// placed at bits 7..10 so that one 24-bit multiply by 1 + 2^7 + 2^14 + 2^21 moves bit i to bit 8i + 7.
+__device__ __forceinline__ uint32_t coset_bytes(uint32_t H, uint32_t bankbytes, int q) {
+    const uint32_t nib7 = (4 * q >= 7 ? H >> (4 * q - 7) : H << (7 - 4 * q)) & 0x780u;
+    return (__umul24(nib7, 0x00204081u) & 0x80808080u) | bankbytes;
+}
+
+// Raw payload words of one lane-slice of class C, loaded in rotated order (before the v_alignbit step),
+// plus the lane's fp16 row scale. Kept separate from the decode so a wave can hold the next tile's words
+// in flight while it decodes the current one.
+template <int C>
+struct RawSlice {
+    static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
+    uint32_t w[NW];
+    uint16_t s;
+
+    template <int W, int WB, int O>
+    __device__ __forceinline__ void load_region_raw(gptr<const uint32_t> p, int j) {
+        const int wr = ((((32 - j) & 31) * W) >> 5);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const uint32_t nib = __builtin_amdgcn_ubfe(H, 4 * q, 4);
-        const uint32_t spread = (nib * 0x00204081u) & 0x01010101u;
-        hb[q] = (spread << 7) | bankbytes;
+        for (int m = 0; m < W; ++m) w[O + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
     }
+
+    // p = half-slice base, srow = &S[b * rows + 32 g] (scale of lane j at srow[j])
+    __device__ __forceinline__ void load(gptr<const uint32_t> p, gptr<const uint16_t> srow, int j) {
+        if constexpr (W1 == 8) {
+            load_region_raw<8, 0, 0>(p, j);
+        } else {
+            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
+            load_region_raw<W1 - 1, 1, 1>(p, j);
+        }
+        if constexpr (W2 > 0) load_region_raw<W2, W1, W1>(p, j);
+        if constexpr (W3 > 0) load_region_raw<W3, W1 + W2, W1 + W2>(p, j);
+        s = __builtin_nontemporal_load(srow + j);
+    }
+};
+
+template <int W, int O, int NWT>
+__device__ __forceinline__ void rotate_region(const uint32_t (&w)[NWT], int j, uint32_t (&R)[W]) {
+    const int br = (((32 - j) & 31) * W) & 31;
+#pragma unroll
+    for (int i = 0; i < W; ++i) R[i] = __builtin_amdgcn_alignbit(w[O + (i + 1) % W], w[O + i], br);
 }
 
 // Decoded state of one lane-slice of class C.
@@ -106,7 +147,8 @@ struct LaneSlice {
     uint32_t r1[NR1];
     uint32_t r2[NR2];
     uint32_t r3[NR3];
-    uint32_t hb[8];
+    uint32_t H;            // coset bits, chunk order
+    uint32_t bankbytes;
 
     // p = half-slice base (tile payload + hs * NW * 32), j = lane row
     __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j) {
@@ -121,18 +163,33 @@ struct LaneSlice {
         if constexpr (W3 > 0) load_region<W3, W1 + W2>(p, j, r3);
     }
 
-    __device__ __forceinline__ void prepare(uint32_t bankbytes) {
+    // same state from words already in registers
+    __device__ __forceinline__ void from_raw(const RawSlice<C> &raw, int j) {
+        if constexpr (W1 == 8) {
+            rotate_region<8, 0>(raw.w, j, r1);
+        } else {
+            r0 = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
+            rotate_region<W1 - 1, 1>(raw.w, j, r1);
+        }
+        if constexpr (W2 > 0) rotate_region<W2, W1>(raw.w, j, r2);
+        if constexpr (W3 > 0) rotate_region<W3, W1 + W2>(raw.w, j, r3);
+    }
+
+    __device__ __forceinline__ void prepare(uint32_t bb) {
         uint32_t z;
         if constexpr (W1 == 8) z = labels_from_bytes(r1);
         else z = r0;
-        coset_bytes(trellis_coset_bits(z), bankbytes, hb);
+        H = trellis_coset_bits(z);
+        bankbytes = bb;
     }
 
-    // LDS byte address of stage S (0..2) at chunk t
+    // address bytes of chunks 4q .. 4q+3 (computed once per group, passed to addr)
+    __device__ __forceinline__ uint32_t group_bytes(int q) const { return coset_bytes(H, bankbytes, q); }
+
+    // LDS byte address of stage S (0..2) at chunk t, hq = group_bytes(t >> 2)
     template <int S>
-    __device__ __forceinline__ uint32_t addr(int t) const {
+    __device__ __forceinline__ uint32_t addr(int t, uint32_t hq) const {
         const int e = t & 3;
-        const uint32_t hq = hb[t >> 2];
         if constexpr (S == 0) {
             if constexpr (W1 == 8) return __builtin_amdgcn_perm(r1[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
             else {

@@ -21,7 +21,8 @@ EXPORTS = [
     "p8x_version", "p8x_error_string", "p8x_last_error", "p8x_need", "p8x_probe", "p8x_prepare", "p8x_release",
     "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
     "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_synth_random",
-    "p8x_quantize_tensor", "p8x_slot_bytes",
+    "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
+    "p8x_gemv_batch_release",
 ]
 
 
@@ -60,13 +61,17 @@ def lib():
     L.p8x_decode_rotated.argtypes = [vp, i, vp, sz, vp]
     L.p8x_quantize_q8_128.argtypes = [vp, vp, i, sz, vp, vp, vp, vp]
     L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
-    L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, vp]
+    L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
     L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
     L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
     L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
+    L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
+    L.p8x_gemv_batch_run.argtypes = [vp, vp]
+    L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
+    L.p8x_gemv_batch_release.argtypes = [vp]; L.p8x_gemv_batch_release.restype = None
     _lib = L
     return L
 
@@ -287,6 +292,14 @@ class Tensor:
         check(lib().p8x_mul_mat_vec_act(self.h, act, _vp(x), ncols, ldx or self.K, _vp(y), ldy or self.rows,
                                         stream.h if stream else None), "p8x_mul_mat_vec")
 
+    def quantize_q8_128_dev(self, x, q, d, ncols=1, ldx=None, stream=None):
+        check(lib().p8x_quantize_q8_128(self.h, _vp(x), ncols, ldx or self.K, _vp(q), _vp(d), None,
+                                        stream.h if stream else None), "p8x_quantize_q8_128")
+
+    def vec_dot_dev(self, act, q, d, y, ncols=1, x=None, ldx=None, ldy=None, stream=None):
+        check(lib().p8x_vec_dot(self.h, act, _vp(q), _vp(d), ncols, _vp(x), ldx or self.K, _vp(y), ldy or self.rows,
+                                None, stream.h if stream else None), "p8x_vec_dot")
+
     def mul_mat_dev(self, x, x_dtype, N, y, ldx=None, ldy=None, stream=None):
         check(lib().p8x_mul_mat(self.h, _vp(x), x_dtype, N, ldx or self.K, _vp(y), ldy or self.rows,
                                 stream.h if stream else None), "p8x_mul_mat")
@@ -334,7 +347,7 @@ class Tensor:
         y = DeviceBuffer(4 * ncols * self.rows)
         nblk = self.nsl if act == ACT_Q8_128 else self.K // 32
         p = DeviceBuffer(4 * ncols * self.rows * nblk) if partials else None
-        check(lib().p8x_vec_dot(self.h, act, qd.ptr, dd.ptr if dd else None, ncols, y.ptr, self.rows,
+        check(lib().p8x_vec_dot(self.h, act, qd.ptr, dd.ptr if dd else None, ncols, None, 0, y.ptr, self.rows,
                                 p.ptr if p else None, None), "p8x_vec_dot")
         synchronize()
         yo = y.to_numpy(np.float32, (ncols, self.rows))
@@ -359,3 +372,35 @@ class Tensor:
         self.mul_mat_dev(xd, dtype, N, y)
         synchronize()
         return y.to_numpy(np.float32, (N, self.rows))
+
+
+class GemvBatch:
+    """A grouped launch of independent GEMVs (device buffers x_i, y_i fixed at creation)."""
+
+    def __init__(self, tensors, xs, ys, ncols=1):
+        n = len(tensors)
+        T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
+        X = (ctypes.c_void_p * n)(*[x.addr for x in xs])
+        Y = (ctypes.c_void_p * n)(*[y.addr for y in ys])
+        LX = (ctypes.c_size_t * n)(*[t.K for t in tensors])
+        LY = (ctypes.c_size_t * n)(*[t.rows for t in tensors])
+        self.h = ctypes.c_void_p()
+        check(lib().p8x_gemv_batch_create(T, X, LX, Y, LY, n, ncols, ctypes.byref(self.h)), "p8x_gemv_batch_create")
+        self._keep = (tensors, xs, ys)
+
+    def run(self, stream=None):
+        check(lib().p8x_gemv_batch_run(self.h, stream.h if stream else None), "p8x_gemv_batch_run")
+
+    def run_stage(self, stage, stream=None):
+        check(lib().p8x_gemv_batch_run_stage(self.h, stage, stream.h if stream else None), "p8x_gemv_batch_run_stage")
+
+    def release(self):
+        if self.h:
+            lib().p8x_gemv_batch_release(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass

@@ -180,3 +180,28 @@ def test_prepare_rejects_bad_slots():
     dev = p8x.DeviceBuffer.from_numpy(buf)
     t = p8x.Tensor(None, 64, 512, device_slot=dev)
     assert np.array_equal(t.decode_rotated(p8x.I16), O.Oracle(buf, 64, 512).decode_all())
+
+
+@pytest.mark.parametrize("ncols", [1, 3, 8])
+def test_batch_matches_single(ncols):
+    """one grouped launch over mixed shapes and class mixes == fp64 oracle per job"""
+    shapes = [(1024, 4096, (0, 0, 0, 1, 0, 0, 0, 0)), (512, 14336, (0, 0, 1, 8, 1, 0, 0, 0)),
+              (2048, 2560, (0, 0, 0, 0, 0, 0, 1, 0)), (96, 768, (1, 1, 1, 1, 1, 1, 1, 1))]
+    rng = np.random.default_rng(40 + ncols)
+    tensors, orcs, xs, ys, hx = [], [], [], [], []
+    for i, (rows, K, cp) in enumerate(shapes):
+        slot = p8x.synth_random(77 + i, rows, K, class_p=cp, nd=3)
+        tensors.append(p8x.Tensor(slot, rows, K))
+        orcs.append(O.Oracle(slot, rows, K))
+        X = rng.standard_normal((ncols, K)).astype(np.float32)
+        hx.append(X)
+        xs.append(p8x.DeviceBuffer.from_numpy(X))
+        ys.append(p8x.DeviceBuffer(4 * ncols * rows))
+    batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols)
+    for rep in range(2):
+        batch.run()
+        p8x.synchronize()
+        for i, (rows, K, _) in enumerate(shapes):
+            Y = ys[i].to_numpy(np.float32, (ncols, rows))
+            for n in range(ncols):
+                assert rel_l2(Y[n], orcs[i].gemv_f64(hx[i][n])) < 1e-5, (i, n, rep)
