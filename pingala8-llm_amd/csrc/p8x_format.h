@@ -35,8 +35,11 @@ P8X_HD constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
 P8X_HD constexpr size_t offset_S(size_t nt) { return kHeaderBytes + 4 * nt; }
 P8X_HD constexpr size_t offset_D(size_t nt) { return align16(kHeaderBytes + 68 * nt); }
 
-// fp16 bits -> f32 (exact)
+// fp16 bits -> f32 (exact; on the GPU the v_cvt_f32_f16 instruction, also exact for subnormals)
 P8X_HD float half_to_float(uint16_t h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return (float)__builtin_bit_cast(_Float16, h);
+#endif
     const uint32_t sign = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 31u, man = h & 1023u;
     uint32_t bits;
     if (ex == 0) {

@@ -18,6 +18,10 @@
 
 namespace p8x {
 
+#ifndef GEMV_NBUF_C3
+#define GEMV_NBUF_C3 3
+#endif
+
 constexpr int kGemvWaves = 8;
 constexpr int kGemvThreads = 64 * kGemvWaves;
 
@@ -34,6 +38,7 @@ struct GemvJob {
     float *wpart; unsigned *wcnt;    // K-chunk partial rows [nks][ncol][rows] and arrival counters [ng]
     int rows, K, nb, ng, nsl;
     int kchunk, nks, task0, ntasks;
+    unsigned dbytes;                 // payload region bytes (D .. end of the slot's payload)
 };
 
 constexpr int kXBytes = 14336;   // LDS activation bytes per task: ncol x kchunk x 256
@@ -50,7 +55,7 @@ struct GemvSmem {
 
 template <int NCOL, int ACT>
 struct TaskCtx {
-    GemvJob J;   // by value: fields live in SGPRs
+    const GemvJob *J;   // the descriptor in place (kernel argument or the launch's job array): never copied
     int g, b0, nbl, hs, j;
     uint32_t bankbytes;
 };
@@ -95,7 +100,7 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
                 for (int s = 0; s < NST; ++s) acc[s][n][u] = __builtin_amdgcn_sdot4((int)w[s], (int)xc, acc[s][n][u], false);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);   // bound the live ranges: one group of 4 chunks at a time
+        __asm__ volatile("" ::: "memory");   // one group of 4 chunks at a time: bounds the live registers
     }
     const float sc = half_to_float(raw.s);
 #pragma unroll
@@ -107,8 +112,8 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
             if constexpr (NST > 2) isum += acc[2][n][u];
             if constexpr (PARTIALS) {
                 const int r = 32 * c.g + c.j;
-                if constexpr (ACT == P8X_ACT_Q8_128) c.J.partials[((size_t)n * c.J.rows + r) * c.J.nsl + 2 * b + c.hs] = isum;
-                else c.J.partials[((size_t)n * c.J.rows + r) * (c.J.K / 32) + 8 * b + 4 * c.hs + u] = isum;
+                if constexpr (ACT == P8X_ACT_Q8_128) c.J->partials[((size_t)n * c.J->rows + r) * c.J->nsl + 2 * b + c.hs] = isum;
+                else c.J->partials[((size_t)n * c.J->rows + r) * (c.J->K / 32) + 8 * b + 4 * c.hs + u] = isum;
             }
             const float dsc = ACT == P8X_ACT_Q8_128 ? sm.xd[n * NSC + 2 * bl + c.hs] : sm.xd[n * NSC + 8 * bl + 4 * c.hs + u];
             yacc[n] += ((float)isum * dsc) * sc;
@@ -116,39 +121,66 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
     }
 }
 
-// A run of consecutive tiles of class C in row group g: the next tile's words are in flight while the
-// current one is decoded (two register buffers, alternating). Returns the first block not consumed.
-template <int NCOL, int ACT, bool PARTIALS, int C>
+// A run of consecutive tiles of class C in row group g: the run's extent is found from the tile words
+// first, then NBUF register buffers rotate so that NBUF - 1 following tiles are in flight while the current
+// one is decoded. Every step issues its prefetch (past the run's end through an empty resource, which reads
+// zeros without memory traffic), so the loop body is straight-line and the wait counts stay exact.
+// Returns the first block after the run.
+template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C>
 __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, int b, int bend, float (&yacc)[NCOL]) {
     constexpr int NW = nw_of(C);
-    const GemvJob &J = c.J;
-    const gptr<const uint32_t> mrow = as_global(J.M) + (size_t)c.g * J.nb;
-    const gptr<const uint32_t> D = as_global(J.D) + c.hs * NW * 32;
-    const gptr<const uint16_t> S = as_global(J.S) + 32 * c.g;
-    RawSlice<C> A, B;
-    A.load(D + (mrow[b] & 0x1FFFFFFFu), S + (size_t)b * J.rows, c.j);
-    for (;;) {
-        int bn = b + 1;
-        uint32_t mn = bn < bend ? mrow[bn] : 0u;
-        bool more = (mn >> 29) == (uint32_t)C;
-        if (more) B.load(D + (mn & 0x1FFFFFFFu), S + (size_t)bn * J.rows, c.j);
-        gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, A, b, yacc);
-        if (!more) return bn;
-        b = bn++;
-        mn = bn < bend ? mrow[bn] : 0u;
-        more = (mn >> 29) == (uint32_t)C;
-        if (more) A.load(D + (mn & 0x1FFFFFFFu), S + (size_t)bn * J.rows, c.j);
-        gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, B, b, yacc);
-        if (!more) return bn;
-        b = bn;
+    const GemvJob &J = *c.J;
+    const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)c.g * J.nb;   // tile words: scalar loads
+    auto tile_word = [&](int bb) { return mrow[bb]; };
+    int e = bend;   // ONLY_C: every tile of the tensor has class C
+    if constexpr (!ONLY_C) {
+        e = b + 1;
+        while (e < bend && (tile_word(e) >> 29) == (uint32_t)C) ++e;
     }
+    const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(J.D, J.dbytes), rs = buffer_rsrc(J.S, (uint32_t)J.nb * J.rows * 2u);
+    const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(J.D, 0u);
+    uint32_t vo[NW];
+    RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
+    const uint32_t vs = 2u * (uint32_t)c.j;
+    // wn = tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
+    uint32_t wn = tile_word(b);
+    auto issue = [&](RawSlice<C> &r, int ta) {
+        const bool ok = ta < e;
+        const int tc = ok ? ta : b;
+        const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
+        const uint32_t soff = ((uint32_t)tc * (uint32_t)J.rows + 32u * (uint32_t)c.g) * 2u;
+        r.load(ok ? rd : r0, toff, vo, ok ? rs : r0, soff, vs);
+        wn = tile_word(min(ta + 1, e - 1));
+    };
+    RawSlice<C> buf[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
+    // whole groups of NBUF tiles: the loop body is straight-line, so the same loads are in flight at every
+    // back edge
+    int base = b;
+    for (; base + NBUF <= e; base += NBUF) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            issue(buf[(i + NBUF - 1) % NBUF], base + i + NBUF - 1);
+            gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, buf[i], base + i, yacc);
+        }
+    }
+    // the last e - base < NBUF tiles are already in flight in buf[0 ..]
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i)
+        if (base + i < e) gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, buf[i], base + i, yacc);
+    return e;
 }
+
+// prefetch depth (register buffers) per variant
+__host__ __device__ constexpr int gemv_nbuf(int ncol, int c) { return ncol == 1 && c == 3 ? GEMV_NBUF_C3 : 2; }
 
 // waves per SIMD the register budget is sized for: 4 (<= 128 VGPRs) where the kernel fits without spills
 // (one column, class-3 tiles), else 2
 __host__ __device__ constexpr int gemv_waves_per_eu(int ncol, int cm) { return ncol == 1 && cm == (1 << 3) ? 4 : 2; }
 
-template <int NCOL, int ACT, bool PARTIALS, int CM>
+// MULTI: the launch walks a job array in global memory (grouped launch); else its one job is the kernel argument
+template <int NCOL, int ACT, bool PARTIALS, int CM, bool MULTI>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu(NCOL, CM), gemv_waves_per_eu(NCOL, CM))))
 void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_tasks, const uint32_t *__restrict__ a2) {
     __shared__ GemvSmem<NCOL, ACT> sm;   // static: the table sits at LDS address 0 at compile time
@@ -160,24 +192,21 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
     build_coset_table(sm.tab, a2, tid, kGemvThreads);
     int jc = 0;
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
-        if (jobs) {
+        if constexpr (MULTI)
             while (task >= jobs[jc].task0 + jobs[jc].ntasks) ++jc;
-            c.J = jobs[jc];
-        } else {
-            c.J = job0;
-        }
-        const GemvJob *J = &c.J;
-        const int local = task - J->task0, oct = local / J->nks, ks = local % J->nks;
-        c.b0 = ks * J->kchunk;
-        c.nbl = min(J->kchunk, J->nb - c.b0);
+        const GemvJob &J = MULTI ? jobs[jc] : job0;
+        c.J = &J;
+        const int local = task - J.task0, oct = local / J.nks, ks = local % J.nks;
+        c.b0 = ks * J.kchunk;
+        c.nbl = min(J.kchunk, J.nb - c.b0);
         c.g = 8 * oct + w;
         // stage this task's activations and scales
         __syncthreads();
         for (int i = tid; i < NCOL * c.nbl * 64; i += kGemvThreads) {
             const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
             uint32_t v;
-            if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J->q + (size_t)n * J->K + 256 * c.b0)[wi];
-            else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J->q + ((size_t)n * (J->K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
+            if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[wi];
+            else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
             sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
         }
         {
@@ -185,34 +214,34 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
             for (int i = tid; i < NCOL * PER * c.nbl; i += kGemvThreads) {
                 const int n = i / (PER * c.nbl), si = i % (PER * c.nbl);
                 float v;
-                if constexpr (ACT == P8X_ACT_Q8_128) v = J->d[(size_t)n * J->nsl + 2 * c.b0 + si];
-                else v = half_to_float(*reinterpret_cast<const uint16_t *>((const uint8_t *)J->q + ((size_t)n * (J->K / 32) + 8 * c.b0 + si) * 36));
+                if constexpr (ACT == P8X_ACT_Q8_128) v = J.d[(size_t)n * J.nsl + 2 * c.b0 + si];
+                else v = half_to_float(*reinterpret_cast<const uint16_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + si) * 36));
                 sm.xd[n * NSC + si] = v;
             }
         }
         __syncthreads();
-        if (c.g >= J->ng) continue;
+        if (c.g >= J.ng) continue;
         float yacc[NCOL];
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
         const int bend = c.b0 + c.nbl;
         for (int b = c.b0; b < bend;) {
-            const uint32_t mt = J->M[(size_t)c.g * J->nb + b];
+            const uint32_t mt = as_const(J.M)[(size_t)c.g * J.nb + b];
             // CM: the tile classes this instantiation decodes (chosen from the tensor's class histogram)
             switch (mt >> 29) {
-                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 1>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 2>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 3>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 4>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 5>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 6>(c, sm, b, bend, yacc); break; } [[fallthrough]];
-                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 7>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 2, gemv_nbuf(NCOL, 2), CM == (1 << 2)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 3, gemv_nbuf(NCOL, 3), CM == (1 << 3)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 4, gemv_nbuf(NCOL, 4), CM == (1 << 4)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 5, gemv_nbuf(NCOL, 5), CM == (1 << 5)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 6, gemv_nbuf(NCOL, 6), CM == (1 << 6)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 7, gemv_nbuf(NCOL, 7), CM == (1 << 7)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
                 default:
                     if constexpr (PARTIALS) {   // class 0: zero weights
                         const int r = 32 * c.g + c.j;
                         for (int n = 0; n < NCOL; ++n) {
-                            if constexpr (ACT == P8X_ACT_Q8_128) J->partials[((size_t)n * J->rows + r) * J->nsl + 2 * b + c.hs] = 0;
-                            else for (int u = 0; u < 4; ++u) J->partials[((size_t)n * J->rows + r) * (J->K / 32) + 8 * b + 4 * c.hs + u] = 0;
+                            if constexpr (ACT == P8X_ACT_Q8_128) J.partials[((size_t)n * J.rows + r) * J.nsl + 2 * b + c.hs] = 0;
+                            else for (int u = 0; u < 4; ++u) J.partials[((size_t)n * J.rows + r) * (J.K / 32) + 8 * b + 4 * c.hs + u] = 0;
                         }
                     }
                     ++b;
@@ -222,51 +251,51 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
         // half-slice 1 joins half-slice 0; lanes 0..31 hold the 32 rows
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] += __shfl_xor(yacc[n], 32);
-        bool final_rows = J->nks == 1;
-        if (J->nks > 1) {
+        bool final_rows = J.nks == 1;
+        if (J.nks > 1) {
             // K-chunk fix-up, no agent-scope fences (on gfx950 those write back and invalidate the XCD's whole L2):
             // partial rows are agent-coherent stores; the wave waits for them, then bumps the row group's arrival
             // counter; the last arrival reads the partials with agent-coherent loads and sums them in chunk order.
             if (lane < 32)
 #pragma unroll
                 for (int n = 0; n < NCOL; ++n)
-                    __hip_atomic_store(&J->wpart[((size_t)ks * NCOL + n) * J->rows + 32 * c.g + c.j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&J.wpart[((size_t)ks * NCOL + n) * J.rows + 32 * c.g + c.j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             unsigned old = 0;
-            if (lane == 0) old = __hip_atomic_fetch_add(&J->wcnt[c.g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) old = __hip_atomic_fetch_add(&J.wcnt[c.g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             old = __builtin_amdgcn_readfirstlane(old);
-            final_rows = old == (unsigned)(J->nks - 1);
+            final_rows = old == (unsigned)(J.nks - 1);
             if (final_rows) {
                 if (lane < 32)
 #pragma unroll
                     for (int n = 0; n < NCOL; ++n) {
                         // issue 8 partial loads at a time (one memory round trip per 8 chunks), sum in chunk order
                         float sacc = 0.f;
-                        for (int k0 = 0; k0 < J->nks; k0 += 8) {
+                        for (int k0 = 0; k0 < J.nks; k0 += 8) {
                             float pv[8];
 #pragma unroll
                             for (int i = 0; i < 8; ++i)
-                                pv[i] = k0 + i < J->nks ? __hip_atomic_load(&J->wpart[((size_t)(k0 + i) * NCOL + n) * J->rows + 32 * c.g + c.j],
+                                pv[i] = k0 + i < J.nks ? __hip_atomic_load(&J.wpart[((size_t)(k0 + i) * NCOL + n) * J.rows + 32 * c.g + c.j],
                                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
 #pragma unroll
                             for (int i = 0; i < 8; ++i)
-                                if (k0 + i < J->nks) sacc += pv[i];
+                                if (k0 + i < J.nks) sacc += pv[i];
                         }
                         yacc[n] = sacc;
                     }
-                if (lane == 0) __hip_atomic_store(&J->wcnt[c.g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) __hip_atomic_store(&J.wcnt[c.g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         if (final_rows && lane < 32) {
-            const int ro = J->prm[32 * c.g + c.j];
+            const int ro = J.prm[32 * c.g + c.j];
 #pragma unroll
             for (int n = 0; n < NCOL; ++n) {
                 float v = yacc[n];
-                if (J->x) {
-                    const float *xr = J->x + (size_t)n * J->ldx;
-                    for (int e = J->cp[ro]; e < J->cp[ro + 1]; ++e) v += J->cv[e] * xr[J->cc[e]];
+                if (J.x) {
+                    const float *xr = J.x + (size_t)n * J.ldx;
+                    for (int e = J.cp[ro]; e < J.cp[ro + 1]; ++e) v += J.cv[e] * xr[J.cc[e]];
                 }
-                J->y[(size_t)n * J->ldy + ro] = v;
+                J.y[(size_t)n * J.ldy + ro] = v;
             }
         }
     }
@@ -281,7 +310,8 @@ template <int NCOL, int ACT, bool PARTIALS, int CM>
 static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
     const int per_cu = gemv_waves_per_eu(NCOL, CM) >= 4 ? 2 : 1;   // 8-wave workgroups resident per CU
     const int grid = std::min(tasks, per_cu * num_cus());
-    hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
+    if (jobs) hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
+    else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
     return hip_check(hipGetLastError(), "k_gemv launch");
 }
 

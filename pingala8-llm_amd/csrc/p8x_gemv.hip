@@ -142,6 +142,7 @@ static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float
     g.wpart = t->wpart; g.wcnt = t->wcnt;
     g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl;
     g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + 7) / 8) * nks;
+    g.dbytes = (unsigned)(t->kbytes - offset_D(t->nt));
 }
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,

@@ -40,6 +40,19 @@ template <typename T>
 using gptr = __attribute__((address_space(1))) T *;
 template <typename T>
 __device__ __forceinline__ gptr<const T> as_global(const T *p) { return (gptr<const T>)p; }
+// constant address-space view (read-only for the kernel's lifetime): uniform loads become scalar s_load,
+// which wait on their own counter instead of behind the in-flight vector loads
+// raw buffer resources (stride 0, byte records); word 3 is the gfx9-family default for untyped access
+constexpr int kBufFlags = 0x00020000;
+constexpr int kBufNT = 2;   // cache policy: non-temporal (streamed once)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kBufFlags);
+}
+
+template <typename T>
+using kptr = __attribute__((address_space(4))) T *;
+template <typename T>
+__device__ __forceinline__ kptr<const T> as_const(const T *p) { return (kptr<const T>)p; }
 
 __device__ __forceinline__ uint32_t lds_word(const uint32_t *tab, uint32_t byte_addr) {
     return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(tab) + byte_addr);
@@ -110,23 +123,33 @@ struct RawSlice {
     uint16_t s;
 
     template <int W, int WB, int O>
-    __device__ __forceinline__ void load_region_raw(gptr<const uint32_t> p, int j) {
+    static __device__ __forceinline__ void region_offsets(uint32_t hsoff, int j, uint32_t (&vo)[NW]) {
         const int wr = ((((32 - j) & 31) * W) >> 5);
 #pragma unroll
-        for (int m = 0; m < W; ++m) w[O + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
+        for (int m = 0; m < W; ++m) vo[O + m] = 4u * (hsoff + (uint32_t)lane_word_offset(WB + (m + wr) % W, j));
     }
 
-    // p = half-slice base, srow = &S[b * rows + 32 g] (scale of lane j at srow[j])
-    __device__ __forceinline__ void load(gptr<const uint32_t> p, gptr<const uint16_t> srow, int j) {
+    // Byte offsets, within a tile's payload, of the lane's NW words in load order. They depend only on the
+    // lane (j, and hsoff = hs * NW * 32 for its half-slice), so a wave computes them once.
+    static __device__ __forceinline__ void lane_offsets(uint32_t hsoff, int j, uint32_t (&vo)[NW]) {
         if constexpr (W1 == 8) {
-            load_region_raw<8, 0, 0>(p, j);
+            region_offsets<8, 0, 0>(hsoff, j, vo);
         } else {
-            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
-            load_region_raw<W1 - 1, 1, 1>(p, j);
+            vo[0] = 4u * (hsoff + (uint32_t)lane_word_offset(0, j));
+            region_offsets<W1 - 1, 1, 1>(hsoff, j, vo);
         }
-        if constexpr (W2 > 0) load_region_raw<W2, W1, W1>(p, j);
-        if constexpr (W3 > 0) load_region_raw<W3, W1 + W2, W1 + W2>(p, j);
-        s = __builtin_nontemporal_load(srow + j);
+        if constexpr (W2 > 0) region_offsets<W2, W1, W1>(hsoff, j, vo);
+        if constexpr (W3 > 0) region_offsets<W3, W1 + W2, W1 + W2>(hsoff, j, vo);
+    }
+
+    // Buffer-resource loads: the tile's payload byte offset and its scale-row byte offset ride in the uniform
+    // soffset; the lane parts (vo, vs = 2 j) are fixed. A resource with no records reads zeros without
+    // touching memory, which is how a prefetch past the end of a run is issued unconditionally.
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rd, uint32_t toff, const uint32_t (&vo)[NW],
+                                         __amdgpu_buffer_rsrc_t rs, uint32_t soff, uint32_t vs) {
+#pragma unroll
+        for (int m = 0; m < NW; ++m) w[m] = __builtin_amdgcn_raw_buffer_load_b32(rd, vo[m], toff, kBufNT);
+        s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, soff, kBufNT);
     }
 };
 
