@@ -13,6 +13,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "p8x_internal.h"
 #include "p8x_lane.h"
 
@@ -41,15 +43,19 @@ struct GemvJob {
     unsigned dbytes;                 // payload region bytes (D .. end of the slot's payload)
 };
 
-constexpr int kXBytes = 14336;   // LDS activation bytes per task: ncol x kchunk x 256
+// LDS activation bytes per task: ncol x kchunk x 512. The step-order kernels keep each 128-column half of a
+// block twice in a row ([n][block][half][64 words], word i = chunk i & 31), so lane j reads its chunks
+// (j + k) & 31 for k = 0..31 at the unwrapped word offsets j + k; the other kernels use the first half.
+// Sized so that two workgroups (64 KB table + this + scales each) share one CU's 160 KB.
+constexpr int kXBytes = 15360;
 
-__host__ __device__ constexpr int kchunk_max(int ncol) { return kXBytes / (256 * ncol); }
+__host__ __device__ constexpr int kchunk_max(int ncol) { return kXBytes / (512 * ncol); }
 
 template <int NCOL, int ACT>
 struct GemvSmem {
     static constexpr int kScales = NCOL * (ACT == P8X_ACT_Q8_128 ? 2 : 8) * kchunk_max(NCOL);
     uint32_t tab[kTabWords];   // first member: LDS address 0, so table addresses need no base add
-    uint32_t xq[kXBytes / 4];  // [ncol][kchunk * 256 bytes]
+    uint32_t xq[kXBytes / 4];  // [ncol][kchunk][2][64] words (step order) or [ncol][kchunk][64] words
     float xd[kScales];         // [ncol][scales of the chunk]
 };
 
@@ -58,7 +64,12 @@ struct TaskCtx {
     const GemvJob *J;   // the descriptor in place (kernel argument or the launch's job array): never copied
     int g, b0, nbl, hs, j;
     uint32_t bankbytes;
+    int xlane;          // step order: the lane's word offset hs * 64 + j in a block's activation words
 };
+
+// Q8_128 activations without integer partials run in step order (natural, coalesced payload loads)
+template <int ACT, bool PARTIALS>
+__host__ __device__ constexpr bool gemv_step_order() { return ACT == P8X_ACT_Q8_128 && !PARTIALS; }
 
 template <int NCOL, int ACT, bool PARTIALS, int C>
 __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, const RawSlice<C> &raw,
@@ -121,6 +132,54 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
     }
 }
 
+// One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
+// order, only summed in another order.
+template <int NCOL, int C>
+__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const GemvSmem<NCOL, P8X_ACT_Q8_128> &sm,
+                                               const StepSlice<C> &raw, int b, float (&yacc)[NCOL]) {
+    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
+    constexpr int XW = kXBytes / 4 / NCOL;
+    constexpr int NSC = GemvSmem<NCOL, P8X_ACT_Q8_128>::kScales / NCOL;
+    const uint32_t H = raw.coset_bits(c.j);
+    const int bl = b - c.b0;
+    int acc[NST][NCOL];
+#pragma unroll
+    for (int s = 0; s < NST; ++s)
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
+    const uint32_t *xl = sm.xq + bl * 128 + c.xlane;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        uint32_t xv[NCOL][4];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[n][e] = xl[n * XW + 4 * q + e];
+        const uint32_t hq = coset_bytes(H, c.bankbytes, q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k = 4 * q + e;
+            uint32_t w[3];
+            w[0] = lds_word(sm.tab, raw.template addr<0>(k, hq));
+            if constexpr (NST > 1) w[1] = lds_word(sm.tab, raw.template addr<1>(k, hq));
+            if constexpr (NST > 2) w[2] = lds_word(sm.tab, raw.template addr<2>(k, hq));
+#pragma unroll
+            for (int n = 0; n < NCOL; ++n)
+#pragma unroll
+                for (int s = 0; s < NST; ++s) acc[s][n] = __builtin_amdgcn_sdot4((int)w[s], (int)xv[n][e], acc[s][n], false);
+        }
+        __asm__ volatile("" ::: "memory");   // one group of 4 steps at a time: bounds the live registers
+    }
+    const float sc = half_to_float(raw.s);
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) {
+        int isum = acc[0][n] * (1 << SH1);
+        if constexpr (NST > 1) isum += acc[1][n] * (1 << SH2);
+        if constexpr (NST > 2) isum += acc[2][n];
+        yacc[n] += ((float)isum * sm.xd[n * NSC + 2 * bl + c.hs]) * sc;
+    }
+}
+
 // A run of consecutive tiles of class C in row group g: the run's extent is found from the tile words
 // first, then NBUF register buffers rotate so that NBUF - 1 following tiles are in flight while the current
 // one is decoded. Every step issues its prefetch (past the run's end through an empty resource, which reads
@@ -139,12 +198,16 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
     }
     const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(J.D, J.dbytes), rs = buffer_rsrc(J.S, (uint32_t)J.nb * J.rows * 2u);
     const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(J.D, 0u);
-    uint32_t vo[NW];
-    RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
+    constexpr bool STEP = gemv_step_order<ACT, PARTIALS>();
+    using Slice = std::conditional_t<STEP, StepSlice<C>, RawSlice<C>>;
+    // lane part of the payload offsets: one base (step order) or the NW rotated word offsets
+    std::conditional_t<STEP, uint32_t, uint32_t[NW]> vo;
+    if constexpr (STEP) vo = (uint32_t)(c.hs * NW * 128 + 8 * c.j);
+    else RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
     const uint32_t vs = 2u * (uint32_t)c.j;
     // wn = tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
     uint32_t wn = tile_word(b);
-    auto issue = [&](RawSlice<C> &r, int ta) {
+    auto issue = [&](Slice &r, int ta) {
         const bool ok = ta < e;
         const int tc = ok ? ta : b;
         const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
@@ -152,7 +215,11 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
         r.load(ok ? rd : r0, toff, vo, ok ? rs : r0, soff, vs);
         wn = tile_word(min(ta + 1, e - 1));
     };
-    RawSlice<C> buf[NBUF];
+    auto tile = [&](const Slice &r, int t) {
+        if constexpr (STEP) gemv_tile_step<NCOL, C>(c, sm, r, t, yacc);
+        else gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, r, t, yacc);
+    };
+    Slice buf[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
     // whole groups of NBUF tiles: the loop body is straight-line, so the same loads are in flight at every
@@ -162,13 +229,13 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
             issue(buf[(i + NBUF - 1) % NBUF], base + i + NBUF - 1);
-            gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, buf[i], base + i, yacc);
+            tile(buf[i], base + i);
         }
     }
     // the last e - base < NBUF tiles are already in flight in buf[0 ..]
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i)
-        if (base + i < e) gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, buf[i], base + i, yacc);
+        if (base + i < e) tile(buf[i], base + i);
     return e;
 }
 
@@ -189,6 +256,7 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
     TaskCtx<NCOL, ACT> c;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
+    c.xlane = c.hs * 64 + c.j;
     build_coset_table(sm.tab, a2, tid, kGemvThreads);
     int jc = 0;
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
@@ -202,12 +270,21 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
         c.g = 8 * oct + w;
         // stage this task's activations and scales
         __syncthreads();
-        for (int i = tid; i < NCOL * c.nbl * 64; i += kGemvThreads) {
-            const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
-            uint32_t v;
-            if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[wi];
-            else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
-            sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
+        if constexpr (gemv_step_order<ACT, PARTIALS>()) {
+            // [n][block][half][64]: word i of a half = activation word (i & 31) of that half
+            for (int i = tid; i < NCOL * c.nbl * 128; i += kGemvThreads) {
+                const int n = i / (c.nbl * 128), wi = i % (c.nbl * 128);
+                const int src = (wi >> 7) * 64 + ((wi >> 6) & 1) * 32 + (wi & 31);
+                sm.xq[n * (kXBytes / 4 / NCOL) + wi] = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[src];
+            }
+        } else {
+            for (int i = tid; i < NCOL * c.nbl * 64; i += kGemvThreads) {
+                const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
+                uint32_t v;
+                if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[wi];
+                else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
+                sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
+            }
         }
         {
             constexpr int PER = ACT == P8X_ACT_Q8_128 ? 2 : 8;

@@ -228,6 +228,73 @@ struct LaneSlice {
     }
 };
 
+// ------------------------------------------------------------------------------------------------ step order
+// The same lane-slice decoded in step order: payload words exactly as stored, so a wave loads each pair of
+// words [i >> 1][j][i & 1] of its half-slice as one contiguous 8-byte-per-lane access (whole cache lines per
+// instruction). Field k of a region is step k of lane j, which encodes chunk (j + k) & 31: the activation
+// chunk is then lane-dependent (the caller reads it at a per-lane offset), while the coset bits come from the
+// trellis in chunk order, rotated into step order.
+template <int W, int OFF, int NW>
+__device__ __forceinline__ uint32_t field_at(const uint32_t (&w)[NW], int k) {
+    const int pos = W * k, wi = OFF + (pos >> 5), bb = pos & 31;
+    if (bb + W <= 32) return __builtin_amdgcn_ubfe(w[wi], bb, W);
+    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], bb) & ((1u << W) - 1u);
+}
+
+template <int C>
+struct StepSlice {
+    static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C), NP = NW / 2;
+    static constexpr int O1 = W1 == 8 ? 0 : 1, O2 = W1, O3 = W1 + W2;   // first word of each stage's fields
+    uint32_t w[NW];
+    uint16_t s;
+
+    // vo = hs * NW * 128 + 8 j: the lane's byte offset of word pair 0; pair p sits 256 p bytes further
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rd, uint32_t toff, uint32_t vo,
+                                         __amdgpu_buffer_rsrc_t rs, uint32_t soff, uint32_t vs) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, vo + 256u * p, toff, kBufNT);
+            w[2 * p] = v[0];
+            w[2 * p + 1] = v[1];
+        }
+        s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, soff, kBufNT);
+    }
+
+    // coset bits in step order for lane j
+    __device__ __forceinline__ uint32_t coset_bits(int j) const {
+        uint32_t z;
+        if constexpr (W1 == 8) {
+            uint32_t r[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r[i] = w[i];
+            z = labels_from_bytes(r);
+        } else {
+            z = w[0];
+        }
+        const uint32_t zc = __builtin_amdgcn_alignbit(z, z, (32 - j) & 31);   // bit k -> bit (j + k) & 31
+        const uint32_t hc = trellis_coset_bits(zc);
+        return __builtin_amdgcn_alignbit(hc, hc, j & 31);                      // back to step order
+    }
+
+    // LDS byte address of stage S at step k, hq = coset_bytes(H, bankbytes, k >> 2)
+    template <int S>
+    __device__ __forceinline__ uint32_t addr(int k, uint32_t hq) const {
+        const int e = k & 3;
+        if constexpr (S == 0) {
+            if constexpr (W1 == 8) return __builtin_amdgcn_perm(w[k >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else {
+                const uint32_t f = field_at<W1 - 1, O1>(w, k) | (__builtin_amdgcn_ubfe(w[0], k, 1) << (W1 - 1));
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
+            }
+        } else if constexpr (S == 1) {
+            if constexpr (W2 == 8) return __builtin_amdgcn_perm(w[O2 + (k >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else return __builtin_amdgcn_perm(field_at<W2, O2>(w, k), hq, 0x0c0c0400u | e);
+        } else {
+            return __builtin_amdgcn_perm(w[O3 + (k >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+        }
+    }
+};
+
 __device__ __forceinline__ int sext8(uint32_t w, int e) { return (int)(int8_t)(w >> (8 * e)); }
 
 }  // namespace p8x
