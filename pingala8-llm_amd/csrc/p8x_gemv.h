@@ -24,8 +24,6 @@ namespace p8x {
 #define GEMV_NBUF_C3 3
 #endif
 
-constexpr int kGemvWaves = 8;
-constexpr int kGemvThreads = 64 * kGemvWaves;
 
 // ------------------------------------------------------------------------------------------------ fused decode + GEMV
 // One GEMV of a launch. A launch walks a list of these (one entry for p8x_mul_mat_vec, many for a grouped
@@ -58,6 +56,23 @@ struct GemvSmem {
     uint32_t xq[kXBytes / 4];  // [ncol][kchunk][2][64] words (step order) or [ncol][kchunk][64] words
     float xd[kScales];         // [ncol][scales of the chunk]
 };
+
+// class sets with their own instantiations: class 3 only (the 2-bit bulk), class 6 only (4-bit attn_v),
+// classes 2-4 (mixed ffn_down), everything
+constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmAll = 0xFE;
+
+// Waves per workgroup (each owns one row group of a task) and the waves per SIMD the registers are sized for.
+// LDS holds two workgroups per CU; a variant that fits 64 VGPRs (one column, class 3, step order) runs
+// 16-wave workgroups, 8 waves per SIMD; the others 8-wave workgroups at 4 (<= 128 VGPRs) or 2 waves per SIMD.
+__host__ __device__ constexpr int gemv_waves(int ncol, int act, bool partials, int cm) {
+    return ncol == 1 && act == P8X_ACT_Q8_128 && !partials && cm == kCmC3 ? 16 : 8;
+}
+__host__ __device__ constexpr int gemv_waves_per_eu(int ncol, int act, bool partials, int cm) {
+    return gemv_waves(ncol, act, partials, cm) == 16 ? 8 : ncol == 1 && cm == kCmC3 ? 4 : 2;
+}
+__host__ __device__ constexpr int gemv_wg_per_cu(int ncol, int act, bool partials, int cm) {
+    return 4 * gemv_waves_per_eu(ncol, act, partials, cm) >= 2 * gemv_waves(ncol, act, partials, cm) ? 2 : 1;
+}
 
 template <int NCOL, int ACT>
 struct TaskCtx {
@@ -242,22 +257,20 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
 // prefetch depth (register buffers) per variant
 __host__ __device__ constexpr int gemv_nbuf(int ncol, int c) { return ncol == 1 && c == 3 ? GEMV_NBUF_C3 : 2; }
 
-// waves per SIMD the register budget is sized for: 4 (<= 128 VGPRs) where the kernel fits without spills
-// (one column, class-3 tiles), else 2
-__host__ __device__ constexpr int gemv_waves_per_eu(int ncol, int cm) { return ncol == 1 && cm == (1 << 3) ? 4 : 2; }
-
 // MULTI: the launch walks a job array in global memory (grouped launch); else its one job is the kernel argument
 template <int NCOL, int ACT, bool PARTIALS, int CM, bool MULTI>
-__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu(NCOL, CM), gemv_waves_per_eu(NCOL, CM))))
+__global__ __launch_bounds__(64 * gemv_waves(NCOL, ACT, PARTIALS, CM))
+__attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu(NCOL, ACT, PARTIALS, CM), gemv_waves_per_eu(NCOL, ACT, PARTIALS, CM))))
 void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_tasks, const uint32_t *__restrict__ a2) {
     __shared__ GemvSmem<NCOL, ACT> sm;   // static: the table sits at LDS address 0 at compile time
+    constexpr int WAVES = gemv_waves(NCOL, ACT, PARTIALS, CM), NT = 64 * WAVES;
     constexpr int NSC = GemvSmem<NCOL, ACT>::kScales / NCOL;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     TaskCtx<NCOL, ACT> c;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
-    build_coset_table(sm.tab, a2, tid, kGemvThreads);
+    build_coset_table(sm.tab, a2, tid, NT);
     int jc = 0;
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
         if constexpr (MULTI)
@@ -267,18 +280,18 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
         const int local = task - J.task0, oct = local / J.nks, ks = local % J.nks;
         c.b0 = ks * J.kchunk;
         c.nbl = min(J.kchunk, J.nb - c.b0);
-        c.g = 8 * oct + w;
+        c.g = WAVES * oct + w;
         // stage this task's activations and scales
         __syncthreads();
         if constexpr (gemv_step_order<ACT, PARTIALS>()) {
             // [n][block][half][64]: word i of a half = activation word (i & 31) of that half
-            for (int i = tid; i < NCOL * c.nbl * 128; i += kGemvThreads) {
+            for (int i = tid; i < NCOL * c.nbl * 128; i += NT) {
                 const int n = i / (c.nbl * 128), wi = i % (c.nbl * 128);
                 const int src = (wi >> 7) * 64 + ((wi >> 6) & 1) * 32 + (wi & 31);
                 sm.xq[n * (kXBytes / 4 / NCOL) + wi] = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[src];
             }
         } else {
-            for (int i = tid; i < NCOL * c.nbl * 64; i += kGemvThreads) {
+            for (int i = tid; i < NCOL * c.nbl * 64; i += NT) {
                 const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
                 uint32_t v;
                 if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[wi];
@@ -288,7 +301,7 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
         }
         {
             constexpr int PER = ACT == P8X_ACT_Q8_128 ? 2 : 8;
-            for (int i = tid; i < NCOL * PER * c.nbl; i += kGemvThreads) {
+            for (int i = tid; i < NCOL * PER * c.nbl; i += NT) {
                 const int n = i / (PER * c.nbl), si = i % (PER * c.nbl);
                 float v;
                 if constexpr (ACT == P8X_ACT_Q8_128) v = J.d[(size_t)n * J.nsl + 2 * c.b0 + si];
@@ -379,16 +392,13 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
 }
 
 
-// class sets with their own instantiations: class 3 only (the 2-bit bulk), class 6 only (4-bit attn_v),
-// classes 2-4 (mixed ffn_down), everything
-constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmAll = 0xFE;
 
 template <int NCOL, int ACT, bool PARTIALS, int CM>
 static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
-    const int per_cu = gemv_waves_per_eu(NCOL, CM) >= 4 ? 2 : 1;   // 8-wave workgroups resident per CU
-    const int grid = std::min(tasks, per_cu * num_cus());
-    if (jobs) hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
-    else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(kGemvThreads), 0, st, jobs, job0, njobs, tasks, a2);
+    constexpr int NT = 64 * gemv_waves(NCOL, ACT, PARTIALS, CM);
+    const int grid = std::min(tasks, gemv_wg_per_cu(NCOL, ACT, PARTIALS, CM) * num_cus());
+    if (jobs) hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
+    else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
     return hip_check(hipGetLastError(), "k_gemv launch");
 }
 

@@ -110,10 +110,20 @@ __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, si
 
 // K-split of a single-GEMV launch: about one task per workgroup slot, at least two tiles per wave, chunks no
 // larger than the LDS activation buffer allows.
-GemvPlan gemv_plan(const p8x_tensor *t, int ncols) {
+int class_set(const size_t hist[8]) {
+    int m = 0;
+    for (int c = 1; c < 8; ++c) if (hist[c]) m |= 1 << c;
+    for (int cm : {kCmC3, kCmC6, kCmC234})
+        if ((m & ~cm) == 0) return cm;
+    return kCmAll;
+}
+
+GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
     GemvPlan p;
-    const int octets = (t->ng + 7) / 8;
-    const int slots = 2 * num_cus();
+    const int cm = partials || act != P8X_ACT_Q8_128 ? kCmAll : class_set(t->class_tiles);
+    p.gpt = gemv_waves(ncols, act, partials, cm);
+    const int octets = (t->ng + p.gpt - 1) / p.gpt;
+    const int slots = gemv_wg_per_cu(ncols, act, partials, cm) * num_cus();
     int nks = (slots + octets - 1) / octets;
     nks = std::min(nks, std::max(1, t->nb / 2));
     nks = std::max(nks, (t->nb + kchunk_max(ncols) - 1) / kchunk_max(ncols));
@@ -125,34 +135,27 @@ GemvPlan gemv_plan(const p8x_tensor *t, int ncols) {
     return p;
 }
 
-int class_set(const size_t hist[8]) {
-    int m = 0;
-    for (int c = 1; c < 8; ++c) if (hist[c]) m |= 1 << c;
-    for (int cm : {kCmC3, kCmC6, kCmC234})
-        if ((m & ~cm) == 0) return cm;
-    return kCmAll;
-}
 
 static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
-                     float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int task0) {
+                     float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int gpt, int task0) {
     g = GemvJob{};
     g.M = t->M; g.S = t->S; g.D = t->D; g.prm = t->prm;
     g.cp = t->cp; g.cc = t->cc; g.cv = t->cv;
     g.q = q; g.d = d; g.x = x; g.ldx = (unsigned)ldx; g.y = y; g.ldy = (unsigned)ldy; g.partials = partials;
     g.wpart = t->wpart; g.wcnt = t->wcnt;
     g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl;
-    g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + 7) / 8) * nks;
+    g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + gpt - 1) / gpt) * nks;
     g.dbytes = (unsigned)(t->kbytes - offset_D(t->nt));
 }
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st) {
-    const GemvPlan p = gemv_plan(t, ncols);
-    if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
-    GemvJob job0;
-    fill_job(job0, t, q, d, x, ldx, y, ldy, partials, p.nks, p.bpk, 0);
     const int cm = class_set(t->class_tiles);
     if (partials) {   // integer partials: one column per launch
+        const GemvPlan p1 = gemv_plan(t, 1, act, true);
+        if (p1.nks > 1 && (size_t)p1.nks * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
+        GemvJob job0;
+        fill_job(job0, t, q, d, x, ldx, y, ldy, partials, p1.nks, p1.bpk, p1.gpt, 0);
         for (int n = 0; n < ncols; ++n) {
             GemvJob jn = job0;
             const size_t qcol = act == P8X_ACT_Q8_128 ? (size_t)t->K : (size_t)36 * (t->K / 32);
@@ -161,13 +164,15 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
             if (x) jn.x = x + (size_t)n * ldx;
             jn.y = y + (size_t)n * ldy;
             jn.partials = partials + (size_t)n * t->rows * (act == P8X_ACT_Q8_128 ? t->nsl : t->K / 32);
-            const GemvPlan p1 = gemv_plan(t, 1);
-            jn.nks = p1.nks; jn.kchunk = p1.bpk; jn.ntasks = ((t->ng + 7) / 8) * p1.nks;
             const int rc = launch_gemv_partials(act, jn, t->a2, st);
             if (rc) return rc;
         }
         return P8X_OK;
     }
+    const GemvPlan p = gemv_plan(t, ncols, act, false);
+    if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
+    GemvJob job0;
+    fill_job(job0, t, q, d, x, ldx, y, ldy, nullptr, p.nks, p.bpk, p.gpt, 0);
     if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, nullptr, job0, 1, job0.ntasks, t->a2, st);
     return launch_gemv_q81(ncols, nullptr, job0, 1, job0.ntasks, t->a2, st);
 }
@@ -247,6 +252,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     size_t bytes = 0;
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
     int task0 = 0, blk0 = 0;
+    const int cm = class_set(hist), gpt = gemv_waves(ncols, P8X_ACT_Q8_128, false, cm);
     for (int i = 0; i < njobs; ++i) {
         const p8x_tensor *t = tensors[i];
         const int kc = std::min(t->nb, kchunk_max(ncols));
@@ -255,13 +261,13 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         off_d[i] = take(4 * (size_t)ncols * t->nsl);
         off_p[i] = nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
         off_c[i] = nks > 1 ? take(4 * (size_t)t->ng) : 0;
-        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, task0);
+        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, task0);
         task0 += jobs[i].ntasks;
         act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
         blk0 += t->nb;
     }
     p8x_gemv_batch *b = new p8x_gemv_batch();
-    b->njobs = njobs; b->ncols = ncols; b->cm = class_set(hist); b->total_tasks = task0; b->total_blocks = blk0;
+    b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_tasks = task0; b->total_blocks = blk0;
     b->a2 = tensors[0]->a2;
     int rc;
     if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||

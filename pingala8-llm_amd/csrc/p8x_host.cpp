@@ -207,8 +207,14 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->D = (const uint32_t *)(t->base + offset_D(nt));
     t->prm = (const int16_t *)(t->base + off[2]);
     for (int nc = 1; nc <= P8X_MAX_COLS; ++nc) {   // partial rows of the largest single-GEMV plan
-        const GemvPlan plan = gemv_plan(t, nc);
-        if (plan.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)plan.nks * nc * rows);
+        for (int act : {P8X_ACT_Q8_128, P8X_ACT_Q8_1}) {
+            const GemvPlan plan = gemv_plan(t, nc, act, false);
+            if (plan.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)plan.nks * nc * rows);
+            if (nc == 1) {
+                const GemvPlan pp = gemv_plan(t, 1, act, true);
+                if (pp.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)pp.nks * rows);
+            }
+        }
     }
     if ((rc = alloc((void **)&t->a2, 512 * 4, "tables"))) return fail(rc);
     if ((rc = alloc((void **)&t->ic, 4 * (size_t)K, "ic"))) return fail(rc);

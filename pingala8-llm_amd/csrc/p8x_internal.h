@@ -47,9 +47,9 @@ int set_error(int code, const char *fmt, ...);
 int hip_check(hipError_t e, const char *what);
 
 struct GemvPlan {
-    int bpk, nks, grid, items;
+    int bpk, nks, grid, items, gpt;   // gpt: row groups per task (waves per workgroup)
 };
-GemvPlan gemv_plan(const p8x_tensor *t, int ncols);
+GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials);
 
 // launchers (p8x_gemv.hip, p8x_decode.hip, p8x_gemm.hip)
 int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st);
