@@ -80,7 +80,8 @@ void orc_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]) {
 /* ---------------------------------------------------------------- open (CPU.patch:234-275, :4335-4352) */
 int orc_open(orc_tensor *t, const uint8_t *base, size_t n, int rows, int K) {
     memset(t, 0, sizeof(*t));
-    if (n < 4096 || rows <= 0 || K <= 0 || K % 256 || rows % 32 || rows >= 32768) return 1;
+    /* fixed regions: header 2064, Hadamard signs 256, trailer 32 (vrn_offsets, CPU.patch:37-44) */
+    if (n < 2064 + 256 + 32 || rows <= 0 || K <= 0 || K % 256 || rows % 32 || rows >= 32768) return 1;
     uint32_t tr[8];
     memcpy(tr, base + n - 32, 32);
     if (tr[0] != 0x4E525656u || tr[1] != 0x31354952u || tr[4] != (uint32_t)rows || tr[5] != (uint32_t)K || tr[6] != 108u) return 1;
@@ -95,7 +96,7 @@ int orc_open(orc_tensor *t, const uint8_t *base, size_t n, int rows, int K) {
     t->D = (const uint32_t *)(base + a16(2064 + 68 * t->nt));
     size_t off[6];
     orc_offsets(n, (size_t)rows, (size_t)K, (size_t)t->nd, off);
-    if (t->kbytes > off[0]) return 3;
+    if (off[0] > n || t->kbytes > off[0]) return 3;   /* off[0] > n: the top-down regions wrapped below 0 */
     size_t words = 0;
     for (size_t i = 0; i < t->nt; ++i) words += (size_t)64 * orc_nw((int)(t->M[i] >> 29));
     if (a16(2064 + 68 * t->nt) + 4 * words != t->kbytes) return 4;

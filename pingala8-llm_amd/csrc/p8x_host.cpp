@@ -88,7 +88,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
     for (void *p : {(void *)t->owned, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
-                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->wx16})
+                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
 }
@@ -98,7 +98,8 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     *out = nullptr;
     if (rows <= 0 || K <= 0 || K % 256 || rows % 32 || rows >= 32768)
         return set_error(P8X_ERR_ARG, "p8x_prepare: shape %d x %d (need K %% 256 == 0, rows %% 32 == 0, rows < 32768)", rows, K);
-    if (n < 4096) return set_error(P8X_ERR_FORMAT, "p8x_prepare: slot of %zu bytes is too small", n);
+    // fixed regions: header, Hadamard signs, trailer (the variable ones are checked against the trailer below)
+    if (n < kHeaderBytes + 256 + 32) return set_error(P8X_ERR_FORMAT, "p8x_prepare: slot of %zu bytes is too small", n);
     const uint8_t *src = (const uint8_t *)slot;
     auto fetch = [&](size_t off, size_t len, void *dst) -> int {
         if (off + len > n) return set_error(P8X_ERR_FORMAT, "p8x_prepare: region [%zu, %zu) beyond the slot", off, off + len);
@@ -227,6 +228,12 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
     if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
+    std::vector<int> drows;
+    for (int r = 0; r < rows; ++r) if (cp[r + 1] > cp[r]) drows.push_back(r);
+    t->ndrows = (int)drows.size();
+    if ((rc = alloc((void **)&t->drows, 4 * std::max<size_t>(1, drows.size()), "delta row list"))) return fail(rc);
+    if (!drows.empty() && (rc = hip_check(hipMemcpy(t->drows, drows.data(), 4 * drows.size(), hipMemcpyHostToDevice), "p8x_prepare: delta rows")))
+        return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->a2, a2.data(), 512 * 4, hipMemcpyHostToDevice), "p8x_prepare: tables"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->ic, ic.data(), 4 * (size_t)K, hipMemcpyHostToDevice), "p8x_prepare: ic"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->cp, cp.data(), 4 * (size_t)(rows + 1), hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);

@@ -35,8 +35,12 @@ struct p8x_tensor {
     float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan
     size_t wpart_floats = 0;
     unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
-    uint16_t *wx16 = nullptr;        // rotated fp16 activations for the prompt GEMM (grown on demand)
-    size_t wx16_elems = 0;
+    int *drows = nullptr;            // original rows that carry clamp-delta entries [ndrows]
+    int ndrows = 0;
+    uint16_t *wx16 = nullptr;        // prompt GEMM: rotated fp16 activations [N][K] (grown on demand)
+    size_t wx16_elems = 0;           // capacity in bytes
+    float *wmm = nullptr;            // prompt GEMM: K-split partial planes (grown on demand)
+    size_t wmm_bytes = 0;
     bool wrap_free = true;           // |A + c| <= 127 bytewise
     uint32_t a2_host[512];           // host copy of a2 (batches check that tensors share the tables)
 };
