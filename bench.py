@@ -28,6 +28,7 @@ import numpy as np  # noqa: E402
 import p8x  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16/bf16 MFMA, MI355X
 LLAMA_LAYER = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096), ("attn_output", 4096, 4096),
                ("ffn_gate", 14336, 4096), ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 HEAD_SHARDS = [("lm_head", 32064, 4096)] * 4
@@ -129,6 +130,35 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
     return per_linear
 
 
+def measure_gemm(steps, N=512):
+    """prompt GEMM on the Llama-3.1-8B FFN shapes: N bf16 tokens ~ N(0, 1), whole p8x_mul_mat calls timed"""
+    out = {}
+    rng = np.random.default_rng(3)
+    for name, rows, K in (("ffn_up 4096->14336", 14336, 4096), ("ffn_down 14336->4096", 4096, 14336)):
+        t = p8x.Tensor(p8x.synth_random(rows + K, rows, K, nd=8), rows, K)
+        u = rng.standard_normal((N, K)).astype(np.float32).view(np.uint32).astype(np.uint64)
+        xb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        xd = p8x.DeviceBuffer.from_numpy(xb)
+        yd = p8x.DeviceBuffer(4 * N * rows)
+        stream = p8x.Stream()
+        for _ in range(3):
+            t.mul_mat_dev(xd, p8x.BF16, N, yd, stream=stream)
+        stream.sync()
+        ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
+        for a, b in ev:
+            a.record(stream)
+            t.mul_mat_dev(xd, p8x.BF16, N, yd, stream=stream)
+            b.record(stream)
+        stream.sync()
+        ms = float(np.median([a.elapsed_ms(b) for a, b in ev]))
+        tflops = 2.0 * rows * K * N / (ms * 1e-3) / 1e12
+        out[name] = {"us_per_call": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
+                     "frac_of_fp16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "tokens": N}
+        t.release()
+    log("prompt GEMM:", json.dumps(out))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,6 +169,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -183,6 +214,7 @@ def main():
 
     # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
     per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
+    gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     cpu = None
     if not args.no_cpu and host0:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -203,6 +235,7 @@ def main():
                      "bytes_per_launch": int(step_bytes)},
         "cpu_baseline": cpu,
         "per_linear_launches": per_linear,
+        "prompt_gemm": gemm,
         "host_wall_s": round(wall, 3),
     }
     print(json.dumps(out), flush=True)

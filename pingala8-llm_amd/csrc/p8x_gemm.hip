@@ -5,12 +5,13 @@
 // so  Y[n, prm[r]] = sum_b S[b][r] sum_i v[r, 256b + i] x'[n, 256b + i] + delta terms, with
 //   x' = FWHT(x ic) / 16 per 256-block (the GEMV's activation prep, CPU.patch:559-571, kept in fp16 here).
 // Pass 1 (k_mm_act) writes x' as fp16 [N][K]. Pass 2 (k_mm) gives each wave two 32-row tiles of a 256-row
-// workgroup tile: per 256-block it decodes the tiles in chunk order (rotated loads, p8x_lane.h) from a
-// 2 KB LDS copy of the coset table straight into fp16 MFMA operands (v S, one rounding), and multiplies them
-// with x' staged in LDS by v_mfma_f32_32x32x16_f16 with fp32 accumulation. Tokens are the MFMA rows and weight
-// rows its columns, so each lane's outputs run along 32 consecutive sorted rows. Deep-K shapes split K over
-// workgroups into fp32 partial planes summed in a fixed order by k_mm_reduce (deterministic). The sparse
-// clamp delta (CPU.patch:1193) is added last on the original activations by k_mm_delta.
+// workgroup tile: per 256-block it decodes the tiles in chunk order (rotated loads, p8x_lane.h) through a
+// 4 KB fp16 LDS copy of the coset table straight into MFMA operands (v S, one rounding), and multiplies them
+// with the block's x' (staged by direct-to-LDS loads) by v_mfma_f32_32x32x16_f16 with fp32 accumulation.
+// Tokens are the MFMA rows and weight rows its columns, so each lane's outputs run along 32 consecutive sorted
+// rows (coalesced stores). Sorted-row planes (one per K split) are then summed in a fixed order, un-permuted
+// and given the sparse clamp delta (CPU.patch:1193) on the original activations by k_mm_finish; a tensor
+// with identity rows and one K range writes y directly and only adds the delta.
 //
 // Reference role: ggml_cuda_f44_mul_mat_q8 (CPU.patch:2303-2343), which instead dequantizes the tensor to a
 // Q8_0 slab (k_r51_k1, CPU.patch:2138-2235) and calls the stock integer MMQ.
@@ -30,7 +31,7 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 constexpr int kMmRows = 256;     // weight rows per workgroup tile (4 waves x 2 row groups)
 constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles of 32)
 constexpr int kMmThreads = 256;
-constexpr int kMmXStride = 136;  // halfs per staged token row (128 + 8 pad: 16-byte reads spread over the banks)
+constexpr int kXcds = 8;          // MI355X: 8 accelerator dies, each with its own L2
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the
@@ -72,13 +73,40 @@ __global__ __launch_bounds__(64) void k_mm_act(const XT *__restrict__ x, size_t 
 
 // ------------------------------------------------------------------------------------------------ pass 2
 struct MmJob {
-    const uint32_t *M; const uint16_t *S; const uint32_t *D; const int16_t *prm;
+    const uint32_t *M; const uint16_t *S; const uint32_t *D;
     const _Float16 *xr;     // x' [N][K]
-    float *y; unsigned ldy;
-    float *ws;              // partial planes [nsplit][N][rows] (sorted rows), nsplit > 1
+    float *y; unsigned ldy; // direct output (original rows = sorted rows, one K range)
+    float *ws;              // sorted-row planes [nsplit][N][rows] otherwise
     const uint32_t *a2;     // [2][256] coset table words (A[f] + h c), h-major
     int N, rows, K, nb, ng;
-    int tiles_m, tiles_n, nsplit, kper;
+    int tiles_m, tiles_n, nsplit, kper, direct;
+};
+
+// Raw payload words of one lane-slice (any class up to NWMAX words) in rotated load order, plus the lane's
+// fp16 row scale: issued a block ahead, decoded into an MmSlice after the current block's products.
+template <int NWMAX>
+struct MmRaw {
+    uint32_t w[NWMAX];
+    uint16_t s;
+
+    template <int W, int WB>
+    __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
+        const int wr = (((32 - j) & 31) * W) >> 5;
+#pragma unroll
+        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
+    }
+    template <int C>
+    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j, const uint16_t *__restrict__ srow) {
+        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
+        if constexpr (W1 == 8) region<8, 0>(p, j);
+        else {
+            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
+            region<W1 - 1, 1>(p, j);
+        }
+        if constexpr (W2 > 0) region<W2, W1>(p, j);
+        if constexpr (W3 > 0) region<W3, W1 + W2>(p, j);
+        s = srow[j];
+    }
 };
 
 // Rotated lane-slice words of any class up to NWMAX words (chunk order after the per-lane rotation), plus the
@@ -89,64 +117,61 @@ struct MmSlice {
     uint32_t H;
     uint16_t s;
 
+    template <int W, int WB>
+    __device__ __forceinline__ void rotate(const MmRaw<NWMAX> &raw, int j) {
+        const int br = (((32 - j) & 31) * W) & 31;
+#pragma unroll
+        for (int i = 0; i < W; ++i) r[WB + i] = __builtin_amdgcn_alignbit(raw.w[WB + (i + 1) % W], raw.w[WB + i], br);
+    }
     template <int C>
-    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j, const uint16_t *__restrict__ srow) {
+    __device__ __forceinline__ void from_raw(const MmRaw<NWMAX> &raw, int j) {
         constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
         uint32_t z;
         if constexpr (W1 == 8) {
+            rotate<8, 0>(raw, j);
             uint32_t R[8];
-            load_region<8, 0>(p, j, R);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) r[i] = R[i];
+            for (int i = 0; i < 8; ++i) R[i] = r[i];
             z = labels_from_bytes(R);
         } else {
-            const uint32_t w0 = __builtin_nontemporal_load(p + lane_word_offset(0, j));
-            r[0] = __builtin_amdgcn_alignbit(w0, w0, (32 - j) & 31);
+            r[0] = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
             z = r[0];
-            uint32_t R[W1 - 1];
-            load_region<W1 - 1, 1>(p, j, R);
-#pragma unroll
-            for (int i = 0; i < W1 - 1; ++i) r[1 + i] = R[i];
+            rotate<W1 - 1, 1>(raw, j);
         }
-        if constexpr (W2 > 0) {
-            uint32_t R[W2];
-            load_region<W2, W1>(p, j, R);
-#pragma unroll
-            for (int i = 0; i < W2; ++i) r[W1 + i] = R[i];
-        }
-        if constexpr (W3 > 0) {
-            uint32_t R[W3];
-            load_region<W3, W1 + W2>(p, j, R);
-#pragma unroll
-            for (int i = 0; i < W3; ++i) r[W1 + W2 + i] = R[i];
-        }
+        if constexpr (W2 > 0) rotate<W2, W1>(raw, j);
+        if constexpr (W3 > 0) rotate<W3, W1 + W2>(raw, j);
         H = trellis_coset_bits(z);
-        s = srow[j];
+        s = raw.s;
     }
 
-    // stage-S field of chunk t
+    // LDS byte address of stage S at chunk t in the replicated table (p8x_lane.h layout: (f << 8) | (h << 7) |
+    // (bank << 2)); hq = coset_bytes(H, bankbytes, t >> 2) holds the (h << 7) | (bank << 2) byte of each chunk
     template <int C, int S>
-    __device__ __forceinline__ uint32_t field(int t) const {
+    __device__ __forceinline__ uint32_t addr(int t, uint32_t hq) const {
         constexpr int W1 = w1_of(C), W2 = w2_of(C);
+        const int e = t & 3;
         if constexpr (S == 0) {
-            if constexpr (W1 == 8) return __builtin_amdgcn_ubfe(r[t >> 2], 8 * (t & 3), 8);
+            if constexpr (W1 == 8) return __builtin_amdgcn_perm(r[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
             else {
                 constexpr int W = W1 - 1;
                 const int pos = W * t, wi = 1 + (pos >> 5), bb = pos & 31;
                 uint32_t f;
                 if (bb + W <= 32) f = __builtin_amdgcn_ubfe(r[wi], bb, W);
-                else f = __builtin_amdgcn_alignbit(r[1 + ((wi - 1 + 1) % W)], r[wi], bb) & ((1u << W) - 1u);
-                return f | (__builtin_amdgcn_ubfe(r[0], t, 1) << W);
+                else f = __builtin_amdgcn_alignbit(r[1 + (wi % W)], r[wi], bb) & ((1u << W) - 1u);
+                f |= __builtin_amdgcn_ubfe(r[0], t, 1) << W;
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
             }
         } else if constexpr (S == 1) {
-            if constexpr (W2 == 8) return __builtin_amdgcn_ubfe(r[W1 + (t >> 2)], 8 * (t & 3), 8);
+            if constexpr (W2 == 8) return __builtin_amdgcn_perm(r[W1 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
             else {
                 const int pos = W2 * t, wi = pos >> 5, bb = pos & 31;
-                if (bb + W2 <= 32) return __builtin_amdgcn_ubfe(r[W1 + wi], bb, W2);
-                return __builtin_amdgcn_alignbit(r[W1 + (wi + 1) % W2], r[W1 + wi], bb) & ((1u << W2) - 1u);
+                uint32_t f;
+                if (bb + W2 <= 32) f = __builtin_amdgcn_ubfe(r[W1 + wi], bb, W2);
+                else f = __builtin_amdgcn_alignbit(r[W1 + (wi + 1) % W2], r[W1 + wi], bb) & ((1u << W2) - 1u);
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
             }
         } else {
-            return __builtin_amdgcn_ubfe(r[W1 + W2 + (t >> 2)], 8 * (t & 3), 8);
+            return __builtin_amdgcn_perm(r[W1 + W2 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
         }
     }
 };
@@ -155,23 +180,27 @@ struct MmSlice {
 __device__ __forceinline__ half2v ob_lo(uint32_t w) { return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)); }
 __device__ __forceinline__ half2v ob_hi(uint32_t w) { return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)); }
 
-// chunk t of class C -> 4 fp16 weights v S (v exact in fp16, |v| <= 1596; one rounding for the product)
+// LDS words of chunk t, all stages (table bytes are A[f] + h c offset by 128)
 template <int C, int NWMAX>
-__device__ __forceinline__ void decode_chunk(const MmSlice<NWMAX> &ls, const uint32_t *tab, int t, half2v s2, half2v &lo, half2v &hi) {
+__device__ __forceinline__ void lookup_chunk(const MmSlice<NWMAX> &ls, const uint32_t *tab, int t, uint32_t hq, uint32_t (&w)[3]) {
+    constexpr int NST = nstage_of(C);
+    w[0] = lds_word(tab, ls.template addr<C, 0>(t, hq));
+    if constexpr (NST > 1) w[1] = lds_word(tab, ls.template addr<C, 1>(t, hq));
+    if constexpr (NST > 2) w[2] = lds_word(tab, ls.template addr<C, 2>(t, hq));
+}
+
+// table words of one chunk -> 4 fp16 weights v S (v exact in fp16, |v| <= 1596; one rounding for the product)
+template <int C>
+__device__ __forceinline__ void weights_chunk(const uint32_t (&w)[3], half2v s2, half2v &lo, half2v &hi) {
     constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
-    const uint32_t h4 = __builtin_amdgcn_ubfe(ls.H, t, 1) << 2;
     const half2v bias = {(_Float16)-1152.f, (_Float16)-1152.f};
-    uint32_t w[3];
-    w[0] = lds_word(tab, (ls.template field<C, 0>(t) << 3) | h4);
-    if constexpr (NST > 1) w[1] = lds_word(tab, (ls.template field<C, 1>(t) << 3) | h4);
-    if constexpr (NST > 2) w[2] = lds_word(tab, (ls.template field<C, 2>(t) << 3) | h4);
     half2v vl = ob_lo(w[0]) + bias, vh = ob_hi(w[0]) + bias;
     if constexpr (NST > 1) {
         const half2v m1 = {(_Float16)(float)(1 << SH1), (_Float16)(float)(1 << SH1)};
         const half2v m2 = {(_Float16)(float)(1 << SH2), (_Float16)(float)(1 << SH2)};
         half2v al = (ob_lo(w[1]) + bias) * m2, ah = (ob_hi(w[1]) + bias) * m2;
         if constexpr (NST > 2) { al += ob_lo(w[2]) + bias; ah += ob_hi(w[2]) + bias; }
-        vl = vl * m1 + al;
+        vl = vl * m1 + al;   // integers below 2048: exact in fp16
         vh = vh * m1 + ah;
     }
     lo = vl * s2;
@@ -179,11 +208,15 @@ __device__ __forceinline__ void decode_chunk(const MmSlice<NWMAX> &ls, const uin
 }
 
 template <int C, int NWMAX>
-__device__ __forceinline__ half8v decode_pair(const MmSlice<NWMAX> &ls, const uint32_t *tab, int s) {
+__device__ __forceinline__ half8v decode_pair(const MmSlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes, int s) {
     const half2v s2 = {__builtin_bit_cast(_Float16, ls.s), __builtin_bit_cast(_Float16, ls.s)};
+    const uint32_t hq = coset_bytes(ls.H, bankbytes, s >> 1);
+    uint32_t w0[3], w1[3];
+    lookup_chunk<C>(ls, tab, 2 * s, hq, w0);
+    lookup_chunk<C>(ls, tab, 2 * s + 1, hq, w1);
     half2v a, b, c, d;
-    decode_chunk<C>(ls, tab, 2 * s, s2, a, b);
-    decode_chunk<C>(ls, tab, 2 * s + 1, s2, c, d);
+    weights_chunk<C>(w0, s2, a, b);
+    weights_chunk<C>(w1, s2, c, d);
     half8v o;
     o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y; o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
     return o;
@@ -191,49 +224,199 @@ __device__ __forceinline__ half8v decode_pair(const MmSlice<NWMAX> &ls, const ui
 
 // classes decoded by an instantiation: the tensor's class set (class 0 decodes as zeros in all of them)
 constexpr int kMmCmC3 = 1 << 3, kMmCmAll = 0xFE;
+constexpr int kMmMain = 3;   // the class with a branch-free path in every instantiation (the 2-bit bulk)
 __host__ __device__ constexpr int mm_nwmax(int cm) { return cm == kMmCmC3 ? 8 : 24; }
 
 template <int CM, int NWMAX>
-__device__ __forceinline__ half8v decode_any(const MmSlice<NWMAX> &ls, int c, const uint32_t *tab, int s) {
+__device__ __forceinline__ half8v decode_any(const MmSlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
     switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) return decode_pair<1>(ls, tab, s); break;
-        case 2: if constexpr ((CM >> 2) & 1) return decode_pair<2>(ls, tab, s); break;
-        case 3: if constexpr ((CM >> 3) & 1) return decode_pair<3>(ls, tab, s); break;
-        case 4: if constexpr ((CM >> 4) & 1) return decode_pair<4>(ls, tab, s); break;
-        case 5: if constexpr ((CM >> 5) & 1) return decode_pair<5>(ls, tab, s); break;
-        case 6: if constexpr ((CM >> 6) & 1) return decode_pair<6>(ls, tab, s); break;
-        case 7: if constexpr ((CM >> 7) & 1) return decode_pair<7>(ls, tab, s); break;
+        case 1: if constexpr ((CM >> 1) & 1) return decode_pair<1>(ls, tab, bankbytes, s); break;
+        case 2: if constexpr ((CM >> 2) & 1) return decode_pair<2>(ls, tab, bankbytes, s); break;
+        case 3: if constexpr ((CM >> 3) & 1) return decode_pair<3>(ls, tab, bankbytes, s); break;
+        case 4: if constexpr ((CM >> 4) & 1) return decode_pair<4>(ls, tab, bankbytes, s); break;
+        case 5: if constexpr ((CM >> 5) & 1) return decode_pair<5>(ls, tab, bankbytes, s); break;
+        case 6: if constexpr ((CM >> 6) & 1) return decode_pair<6>(ls, tab, bankbytes, s); break;
+        case 7: if constexpr ((CM >> 7) & 1) return decode_pair<7>(ls, tab, bankbytes, s); break;
         default: break;
     }
     return half8v{};
 }
 
 template <int CM, int NWMAX>
-__device__ __forceinline__ void load_any(MmSlice<NWMAX> &ls, int c, const uint32_t *p, int j, const uint16_t *srow) {
+__device__ __forceinline__ void load_any(MmRaw<NWMAX> &raw, int c, const uint32_t *p, int j, const uint16_t *srow) {
     switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) ls.template load<1>(p, j, srow); break;
-        case 2: if constexpr ((CM >> 2) & 1) ls.template load<2>(p, j, srow); break;
-        case 3: if constexpr ((CM >> 3) & 1) ls.template load<3>(p, j, srow); break;
-        case 4: if constexpr ((CM >> 4) & 1) ls.template load<4>(p, j, srow); break;
-        case 5: if constexpr ((CM >> 5) & 1) ls.template load<5>(p, j, srow); break;
-        case 6: if constexpr ((CM >> 6) & 1) ls.template load<6>(p, j, srow); break;
-        case 7: if constexpr ((CM >> 7) & 1) ls.template load<7>(p, j, srow); break;
+        case 1: if constexpr ((CM >> 1) & 1) raw.template load<1>(p, j, srow); break;
+        case 2: if constexpr ((CM >> 2) & 1) raw.template load<2>(p, j, srow); break;
+        case 3: if constexpr ((CM >> 3) & 1) raw.template load<3>(p, j, srow); break;
+        case 4: if constexpr ((CM >> 4) & 1) raw.template load<4>(p, j, srow); break;
+        case 5: if constexpr ((CM >> 5) & 1) raw.template load<5>(p, j, srow); break;
+        case 6: if constexpr ((CM >> 6) & 1) raw.template load<6>(p, j, srow); break;
+        case 7: if constexpr ((CM >> 7) & 1) raw.template load<7>(p, j, srow); break;
         default: break;
     }
 }
 
+template <int CM, int NWMAX>
+__device__ __forceinline__ void prepare_any(MmSlice<NWMAX> &ls, int c, const MmRaw<NWMAX> &raw, int j) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) ls.template from_raw<1>(raw, j); break;
+        case 2: if constexpr ((CM >> 2) & 1) ls.template from_raw<2>(raw, j); break;
+        case 3: if constexpr ((CM >> 3) & 1) ls.template from_raw<3>(raw, j); break;
+        case 4: if constexpr ((CM >> 4) & 1) ls.template from_raw<4>(raw, j); break;
+        case 5: if constexpr ((CM >> 5) & 1) ls.template from_raw<5>(raw, j); break;
+        case 6: if constexpr ((CM >> 6) & 1) ls.template from_raw<6>(raw, j); break;
+        case 7: if constexpr ((CM >> 7) & 1) ls.template from_raw<7>(raw, j); break;
+        default: break;
+    }
+}
+
+// x' half-block tile in LDS: half sh of block b holds, per token, columns 128 kh + 64 sh + 8 c8 + (0..7) as
+// chunk c = 8 kh + c8 at position c ^ (t & 15) of the token's 256-byte row, so the 16-byte operand reads of
+// 16 consecutive tokens cover all 64 banks once.
+constexpr int kMmXsHalfs = kMmTok * 128;
+
+// Stage half sh of block b: instruction i of wave w fills token rows 4 (8 w + i) + (0..3); lane l lands at the
+// instruction's LDS base + 16 l (direct-to-LDS), i.e. row + (l >> 4), position l & 15.
+__device__ __forceinline__ void mm_stage(const MmJob &J, _Float16 *xb, int tok0, int b, int sh, int w, int lane) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 4 * (8 * w + i), t = row + (lane >> 4);
+        const int ts = min(tok0 + t, J.N - 1);   // rows past N repeat the last token (never written out)
+        const int c = (lane & 15) ^ (t & 15);
+        const _Float16 *src = J.xr + (size_t)ts * J.K + 256 * b + 128 * (c >> 3) + 64 * sh + 8 * (c & 7);
+        __builtin_amdgcn_global_load_lds(src, xb + row * 128, 16, 0, 0);
+    }
+}
+
+// issue the raw payload loads of the wave's two tiles at block b
+template <int CM, int NWMAX>
+__device__ __forceinline__ void mm_issue(const MmJob &J, MmRaw<NWMAX> (&raw)[2], int (&cl)[2], const int (&g)[2], int b, int j, int kh) {
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj) {
+        cl[tj] = 0;
+        if constexpr (CM == kMmCmC3) {   // the class-3-only path decodes every tile; zero weights through S = 0
+#pragma unroll
+            for (int i = 0; i < NWMAX; ++i) raw[tj].w[i] = 0;
+            raw[tj].s = 0;
+        }
+        if (g[tj] < J.ng) {
+            const uint32_t mt = as_const(J.M)[(size_t)g[tj] * J.nb + b];   // scalar load: not counted with the x' loads
+            cl[tj] = (int)(mt >> 29);
+            load_any<CM>(raw[tj], cl[tj], J.D + (mt & 0x1FFFFFFFu) + kh * nw_of(cl[tj]) * 32, j, J.S + (size_t)b * J.rows + 32 * g[tj]);
+        }
+    }
+}
+
+// decode the raw words into the slices the products read (after the loads have landed)
+template <int CM, int NWMAX>
+__device__ __forceinline__ void mm_prepare(MmSlice<NWMAX> (&ls)[2], const int (&cl)[2], const MmRaw<NWMAX> (&raw)[2], int j) {
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj) {
+        if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj], j);   // zero raw words, S = 0: zero weights
+        else prepare_any<CM>(ls[tj], cl[tj], raw[tj], j);
+    }
+}
+
+// The 8 MFMA steps of one half-block (steps s = 8 sh .. 8 sh + 7) from x' buffer xb.
+template <int CM, int NWMAX>
+__device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const MmSlice<NWMAX> (&ls)[2], const int (&cl)[2], const uint32_t *tab,
+                                        uint32_t bankbytes, int sh, int j, int kh, float16v (&acc)[4][2]) {
+    auto read_a = [&](int s8, half8v (&A)[4]) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+            A[ti] = *reinterpret_cast<const half8v *>(xb + (32 * ti + j) * 128 + 8 * ((8 * kh + s8) ^ (j & 15)));
+    };
+    if (CM == kMmCmC3 || (cl[0] == kMmMain && cl[1] == kMmMain)) {
+        // software-pipelined by one step: x' operands and table words of step s + 1 are read before the 8 MFMAs of
+        // step s, which then wait only for the fp16 conversion of their B operands
+        const half2v s2[2] = {{__builtin_bit_cast(_Float16, ls[0].s), __builtin_bit_cast(_Float16, ls[0].s)},
+                              {__builtin_bit_cast(_Float16, ls[1].s), __builtin_bit_cast(_Float16, ls[1].s)}};
+        auto lookups = [&](int s, uint32_t (&W)[2][2][3]) {
+#pragma unroll
+            for (int tj = 0; tj < 2; ++tj) {
+                const uint32_t hq = coset_bytes(ls[tj].H, bankbytes, s >> 1);
+                lookup_chunk<kMmMain>(ls[tj], tab, 2 * s, hq, W[tj][0]);
+                lookup_chunk<kMmMain>(ls[tj], tab, 2 * s + 1, hq, W[tj][1]);
+            }
+        };
+        half8v A[4];
+        uint32_t W[2][2][3];
+        read_a(0, A);
+        lookups(8 * sh, W);
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            half8v An[4];
+            uint32_t Wn[2][2][3];
+            if (s8 < 7) { read_a(s8 + 1, An); lookups(8 * sh + s8 + 1, Wn); }
+            half8v B[2];
+#pragma unroll
+            for (int tj = 0; tj < 2; ++tj) {
+                half2v a, b, c, d;
+                weights_chunk<kMmMain>(W[tj][0], s2[tj], a, b);
+                weights_chunk<kMmMain>(W[tj][1], s2[tj], c, d);
+                B[tj][0] = a.x; B[tj][1] = a.y; B[tj][2] = b.x; B[tj][3] = b.y;
+                B[tj][4] = c.x; B[tj][5] = c.y; B[tj][6] = d.x; B[tj][7] = d.y;
+            }
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
+            if (s8 < 7) {
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti) A[ti] = An[ti];
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int q = 0; q < 3; ++q) W[tj][u][q] = Wn[tj][u][q];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            half8v A[4], B[2];
+            read_a(s8, A);
+#pragma unroll
+            for (int tj = 0; tj < 2; ++tj) B[tj] = decode_any<CM>(ls[tj], cl[tj], tab, bankbytes, 8 * sh + s8);
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
+        }
+    }
+}
+
+// One 4-wave workgroup per CU (each wave: 64 weight rows x 128 tokens, 128 accumulator registers). K advances
+// by half-blocks; the x' of the next half-block and the next block's payload are in flight while the current
+// half-block is multiplied.
 template <int CM>
-__global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_mm(MmJob J) {
     constexpr int NWMAX = mm_nwmax(CM);
-    __shared__ uint32_t tab[512];                          // (f << 1 | h): A[f] + h c, bytes offset by 128
-    __shared__ __attribute__((aligned(16))) _Float16 xs[kMmTok * kMmXStride];   // x' part: [token][kh * 64 + 8 (s & 7) + i]
+    __shared__ uint32_t tab[kTabWords];   // first: LDS address 0, replicated coset table (bytes offset by 128)
+    __shared__ __attribute__((aligned(16))) _Float16 xs0[kMmXsHalfs];   // half 0 of a block
+    __shared__ __attribute__((aligned(16))) _Float16 xs1[kMmXsHalfs];   // half 1
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, kh = lane >> 5;
-    int wg = blockIdx.x;
-    const int ks = wg % J.nsplit; wg /= J.nsplit;
-    const int tn = wg % J.tiles_n, tm = wg / J.tiles_n;
-    for (int i = tid; i < 512; i += kMmThreads) tab[i] = J.a2[(i & 1) * 256 + (i >> 1)] ^ 0x80808080u;
+    const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
+    // Workgroups are dealt to the 8 XCDs round-robin (XCD = blockIdx % 8). Linear tile order is x'-slice-major
+    // (slice = token tile x K split, then row tile), and each XCD takes one contiguous run of it, so the
+    // workgroups that read one x' slice share an L2.
+    const int per = (J.tiles_m * J.tiles_n * J.nsplit + kXcds - 1) / kXcds;
+    const int lin = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (lin >= J.tiles_m * J.tiles_n * J.nsplit) return;
+    const int tm = lin % J.tiles_m, slice = lin / J.tiles_m;
+    const int ks = slice % J.nsplit, tn = slice / J.nsplit;
+    {
+        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
+        for (int i = tid; i < kTabWords / 4; i += kMmThreads) {
+            const int f = i >> 4, h = (i >> 3) & 1;
+            const uint32_t v = J.a2[h * 256 + f] ^ 0x80808080u;
+            t4[i] = make_uint4(v, v, v, v);
+        }
+    }
     const int tok0 = tn * kMmTok;
     const int b0 = ks * J.kper, b1 = min(J.nb, b0 + J.kper);
     int g[2];
@@ -244,76 +427,78 @@ void k_mm(MmJob J) {
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
         for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = float16v{};
-    // staging map: thread -> (token, kh): 128 contiguous bytes of x' per part
-    const int st_tok = tid >> 1, st_kh = tid & 1;
-    const bool st_ok = tok0 + st_tok < J.N;
-    const _Float16 *xsrc = J.xr + (size_t)(tok0 + st_tok) * J.K + 128 * st_kh;
+    MmSlice<NWMAX> ls[2];
+    MmRaw<NWMAX> raw[2];
+    int cl[2], ncl[2];
+    mm_stage(J, xs0, tok0, b0, 0, w, lane);
+    mm_issue<CM>(J, raw, cl, g, b0, j, kh);
+    __builtin_amdgcn_s_waitcnt(0);
+    mm_prepare<CM>(ls, cl, raw, j);
+    __syncthreads();   // table and the first half-block's x' are in LDS
+    // The two x' buffers are separate LDS objects named statically (half 0 always in xs0, half 1 in xs1), so
+    // the compiler can tell the operand reads from the in-flight direct-to-LDS writes and does not wait for them.
     for (int b = b0; b < b1; ++b) {
-        MmSlice<NWMAX> ls[2];
-        int cl[2];
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj) {
-            cl[tj] = 0;
-            if (g[tj] < J.ng) {
-                const uint32_t mt = J.M[(size_t)g[tj] * J.nb + b];
-                cl[tj] = (int)(mt >> 29);
-                const int nw = nw_of(cl[tj]);
-                load_any<CM>(ls[tj], cl[tj], J.D + (mt & 0x1FFFFFFFu) + kh * nw * 32, j, J.S + (size_t)b * J.rows + 32 * g[tj]);
-            }
+        mm_stage(J, xs1, tok0, b, 1, w, lane);
+        if (b + 1 < b1) mm_issue<CM>(J, raw, ncl, g, b + 1, j, kh);
+        mm_half<CM>(xs0, ls, cl, tab, bankbytes, 0, j, kh, acc);
+        __builtin_amdgcn_s_waitcnt(0);   // half 1 of b landed (and the next block's payload)
+        __syncthreads();
+        if (b + 1 < b1) mm_stage(J, xs0, tok0, b + 1, 0, w, lane);
+        mm_half<CM>(xs1, ls, cl, tab, bankbytes, 1, j, kh, acc);
+        __builtin_amdgcn_s_waitcnt(0);   // half 0 of b + 1 landed
+        if (b + 1 < b1) {
+            cl[0] = ncl[0]; cl[1] = ncl[1];
+            mm_prepare<CM>(ls, cl, raw, j);
         }
-#pragma unroll
-        for (int sh = 0; sh < 2; ++sh) {
-            uint4 v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = st_ok ? reinterpret_cast<const uint4 *>(xsrc + 256 * b + 64 * sh)[i] : make_uint4(0, 0, 0, 0);
-            __syncthreads();   // the previous part's reads are done
-#pragma unroll
-            for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(xs + st_tok * kMmXStride + 64 * st_kh + 8 * i) = v[i];
-            __syncthreads();
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8) {
-                const int s = 8 * sh + s8;
-                half8v A[4], B[2];
-#pragma unroll
-                for (int ti = 0; ti < 4; ++ti) A[ti] = *reinterpret_cast<const half8v *>(xs + (32 * ti + j) * kMmXStride + 64 * kh + 8 * s8);
-#pragma unroll
-                for (int tj = 0; tj < 2; ++tj) B[tj] = decode_any<CM>(ls[tj], cl[tj], tab, s);
-#pragma unroll
-                for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-                    for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
-            }
-        }
+        __syncthreads();
     }
-    // acc[ti][tj] lane l, reg q: token 32 ti + 8 (q >> 2) + 4 kh + (q & 3), sorted row 32 g[tj] + j
+    // acc[ti][tj] lane l, reg q: token 32 ti + 8 (q >> 2) + 4 kh + (q & 3), sorted row 32 g[tj] + j: 32 lanes
+    // store 32 consecutive rows of one token
+    float *dst = J.direct ? J.y : J.ws + (size_t)ks * J.N * J.rows;
+    const size_t ld = J.direct ? (size_t)J.ldy : (size_t)J.rows;
 #pragma unroll
     for (int tj = 0; tj < 2; ++tj) {
         if (g[tj] >= J.ng) continue;
         const int r = 32 * g[tj] + j;
-        const int ro = J.nsplit == 1 ? J.prm[r] : r;
-        float *dst = J.nsplit == 1 ? J.y : J.ws + (size_t)ks * J.N * J.rows;
-        const size_t ld = J.nsplit == 1 ? J.ldy : (size_t)J.rows;
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int tok = tok0 + 32 * ti + 8 * (q >> 2) + 4 * kh + (q & 3);
-                if (tok < J.N) dst[(size_t)tok * ld + ro] = acc[ti][tj][q];
+                if (tok < J.N) dst[(size_t)tok * ld + r] = acc[ti][tj][q];
             }
     }
 }
 
-// y[n][prm[r]] = sum over K splits in split order
-__global__ __launch_bounds__(256) void k_mm_reduce(const float *__restrict__ ws, int nsplit, int N, int rows, const int16_t *__restrict__ prm,
-                                                   float *__restrict__ y, size_t ldy) {
-    const int r = blockIdx.x * 256 + threadIdx.x, n = blockIdx.y;
-    if (r >= rows) return;
-    float s = 0.f;
-    for (int k = 0; k < nsplit; ++k) s += ws[((size_t)k * N + n) * rows + r];
-    y[(size_t)n * ldy + prm[r]] = s;
+// y[n][ro] = sum over K splits (split order) of the sorted planes at row pinv[ro], plus the clamp delta on the
+// original activations. One workgroup per token: the planes are read coalesced into LDS (sorted order), the
+// un-permute gathers from LDS, the stores are coalesced.
+template <typename XT>
+__global__ __launch_bounds__(1024) void k_mm_finish(const float *__restrict__ ws, int nsplit, int N, int rows, const int16_t *__restrict__ pinv,
+                                                    const int *__restrict__ cp, const uint16_t *__restrict__ cc, const float *__restrict__ cv,
+                                                    const XT *__restrict__ x, size_t ldx, float *__restrict__ y, size_t ldy) {
+    extern __shared__ float srow[];   // [rows]
+    const int n = blockIdx.x;
+    for (int r = threadIdx.x; r < rows; r += 1024) {
+        float v = 0.f;
+        for (int k = 0; k < nsplit; ++k) v += ws[((size_t)k * N + n) * rows + r];
+        srow[r] = v;
+    }
+    __syncthreads();
+    const XT *xr = x + (size_t)n * ldx;
+    for (int ro = threadIdx.x; ro < rows; ro += 1024) {
+        float v = srow[pinv[ro]];
+        for (int e = cp[ro]; e < cp[ro + 1]; ++e) {
+            float xv;
+            if constexpr (sizeof(XT) == 4) xv = xr[cc[e]];
+            else xv = bf16_to_float((uint16_t)xr[cc[e]]);
+            v += cv[e] * xv;
+        }
+        y[(size_t)n * ldy + ro] = v;
+    }
 }
 
-// clamp delta on the original activations: y[n][row] += sum_e cv[e] x[n][cc[e]] for the rows that have entries
+// clamp delta alone (direct output): y[n][row] += sum_e cv[e] x[n][cc[e]] for the rows that have entries
 template <typename XT>
 __global__ __launch_bounds__(256) void k_mm_delta(const int *__restrict__ drows, const int *__restrict__ cp, const uint16_t *__restrict__ cc,
                                                   const float *__restrict__ cv, const XT *__restrict__ x, size_t ldx, int N, float *__restrict__ y, size_t ldy) {
@@ -349,15 +534,22 @@ struct MmPlan {
     int tiles_m, tiles_n, nsplit, kper;
 };
 
+// One workgroup per CU. Estimated time = rounds of workgroups x blocks per workgroup x ~3.4 us (one block of a
+// 256 x 128 tile at about half the MFMA rate) + the sorted-plane traffic of k_mm_finish (written once, read
+// once, ~5 TB/s) when planes are used (K split, or rows to un-permute).
 static MmPlan mm_plan(const p8x_tensor *t, int N) {
     MmPlan p;
     p.tiles_m = (t->rows + kMmRows - 1) / kMmRows;
     p.tiles_n = (N + kMmTok - 1) / kMmTok;
-    const int base = p.tiles_m * p.tiles_n, slots = 2 * num_cus();
-    int ns = (slots + base - 1) / base;
-    ns = std::max(1, std::min(ns, t->nb / 4));
-    p.kper = (t->nb + ns - 1) / ns;
-    p.nsplit = (t->nb + p.kper - 1) / p.kper;
+    const long base = (long)p.tiles_m * p.tiles_n, slots = num_cus();
+    const double plane_us = 2.0 * 4.0 * N * t->rows / 5e6;
+    double best = -1.0;
+    p.nsplit = 1; p.kper = t->nb;
+    for (int ns = 1; ns <= std::min(t->nb, 16); ++ns) {
+        const int kper = (t->nb + ns - 1) / ns, nsr = (t->nb + kper - 1) / kper;
+        const double cost = (double)((base * nsr + slots - 1) / slots) * kper * 3.4 + ((nsr > 1 || !t->prm_identity) ? nsr * plane_us : 0.0);
+        if (best < 0 || cost < best) { best = cost; p.nsplit = nsr; p.kper = kper; }
+    }
     return p;
 }
 
@@ -365,27 +557,41 @@ int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_
     if (((uintptr_t)x & 15) || (ldx % 8)) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x must be 16-byte aligned with ldx %% 8 == 0");
     p8x_tensor *tw = const_cast<p8x_tensor *>(t);
     const MmPlan p = mm_plan(t, N);
+    const bool direct = p.nsplit == 1 && t->prm_identity;
     int rc;
     if ((rc = grow((void **)&tw->wx16, &tw->wx16_elems, (size_t)N * t->K * sizeof(_Float16), "p8x_mul_mat: activation workspace"))) return rc;
-    if (p.nsplit > 1 && (rc = grow((void **)&tw->wmm, &tw->wmm_bytes, (size_t)p.nsplit * N * t->rows * 4, "p8x_mul_mat: split workspace"))) return rc;
+    if (!direct && (rc = grow((void **)&tw->wmm, &tw->wmm_bytes, (size_t)p.nsplit * N * t->rows * 4, "p8x_mul_mat: output planes"))) return rc;
     _Float16 *xr = reinterpret_cast<_Float16 *>(tw->wx16);
     if (x_dtype == P8X_F32) hipLaunchKernelGGL(k_mm_act<float>, dim3(t->nb, N), dim3(64), 0, st, (const float *)x, ldx, t->ic, t->K, xr);
     else hipLaunchKernelGGL(k_mm_act<uint16_t>, dim3(t->nb, N), dim3(64), 0, st, (const uint16_t *)x, ldx, t->ic, t->K, xr);
     if ((rc = hip_check(hipGetLastError(), "k_mm_act launch"))) return rc;
     MmJob J;
-    J.M = t->M; J.S = t->S; J.D = t->D; J.prm = t->prm; J.xr = xr;
+    J.M = t->M; J.S = t->S; J.D = t->D; J.xr = xr;
     J.y = y; J.ldy = (unsigned)ldy; J.ws = tw->wmm; J.a2 = t->a2;
     J.N = N; J.rows = t->rows; J.K = t->K; J.nb = t->nb; J.ng = t->ng;
-    J.tiles_m = p.tiles_m; J.tiles_n = p.tiles_n; J.nsplit = p.nsplit; J.kper = p.kper;
-    const int grid = p.tiles_m * p.tiles_n * p.nsplit;
+    J.tiles_m = p.tiles_m; J.tiles_n = p.tiles_n; J.nsplit = p.nsplit; J.kper = p.kper; J.direct = direct;
+    const int grid = ((p.tiles_m * p.tiles_n * p.nsplit + kXcds - 1) / kXcds) * kXcds;
     bool only_c3 = true;
     for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) only_c3 = false;
     if (only_c3) hipLaunchKernelGGL(k_mm<kMmCmC3>, dim3(grid), dim3(kMmThreads), 0, st, J);
     else hipLaunchKernelGGL(k_mm<kMmCmAll>, dim3(grid), dim3(kMmThreads), 0, st, J);
     if ((rc = hip_check(hipGetLastError(), "k_mm launch"))) return rc;
-    if (p.nsplit > 1) {
-        hipLaunchKernelGGL(k_mm_reduce, dim3((t->rows + 255) / 256, N), dim3(256), 0, st, (const float *)tw->wmm, p.nsplit, N, t->rows, t->prm, y, ldy);
-        if ((rc = hip_check(hipGetLastError(), "k_mm_reduce launch"))) return rc;
+    if (!direct) {
+        const size_t lds = 4 * (size_t)t->rows;   // rows < 32768: at most 128 KB
+        static bool attr_set = false;
+        if (!attr_set) {
+            if ((rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<float>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")) ||
+                (rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")))
+                return rc;
+            attr_set = true;
+        }
+        if (x_dtype == P8X_F32)
+            hipLaunchKernelGGL(k_mm_finish<float>, dim3(N), dim3(1024), lds, st, (const float *)tw->wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
+                               (const float *)x, ldx, y, ldy);
+        else
+            hipLaunchKernelGGL(k_mm_finish<uint16_t>, dim3(N), dim3(1024), lds, st, (const float *)tw->wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
+                               (const uint16_t *)x, ldx, y, ldy);
+        return hip_check(hipGetLastError(), "k_mm_finish launch");
     }
     if (t->ndrows) {
         if (x_dtype == P8X_F32)

@@ -70,7 +70,7 @@ size_t p8x_need(size_t kbytes, int rows, int K, int nd) {
 }
 
 int p8x_probe(const void *slot, size_t n, int rows, int K) {
-    if (!slot || n < 4096) return 0;
+    if (!slot || n < kHeaderBytes + 256 + 32) return 0;
     uint32_t tr[8];
     memcpy(tr, (const uint8_t *)slot + n - 32, 32);
     return tr[0] == kMagic0 && tr[1] == kMagic1 && tr[4] == (uint32_t)rows && tr[5] == (uint32_t)K && tr[6] == kNS;
@@ -88,7 +88,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
     for (void *p : {(void *)t->owned, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
-                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->wx16, (void *)t->wmm})
+                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
 }
@@ -228,6 +228,14 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
     if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
+    {
+        std::vector<int16_t> pinv(rows);
+        bool ident = true;
+        for (int r = 0; r < rows; ++r) { pinv[prm[r]] = (int16_t)r; ident = ident && prm[r] == r; }
+        t->prm_identity = ident;
+        if ((rc = alloc((void **)&t->pinv, 2 * (size_t)rows, "pinv"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->pinv, pinv.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: pinv"))) return fail(rc);
+    }
     std::vector<int> drows;
     for (int r = 0; r < rows; ++r) if (cp[r + 1] > cp[r]) drows.push_back(r);
     t->ndrows = (int)drows.size();

@@ -21,6 +21,8 @@ struct p8x_tensor {
     const uint16_t *S = nullptr;
     const uint32_t *D = nullptr;
     const int16_t *prm = nullptr;
+    int16_t *pinv = nullptr;         // original row -> sorted row (built at prepare)
+    bool prm_identity = false;
     // device metadata built at prepare
     uint32_t *a2 = nullptr;          // [2][256]: A[f] + h c (bytewise), h-major
     float *ic = nullptr;             // sg / c per column [K]
