@@ -159,6 +159,21 @@ def measure_gemm(steps, N=512):
     return out
 
 
+def measured_traffic(step_bytes, layers, mix):
+    """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload
+    (counter KiB scaled by what the same counters read for a device copy of known size); None if absent or
+    taken on another workload."""
+    path = os.path.join(ROOT, "profiles", "k_gemv_llama8b_stream.json")
+    try:
+        with open(path) as f:
+            prof = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if prof.get("stream_bytes_per_step") != step_bytes or prof.get("layers") != layers or prof.get("class_mix") != mix:
+        return None, None
+    return int(prof["traffic_bytes_per_launch"]), "profiles/k_gemv_llama8b_stream.json"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +185,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM measurement")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -212,6 +229,16 @@ def main():
     achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
     log(f"stream: {ms_per_step * 1e3:.1f} us/step, GEMV kernel {gemv_ms * 1e3:.1f} us -> {achieved:.0f} GB/s")
 
+    if args.copy_calib:
+        n = args.copy_calib << 20
+        src, dst = p8x.DeviceBuffer(n), p8x.DeviceBuffer(n)
+        src.fill(1)
+        p8x.synchronize()
+        dst.copy_from(src)
+        p8x.synchronize()
+        src.free(); dst.free()
+        log(f"copy calibration: {n} bytes device to device")
+
     # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
     per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
@@ -219,6 +246,7 @@ def main():
     if not args.no_cpu and host0:
         threads = max(1, min(16, os.cpu_count() or 1))
         cpu = cpu_baseline(host0, args.cpu_seconds, threads)
+    traffic, traffic_src = measured_traffic(int(step_bytes), args.layers, args.mix)
     out = {
         "metric": "bs=1 dequant-GEMV HBM GB/s (% of peak), Llama-3.1-8B linear shapes",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -230,7 +258,7 @@ def main():
                    "stream_bytes_per_step": int(step_bytes), "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
                    "activations": "q8 per 128 columns (k_vr_qx_real semantics)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "k_gemv<1,Q8_128,class 3> (fused decode + GEMV, grouped launch)", "launches": args.steps,
                      "bytes_per_launch": int(step_bytes)},
         "cpu_baseline": cpu,

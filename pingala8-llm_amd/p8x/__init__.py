@@ -164,6 +164,11 @@ class DeviceBuffer:
     def fill(self, byte):
         hip_check(hip().hipMemset(self.ptr, byte, self.nbytes), "hipMemset")
 
+    def copy_from(self, other, nbytes=None):
+        """device-to-device copy (synchronous on the null stream)"""
+        n = min(self.nbytes, other.nbytes) if nbytes is None else int(nbytes)
+        hip_check(hip().hipMemcpy(self.ptr, other.ptr, n, D2D), "hipMemcpy D2D")
+
     @property
     def addr(self):
         return self.ptr.value
