@@ -174,6 +174,31 @@ def measured_traffic(step_bytes, layers, mix):
     return int(prof["traffic_bytes_per_launch"]), "profiles/k_gemv_llama8b_stream.json"
 
 
+def measure_dequant(steps):
+    """dequantize-to-fp16 (original rows, Hadamard applied) of one Llama FFN weight, 14336 x 4096: a write-bound
+    kernel; bytes = packed stream read + fp16 output written"""
+    rows, K = 14336, 4096
+    t = p8x.Tensor(p8x.synth_random(99, rows, K, nd=8), rows, K)
+    out = p8x.DeviceBuffer(2 * rows * K)
+    stream = p8x.Stream()
+    for _ in range(3):
+        t.dequantize_dev(p8x.F16, out, stream=stream)
+    stream.sync()
+    ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
+    for a, b in ev:
+        a.record(stream)
+        t.dequantize_dev(p8x.F16, out, stream=stream)
+        b.record(stream)
+    stream.sync()
+    ms = float(np.median([a.elapsed_ms(b) for a, b in ev]))
+    nbytes = t.stream_bytes + 2 * rows * K
+    res = {"tensor": f"{rows} x {K} -> fp16", "us_per_call": round(ms * 1e3, 1), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(nbytes)}
+    t.release()
+    log("dequantize to fp16:", json.dumps(res))
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +267,7 @@ def main():
     # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
     per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
+    deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
     cpu = None
     if not args.no_cpu and host0:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -264,6 +290,7 @@ def main():
         "cpu_baseline": cpu,
         "per_linear_launches": per_linear,
         "prompt_gemm": gemm,
+        "dequantize_f16": deq,
         "host_wall_s": round(wall, 3),
     }
     print(json.dumps(out), flush=True)

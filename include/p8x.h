@@ -72,7 +72,9 @@ int p8x_probe(const void *slot, size_t n, int rows, int K);
 
 /* Validate a slot and build its device-side metadata: vrc_init + vr_prepare_native (CPU.patch:240-275,
  * :4335-4390). on_device = 0: `slot` is host memory and is copied to a device allocation the handle owns;
- * on_device = 1: `slot` is device memory that must outlive the handle. The only allocating call. */
+ * on_device = 1: `slot` is device memory that must outlive the handle. Allocates everything the GEMV,
+ * decode and activation entry points use; only p8x_mul_mat (see p8x_mul_mat_reserve) and
+ * p8x_gemv_batch_create allocate later. */
 int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_tensor **out);
 void p8x_release(p8x_tensor *t);
 int p8x_tensor_info(const p8x_tensor *t, p8x_info *out);
@@ -106,9 +108,15 @@ int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int
  * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. */
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
-/* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T with X in
- * P8X_F32 or P8X_BF16. Weight tiles are decoded to fp16 in LDS and fed to MFMA with fp32 accumulation. */
+/* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
+ * X in P8X_F32 or P8X_BF16 (16-byte aligned, ldx % 8 == 0). The Hadamard rotation is applied to X (fp16 x'),
+ * weight tiles are decoded from the LDS coset table straight into fp16 MFMA operands (v S), fp32 accumulation,
+ * clamp delta on the original X. Uses the handle's workspace (x' and output planes, N-dependent): a call with
+ * a larger N than any before allocates it (synchronizing the device) unless p8x_mul_mat_reserve covered N. */
 int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream);
+/* No counterpart in the reference (ggml's pool allocator serves its temporaries): allocate the p8x_mul_mat
+ * workspace for up to n_max tokens at set-up, so later calls with N <= n_max allocate nothing. */
+int p8x_mul_mat_reserve(const p8x_tensor *t, int n_max);
 
 /* ---- grouped GEMV ------------------------------------------------------------------------------------- */
 /* No counterpart in the reference (ggml issues one mul_mat per graph node). A fixed list of independent

@@ -553,6 +553,19 @@ static MmPlan mm_plan(const p8x_tensor *t, int N) {
     return p;
 }
 
+int reserve_mul_mat(const p8x_tensor *t, int n_max) {
+    p8x_tensor *tw = const_cast<p8x_tensor *>(t);
+    int rc;
+    if ((rc = grow((void **)&tw->wx16, &tw->wx16_elems, (size_t)n_max * t->K * sizeof(_Float16), "p8x_mul_mat_reserve: activation workspace"))) return rc;
+    size_t planes = 0;   // the largest plane need over every N <= n_max (the split count depends on N)
+    for (int n = 1; n <= n_max; ++n) {
+        const MmPlan p = mm_plan(t, n);
+        if (!(p.nsplit == 1 && t->prm_identity)) planes = std::max(planes, (size_t)p.nsplit * n * t->rows * 4);
+    }
+    if (planes && (rc = grow((void **)&tw->wmm, &tw->wmm_bytes, planes, "p8x_mul_mat_reserve: output planes"))) return rc;
+    return P8X_OK;
+}
+
 int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st) {
     if (((uintptr_t)x & 15) || (ldx % 8)) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x must be 16-byte aligned with ldx %% 8 == 0");
     p8x_tensor *tw = const_cast<p8x_tensor *>(t);

@@ -325,6 +325,11 @@ int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, 
     return p8x_mul_mat_vec_act(t, P8X_ACT_Q8_128, x, ncols, ldx, y, ldy, stream);
 }
 
+int p8x_mul_mat_reserve(const p8x_tensor *t, int n_max) {
+    if (!t || n_max < 1) return set_error(P8X_ERR_ARG, "p8x_mul_mat_reserve: null tensor or n_max %d", n_max);
+    return reserve_mul_mat(t, n_max);
+}
+
 int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream) {
     if (!t || !x || !y) return set_error(P8X_ERR_ARG, "p8x_mul_mat: null pointer");
     if (x_dtype != P8X_F32 && x_dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x dtype %d", x_dtype);

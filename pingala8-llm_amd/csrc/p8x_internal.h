@@ -65,6 +65,7 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
 int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
 int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
 int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st);
+int reserve_mul_mat(const p8x_tensor *t, int n_max);
 
 int num_cus();
 

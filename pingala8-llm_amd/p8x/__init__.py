@@ -20,7 +20,7 @@ MAX_COLS = 8
 EXPORTS = [
     "p8x_version", "p8x_error_string", "p8x_last_error", "p8x_need", "p8x_probe", "p8x_prepare", "p8x_release",
     "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
-    "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_synth_random",
+    "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_mul_mat_reserve", "p8x_synth_random",
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
     "p8x_gemv_batch_release",
 ]
@@ -65,6 +65,7 @@ def lib():
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
+    L.p8x_mul_mat_reserve.argtypes = [vp, i]
     L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
     L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
     L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
@@ -304,6 +305,9 @@ class Tensor:
     def vec_dot_dev(self, act, q, d, y, ncols=1, x=None, ldx=None, ldy=None, stream=None):
         check(lib().p8x_vec_dot(self.h, act, _vp(q), _vp(d), ncols, _vp(x), ldx or self.K, _vp(y), ldy or self.rows,
                                 None, stream.h if stream else None), "p8x_vec_dot")
+
+    def mul_mat_reserve(self, n_max):
+        check(lib().p8x_mul_mat_reserve(self.h, n_max), "p8x_mul_mat_reserve")
 
     def mul_mat_dev(self, x, x_dtype, N, y, ldx=None, ldy=None, stream=None):
         check(lib().p8x_mul_mat(self.h, _vp(x), x_dtype, N, ldx or self.K, _vp(y), ldy or self.rows,

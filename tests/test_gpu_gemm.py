@@ -96,3 +96,15 @@ def test_gemm_ffn_512(rows, K):
     tok = np.array([0, 1, 31, 32, 127, 128, 200, 255, 256, 383, 500, 511])
     assert rel_l2(Y[tok], reference(orc, bf16_to_f32(Xb), tok)) < REL_L2
     assert np.isfinite(Y).all()
+
+
+def test_gemm_reserve_then_smaller_calls():
+    """workspace reserved for 300 tokens serves calls with 300 and fewer tokens, results unchanged"""
+    rows, K = 512, 4096
+    slot = p8x.synth_random(21, rows, K, nd=2)
+    t = p8x.Tensor(slot, rows, K)
+    t.mul_mat_reserve(300)
+    orc = O.Oracle(slot, rows, K)
+    for N in (300, 17, 128):
+        X = np.random.default_rng(N).standard_normal((N, K)).astype(np.float32)
+        assert rel_l2(t.mul_mat(X), reference(orc, X)) < REL_L2
