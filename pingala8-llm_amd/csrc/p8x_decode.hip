@@ -5,7 +5,11 @@
 // t = FWHT256(v * S[b][r]) with butterflies h = 1..128 then * 0.0625, t *= ic, row prm[r], + delta.
 // A lane owns one half-row (128 values) in registers: stages h = 1..64 stay in the lane, stage 128 pairs
 // lane j with lane j + 32. Every output is the same a + b / a - b of the same operands as the reference,
-// so the f32 result is bit-identical (no contraction: built with -ffp-contract=off).
+// so the f32 result is bit-identical (no contraction: built with -ffp-contract=off); f16/bf16 are the
+// hardware round-to-nearest-even conversions of that f32.
+//
+// Each wave walks tiles with the next tile's payload already in flight (rotated loads into registers), so
+// the decode of one tile overlaps the memory latency of the next.
 #include <hip/hip_runtime.h>
 
 #include "p8x_internal.h"
@@ -15,6 +19,7 @@ namespace p8x {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = 64 * kDecWaves;
+constexpr int kDecNW = 24;   // raw words held per lane: the largest class
 
 struct DecodeArgs {
     const uint32_t *M; const uint16_t *S; const uint32_t *D; const uint32_t *a2; const int16_t *prm;
@@ -24,97 +29,110 @@ struct DecodeArgs {
     size_t nt;
 };
 
-// exact ints of lane-slice (class C) -> v[128] (chunk-major, element e)
-template <int C>
-__device__ __forceinline__ void lane_ints(const uint32_t *tab, const uint32_t *__restrict__ payload, int hs, int j,
-                                          uint32_t bankbytes, int (&v)[128]) {
-    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C), NW = nw_of(C);
-    LaneSlice<C> ls;
-    ls.load(payload + hs * NW * 32, j);
-    ls.prepare(bankbytes);
+// exact ints of a decoded lane-slice of class C -> v[128] (chunk-major, element e), as float times sc
+// (FP = true) or as ints (FP = false, written through the float array's bits)
+template <int C, bool FP>
+__device__ __forceinline__ void lane_values(const AnySlice<kDecNW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
+    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
-        const uint32_t hq = ls.group_bytes(t >> 2);
-        const uint32_t w0 = lds_word(tab, ls.template addr<0>(t, hq));
+        const uint32_t hq = coset_bytes(ls.H, bankbytes, t >> 2);
+        const uint32_t w0 = lds_word(tab, ls.template addr<C, 0>(t, hq));
         uint32_t w1 = 0, w2 = 0;
-        if constexpr (NST > 1) w1 = lds_word(tab, ls.template addr<1>(t, hq));
-        if constexpr (NST > 2) w2 = lds_word(tab, ls.template addr<2>(t, hq));
+        if constexpr (NST > 1) w1 = lds_word(tab, ls.template addr<C, 1>(t, hq));
+        if constexpr (NST > 2) w2 = lds_word(tab, ls.template addr<C, 2>(t, hq));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             int x = sext8(w0, e) * (1 << SH1);
             if constexpr (NST > 1) x += sext8(w1, e) * (1 << SH2);
             if constexpr (NST > 2) x += sext8(w2, e);
-            v[4 * t + e] = x;
+            v[4 * t + e] = FP ? (float)x * sc : __builtin_bit_cast(float, x);
         }
     }
 }
 
-__device__ __forceinline__ void lane_ints_any(int c, const uint32_t *tab, const uint32_t *__restrict__ payload, int hs, int j,
-                                              uint32_t bankbytes, int (&v)[128]) {
+template <bool FP>
+__device__ __forceinline__ void lane_values_any(int c, const AnySlice<kDecNW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
     switch (c) {
-        case 1: lane_ints<1>(tab, payload, hs, j, bankbytes, v); break;
-        case 2: lane_ints<2>(tab, payload, hs, j, bankbytes, v); break;
-        case 3: lane_ints<3>(tab, payload, hs, j, bankbytes, v); break;
-        case 4: lane_ints<4>(tab, payload, hs, j, bankbytes, v); break;
-        case 5: lane_ints<5>(tab, payload, hs, j, bankbytes, v); break;
-        case 6: lane_ints<6>(tab, payload, hs, j, bankbytes, v); break;
-        case 7: lane_ints<7>(tab, payload, hs, j, bankbytes, v); break;
+        case 1: lane_values<1, FP>(ls, tab, bankbytes, sc, v); break;
+        case 2: lane_values<2, FP>(ls, tab, bankbytes, sc, v); break;
+        case 3: lane_values<3, FP>(ls, tab, bankbytes, sc, v); break;
+        case 4: lane_values<4, FP>(ls, tab, bankbytes, sc, v); break;
+        case 5: lane_values<5, FP>(ls, tab, bankbytes, sc, v); break;
+        case 6: lane_values<6, FP>(ls, tab, bankbytes, sc, v); break;
+        case 7: lane_values<7, FP>(ls, tab, bankbytes, sc, v); break;
         default:
 #pragma unroll
-            for (int i = 0; i < 128; ++i) v[i] = 0;
+            for (int i = 0; i < 128; ++i) v[i] = 0.f;   // class 0: zero weights (0.0f and int 0 share bits)
             break;
+    }
+}
+
+// The wave's walk over tiles tile0, tile0 + stride, ...: body(tile, g, b, class, slice) runs on each tile
+// while the next tile's raw payload loads.
+template <typename Body>
+__device__ __forceinline__ void walk_tiles(const DecodeArgs &a, size_t tile0, size_t stride, int hs, int j, Body body) {
+    if (tile0 >= a.nt) return;
+    constexpr int CM = 0xFE;
+    AnyRaw<kDecNW> raw;
+    auto issue = [&](size_t tile, int &c) {
+        const int g = (int)(tile / a.nb), b = (int)(tile % a.nb);
+        const uint32_t mt = a.M[tile];
+        c = (int)(mt >> 29);
+        load_any<CM>(raw, c, a.D + (mt & 0x1FFFFFFFu) + hs * nw_of(c) * 32, j, a.S + (size_t)b * a.rows + 32 * g);
+    };
+    int c;
+    issue(tile0, c);
+    for (size_t tile = tile0; tile < a.nt; tile += stride) {
+        AnySlice<kDecNW> ls;
+        prepare_any<CM>(ls, c, raw, j);   // consumes the words of this tile
+        const int cur = c;
+        if (tile + stride < a.nt) issue(tile + stride, c);   // the next tile's words load during this tile
+        body(tile, (int)(tile / a.nb), (int)(tile % a.nb), cur, ls);
     }
 }
 
 // DT: P8X_I16 (exact ints) or P8X_F32 (int * S), sorted rows, rotated domain
 template <int DT>
-__global__ __launch_bounds__(kDecThreads) void k_decode_rotated(const DecodeArgs a) {
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_decode_rotated(const DecodeArgs a) {
     __shared__ __align__(16) uint32_t tab[kTabWords];
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hs = lane >> 5, j = lane & 31;
     const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
     build_coset_table(tab, a.a2, tid, kDecThreads);
     __syncthreads();
-    for (size_t tile = (size_t)blockIdx.x * kDecWaves + w; tile < a.nt; tile += (size_t)gridDim.x * kDecWaves) {
-        const int g = (int)(tile / a.nb), b = (int)(tile % a.nb);
-        const uint32_t mt = a.M[tile];
-        int v[128];
-        lane_ints_any((int)(mt >> 29), tab, a.D + (mt & 0x1FFFFFFFu), hs, j, bankbytes, v);
+    walk_tiles(a, (size_t)blockIdx.x * kDecWaves + w, (size_t)gridDim.x * kDecWaves, hs, j,
+               [&](size_t, int g, int b, int c, const AnySlice<kDecNW> &ls) {
+        float v[128];
+        lane_values_any<DT == P8X_F32>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
         const size_t o = (size_t)(32 * g + j) * a.ld + 256 * b + 128 * hs;
         if constexpr (DT == P8X_I16) {
             uint2 *dst = reinterpret_cast<uint2 *>((int16_t *)a.out + o);
 #pragma unroll
-            for (int t = 0; t < 32; ++t)
-                dst[t] = make_uint2((uint32_t)(uint16_t)v[4 * t] | ((uint32_t)(uint16_t)v[4 * t + 1] << 16),
-                                    (uint32_t)(uint16_t)v[4 * t + 2] | ((uint32_t)(uint16_t)v[4 * t + 3] << 16));
+            for (int t = 0; t < 32; ++t) {
+                const int *vi = reinterpret_cast<const int *>(v) + 4 * t;
+                dst[t] = make_uint2((uint32_t)(uint16_t)vi[0] | ((uint32_t)(uint16_t)vi[1] << 16),
+                                    (uint32_t)(uint16_t)vi[2] | ((uint32_t)(uint16_t)vi[3] << 16));
+            }
         } else {
-            const float sc = half_to_float(a.S[(size_t)b * a.rows + 32 * g + j]);
             float4 *dst = reinterpret_cast<float4 *>((float *)a.out + o);
 #pragma unroll
-            for (int t = 0; t < 32; ++t)
-                dst[t] = make_float4((float)v[4 * t] * sc, (float)v[4 * t + 1] * sc, (float)v[4 * t + 2] * sc, (float)v[4 * t + 3] * sc);
+            for (int t = 0; t < 32; ++t) dst[t] = make_float4(v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]);
         }
-    }
+    });
 }
 
 // original-domain weights, DT = P8X_F32 / P8X_F16 / P8X_BF16
 template <int DT>
-__global__ __launch_bounds__(kDecThreads) void k_dequant(const DecodeArgs a) {
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_dequant(const DecodeArgs a) {
     __shared__ __align__(16) uint32_t tab[kTabWords];
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hs = lane >> 5, j = lane & 31;
     const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
     build_coset_table(tab, a.a2, tid, kDecThreads);
     __syncthreads();
-    for (size_t tile = (size_t)blockIdx.x * kDecWaves + w; tile < a.nt; tile += (size_t)gridDim.x * kDecWaves) {
-        const int g = (int)(tile / a.nb), b = (int)(tile % a.nb);
-        const uint32_t mt = a.M[tile];
+    walk_tiles(a, (size_t)blockIdx.x * kDecWaves + w, (size_t)gridDim.x * kDecWaves, hs, j,
+               [&](size_t, int g, int b, int c, const AnySlice<kDecNW> &ls) {
         float v[128];
-        {
-            int vi[128];
-            lane_ints_any((int)(mt >> 29), tab, a.D + (mt & 0x1FFFFFFFu), hs, j, bankbytes, vi);
-            const float sc = half_to_float(a.S[(size_t)b * a.rows + 32 * g + j]);
-#pragma unroll
-            for (int i = 0; i < 128; ++i) v[i] = (float)vi[i] * sc;
-        }
+        lane_values_any<true>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
 #pragma unroll
         for (int h = 1; h < 128; h <<= 1)
 #pragma unroll
@@ -152,11 +170,14 @@ __global__ __launch_bounds__(kDecThreads) void k_dequant(const DecodeArgs a) {
             for (int t = 0; t < 32; ++t) {
                 uint16_t hv[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) hv[e] = DT == P8X_F16 ? float_to_half(v[4 * t + e]) : float_to_bf16(v[4 * t + e]);
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (DT == P8X_F16) hv[e] = __builtin_bit_cast(uint16_t, (_Float16)v[4 * t + e]);   // v_cvt_f16_f32, RNE
+                    else hv[e] = __builtin_bit_cast(uint16_t, (__bf16)v[4 * t + e]);                            // v_cvt_pk_bf16_f32, RNE
+                }
                 dst[t] = make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
             }
         }
-    }
+    });
 }
 
 static DecodeArgs decode_args(const p8x_tensor *t, void *out, size_t ld) {
@@ -168,6 +189,7 @@ static DecodeArgs decode_args(const p8x_tensor *t, void *out, size_t ld) {
     return a;
 }
 
+// two 4-wave workgroups per CU (the 64 KB table each), persistent
 static int decode_grid(const p8x_tensor *t) {
     const size_t wgs = (t->nt + kDecWaves - 1) / kDecWaves;
     return (int)std::min<size_t>(wgs, (size_t)num_cus() * 2);

@@ -82,107 +82,13 @@ struct MmJob {
     int tiles_m, tiles_n, nsplit, kper, direct;
 };
 
-// Raw payload words of one lane-slice (any class up to NWMAX words) in rotated load order, plus the lane's
-// fp16 row scale: issued a block ahead, decoded into an MmSlice after the current block's products.
-template <int NWMAX>
-struct MmRaw {
-    uint32_t w[NWMAX];
-    uint16_t s;
-
-    template <int W, int WB>
-    __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
-        const int wr = (((32 - j) & 31) * W) >> 5;
-#pragma unroll
-        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
-    }
-    template <int C>
-    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j, const uint16_t *__restrict__ srow) {
-        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
-        if constexpr (W1 == 8) region<8, 0>(p, j);
-        else {
-            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
-            region<W1 - 1, 1>(p, j);
-        }
-        if constexpr (W2 > 0) region<W2, W1>(p, j);
-        if constexpr (W3 > 0) region<W3, W1 + W2>(p, j);
-        s = srow[j];
-    }
-};
-
-// Rotated lane-slice words of any class up to NWMAX words (chunk order after the per-lane rotation), plus the
-// coset bits in chunk order. Region layout as stored: [label word if W1 < 8] stage-1 fields, stage 2, stage 3.
-template <int NWMAX>
-struct MmSlice {
-    uint32_t r[NWMAX];
-    uint32_t H;
-    uint16_t s;
-
-    template <int W, int WB>
-    __device__ __forceinline__ void rotate(const MmRaw<NWMAX> &raw, int j) {
-        const int br = (((32 - j) & 31) * W) & 31;
-#pragma unroll
-        for (int i = 0; i < W; ++i) r[WB + i] = __builtin_amdgcn_alignbit(raw.w[WB + (i + 1) % W], raw.w[WB + i], br);
-    }
-    template <int C>
-    __device__ __forceinline__ void from_raw(const MmRaw<NWMAX> &raw, int j) {
-        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
-        uint32_t z;
-        if constexpr (W1 == 8) {
-            rotate<8, 0>(raw, j);
-            uint32_t R[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) R[i] = r[i];
-            z = labels_from_bytes(R);
-        } else {
-            r[0] = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
-            z = r[0];
-            rotate<W1 - 1, 1>(raw, j);
-        }
-        if constexpr (W2 > 0) rotate<W2, W1>(raw, j);
-        if constexpr (W3 > 0) rotate<W3, W1 + W2>(raw, j);
-        H = trellis_coset_bits(z);
-        s = raw.s;
-    }
-
-    // LDS byte address of stage S at chunk t in the replicated table (p8x_lane.h layout: (f << 8) | (h << 7) |
-    // (bank << 2)); hq = coset_bytes(H, bankbytes, t >> 2) holds the (h << 7) | (bank << 2) byte of each chunk
-    template <int C, int S>
-    __device__ __forceinline__ uint32_t addr(int t, uint32_t hq) const {
-        constexpr int W1 = w1_of(C), W2 = w2_of(C);
-        const int e = t & 3;
-        if constexpr (S == 0) {
-            if constexpr (W1 == 8) return __builtin_amdgcn_perm(r[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
-            else {
-                constexpr int W = W1 - 1;
-                const int pos = W * t, wi = 1 + (pos >> 5), bb = pos & 31;
-                uint32_t f;
-                if (bb + W <= 32) f = __builtin_amdgcn_ubfe(r[wi], bb, W);
-                else f = __builtin_amdgcn_alignbit(r[1 + (wi % W)], r[wi], bb) & ((1u << W) - 1u);
-                f |= __builtin_amdgcn_ubfe(r[0], t, 1) << W;
-                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
-            }
-        } else if constexpr (S == 1) {
-            if constexpr (W2 == 8) return __builtin_amdgcn_perm(r[W1 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
-            else {
-                const int pos = W2 * t, wi = pos >> 5, bb = pos & 31;
-                uint32_t f;
-                if (bb + W2 <= 32) f = __builtin_amdgcn_ubfe(r[W1 + wi], bb, W2);
-                else f = __builtin_amdgcn_alignbit(r[W1 + (wi + 1) % W2], r[W1 + wi], bb) & ((1u << W2) - 1u);
-                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
-            }
-        } else {
-            return __builtin_amdgcn_perm(r[W1 + W2 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
-        }
-    }
-};
-
 // offset-binary int8x4 (v + 128 per byte) -> two fp16 pairs holding 1152 + v exactly
 __device__ __forceinline__ half2v ob_lo(uint32_t w) { return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)); }
 __device__ __forceinline__ half2v ob_hi(uint32_t w) { return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)); }
 
 // LDS words of chunk t, all stages (table bytes are A[f] + h c offset by 128)
 template <int C, int NWMAX>
-__device__ __forceinline__ void lookup_chunk(const MmSlice<NWMAX> &ls, const uint32_t *tab, int t, uint32_t hq, uint32_t (&w)[3]) {
+__device__ __forceinline__ void lookup_chunk(const AnySlice<NWMAX> &ls, const uint32_t *tab, int t, uint32_t hq, uint32_t (&w)[3]) {
     constexpr int NST = nstage_of(C);
     w[0] = lds_word(tab, ls.template addr<C, 0>(t, hq));
     if constexpr (NST > 1) w[1] = lds_word(tab, ls.template addr<C, 1>(t, hq));
@@ -208,7 +114,7 @@ __device__ __forceinline__ void weights_chunk(const uint32_t (&w)[3], half2v s2,
 }
 
 template <int C, int NWMAX>
-__device__ __forceinline__ half8v decode_pair(const MmSlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes, int s) {
+__device__ __forceinline__ half8v decode_pair(const AnySlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes, int s) {
     const half2v s2 = {__builtin_bit_cast(_Float16, ls.s), __builtin_bit_cast(_Float16, ls.s)};
     const uint32_t hq = coset_bytes(ls.H, bankbytes, s >> 1);
     uint32_t w0[3], w1[3];
@@ -228,7 +134,7 @@ constexpr int kMmMain = 3;   // the class with a branch-free path in every insta
 __host__ __device__ constexpr int mm_nwmax(int cm) { return cm == kMmCmC3 ? 8 : 24; }
 
 template <int CM, int NWMAX>
-__device__ __forceinline__ half8v decode_any(const MmSlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
+__device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
     switch (c) {
         case 1: if constexpr ((CM >> 1) & 1) return decode_pair<1>(ls, tab, bankbytes, s); break;
         case 2: if constexpr ((CM >> 2) & 1) return decode_pair<2>(ls, tab, bankbytes, s); break;
@@ -240,34 +146,6 @@ __device__ __forceinline__ half8v decode_any(const MmSlice<NWMAX> &ls, int c, co
         default: break;
     }
     return half8v{};
-}
-
-template <int CM, int NWMAX>
-__device__ __forceinline__ void load_any(MmRaw<NWMAX> &raw, int c, const uint32_t *p, int j, const uint16_t *srow) {
-    switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) raw.template load<1>(p, j, srow); break;
-        case 2: if constexpr ((CM >> 2) & 1) raw.template load<2>(p, j, srow); break;
-        case 3: if constexpr ((CM >> 3) & 1) raw.template load<3>(p, j, srow); break;
-        case 4: if constexpr ((CM >> 4) & 1) raw.template load<4>(p, j, srow); break;
-        case 5: if constexpr ((CM >> 5) & 1) raw.template load<5>(p, j, srow); break;
-        case 6: if constexpr ((CM >> 6) & 1) raw.template load<6>(p, j, srow); break;
-        case 7: if constexpr ((CM >> 7) & 1) raw.template load<7>(p, j, srow); break;
-        default: break;
-    }
-}
-
-template <int CM, int NWMAX>
-__device__ __forceinline__ void prepare_any(MmSlice<NWMAX> &ls, int c, const MmRaw<NWMAX> &raw, int j) {
-    switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) ls.template from_raw<1>(raw, j); break;
-        case 2: if constexpr ((CM >> 2) & 1) ls.template from_raw<2>(raw, j); break;
-        case 3: if constexpr ((CM >> 3) & 1) ls.template from_raw<3>(raw, j); break;
-        case 4: if constexpr ((CM >> 4) & 1) ls.template from_raw<4>(raw, j); break;
-        case 5: if constexpr ((CM >> 5) & 1) ls.template from_raw<5>(raw, j); break;
-        case 6: if constexpr ((CM >> 6) & 1) ls.template from_raw<6>(raw, j); break;
-        case 7: if constexpr ((CM >> 7) & 1) ls.template from_raw<7>(raw, j); break;
-        default: break;
-    }
 }
 
 // x' half-block tile in LDS: half sh of block b holds, per token, columns 128 kh + 64 sh + 8 c8 + (0..7) as
@@ -290,7 +168,7 @@ __device__ __forceinline__ void mm_stage(const MmJob &J, _Float16 *xb, int tok0,
 
 // issue the raw payload loads of the wave's two tiles at block b
 template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_issue(const MmJob &J, MmRaw<NWMAX> (&raw)[2], int (&cl)[2], const int (&g)[2], int b, int j, int kh) {
+__device__ __forceinline__ void mm_issue(const MmJob &J, AnyRaw<NWMAX> (&raw)[2], int (&cl)[2], const int (&g)[2], int b, int j, int kh) {
 #pragma unroll
     for (int tj = 0; tj < 2; ++tj) {
         cl[tj] = 0;
@@ -309,7 +187,7 @@ __device__ __forceinline__ void mm_issue(const MmJob &J, MmRaw<NWMAX> (&raw)[2],
 
 // decode the raw words into the slices the products read (after the loads have landed)
 template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_prepare(MmSlice<NWMAX> (&ls)[2], const int (&cl)[2], const MmRaw<NWMAX> (&raw)[2], int j) {
+__device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const AnyRaw<NWMAX> (&raw)[2], int j) {
 #pragma unroll
     for (int tj = 0; tj < 2; ++tj) {
         if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj], j);   // zero raw words, S = 0: zero weights
@@ -319,7 +197,7 @@ __device__ __forceinline__ void mm_prepare(MmSlice<NWMAX> (&ls)[2], const int (&
 
 // The 8 MFMA steps of one half-block (steps s = 8 sh .. 8 sh + 7) from x' buffer xb.
 template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const MmSlice<NWMAX> (&ls)[2], const int (&cl)[2], const uint32_t *tab,
+__device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const uint32_t *tab,
                                         uint32_t bankbytes, int sh, int j, int kh, float16v (&acc)[4][2]) {
     auto read_a = [&](int s8, half8v (&A)[4]) {
 #pragma unroll
@@ -427,8 +305,8 @@ void k_mm(MmJob J) {
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
         for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = float16v{};
-    MmSlice<NWMAX> ls[2];
-    MmRaw<NWMAX> raw[2];
+    AnySlice<NWMAX> ls[2];
+    AnyRaw<NWMAX> raw[2];
     int cl[2], ncl[2];
     mm_stage(J, xs0, tok0, b0, 0, w, lane);
     mm_issue<CM>(J, raw, cl, g, b0, j, kh);

@@ -295,6 +295,130 @@ struct StepSlice {
     }
 };
 
+// ------------------------------------------------------------------------------------------------ any class
+// Raw payload words of one lane-slice (any class up to NWMAX words) in rotated load order, plus the lane's
+// fp16 row scale: issued ahead of use, then decoded into an AnySlice (per-lane rotation, labels, trellis).
+template <int NWMAX>
+struct AnyRaw {
+    uint32_t w[NWMAX];
+    uint16_t s;
+
+    template <int W, int WB>
+    __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
+        const int wr = (((32 - j) & 31) * W) >> 5;
+#pragma unroll
+        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
+    }
+    template <int C>
+    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j, const uint16_t *__restrict__ srow) {
+        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
+        if constexpr (W1 == 8) region<8, 0>(p, j);
+        else {
+            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
+            region<W1 - 1, 1>(p, j);
+        }
+        if constexpr (W2 > 0) region<W2, W1>(p, j);
+        if constexpr (W3 > 0) region<W3, W1 + W2>(p, j);
+        s = srow[j];
+    }
+};
+
+// Rotated lane-slice words of any class up to NWMAX words (chunk order after the per-lane rotation), plus the
+// coset bits in chunk order. Region layout as stored: [label word if W1 < 8] stage-1 fields, stage 2, stage 3.
+template <int NWMAX>
+struct AnySlice {
+    uint32_t r[NWMAX];
+    uint32_t H;
+    uint16_t s;
+
+    template <int W, int WB>
+    __device__ __forceinline__ void rotate(const AnyRaw<NWMAX> &raw, int j) {
+        const int br = (((32 - j) & 31) * W) & 31;
+#pragma unroll
+        for (int i = 0; i < W; ++i) r[WB + i] = __builtin_amdgcn_alignbit(raw.w[WB + (i + 1) % W], raw.w[WB + i], br);
+    }
+    template <int C>
+    __device__ __forceinline__ void from_raw(const AnyRaw<NWMAX> &raw, int j) {
+        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
+        uint32_t z;
+        if constexpr (W1 == 8) {
+            rotate<8, 0>(raw, j);
+            uint32_t R[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) R[i] = r[i];
+            z = labels_from_bytes(R);
+        } else {
+            r[0] = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
+            z = r[0];
+            rotate<W1 - 1, 1>(raw, j);
+        }
+        if constexpr (W2 > 0) rotate<W2, W1>(raw, j);
+        if constexpr (W3 > 0) rotate<W3, W1 + W2>(raw, j);
+        H = trellis_coset_bits(z);
+        s = raw.s;
+    }
+
+    // LDS byte address of stage S at chunk t in the replicated table (p8x_lane.h layout: (f << 8) | (h << 7) |
+    // (bank << 2)); hq = coset_bytes(H, bankbytes, t >> 2) holds the (h << 7) | (bank << 2) byte of each chunk
+    template <int C, int S>
+    __device__ __forceinline__ uint32_t addr(int t, uint32_t hq) const {
+        constexpr int W1 = w1_of(C), W2 = w2_of(C);
+        const int e = t & 3;
+        if constexpr (S == 0) {
+            if constexpr (W1 == 8) return __builtin_amdgcn_perm(r[t >> 2], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else {
+                constexpr int W = W1 - 1;
+                const int pos = W * t, wi = 1 + (pos >> 5), bb = pos & 31;
+                uint32_t f;
+                if (bb + W <= 32) f = __builtin_amdgcn_ubfe(r[wi], bb, W);
+                else f = __builtin_amdgcn_alignbit(r[1 + (wi % W)], r[wi], bb) & ((1u << W) - 1u);
+                f |= __builtin_amdgcn_ubfe(r[0], t, 1) << W;
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
+            }
+        } else if constexpr (S == 1) {
+            if constexpr (W2 == 8) return __builtin_amdgcn_perm(r[W1 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+            else {
+                const int pos = W2 * t, wi = pos >> 5, bb = pos & 31;
+                uint32_t f;
+                if (bb + W2 <= 32) f = __builtin_amdgcn_ubfe(r[W1 + wi], bb, W2);
+                else f = __builtin_amdgcn_alignbit(r[W1 + (wi + 1) % W2], r[W1 + wi], bb) & ((1u << W2) - 1u);
+                return __builtin_amdgcn_perm(f, hq, 0x0c0c0400u | e);
+            }
+        } else {
+            return __builtin_amdgcn_perm(r[W1 + W2 + (t >> 2)], hq, 0x0c0c0000u | ((4u + e) << 8) | e);
+        }
+    }
+};
+
+// class dispatch over the classes of mask CM (uniform per wave: the tile's class)
+template <int CM, int NWMAX>
+__device__ __forceinline__ void load_any(AnyRaw<NWMAX> &raw, int c, const uint32_t *p, int j, const uint16_t *srow) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) raw.template load<1>(p, j, srow); break;
+        case 2: if constexpr ((CM >> 2) & 1) raw.template load<2>(p, j, srow); break;
+        case 3: if constexpr ((CM >> 3) & 1) raw.template load<3>(p, j, srow); break;
+        case 4: if constexpr ((CM >> 4) & 1) raw.template load<4>(p, j, srow); break;
+        case 5: if constexpr ((CM >> 5) & 1) raw.template load<5>(p, j, srow); break;
+        case 6: if constexpr ((CM >> 6) & 1) raw.template load<6>(p, j, srow); break;
+        case 7: if constexpr ((CM >> 7) & 1) raw.template load<7>(p, j, srow); break;
+        default: break;
+    }
+}
+
+template <int CM, int NWMAX>
+__device__ __forceinline__ void prepare_any(AnySlice<NWMAX> &ls, int c, const AnyRaw<NWMAX> &raw, int j) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) ls.template from_raw<1>(raw, j); break;
+        case 2: if constexpr ((CM >> 2) & 1) ls.template from_raw<2>(raw, j); break;
+        case 3: if constexpr ((CM >> 3) & 1) ls.template from_raw<3>(raw, j); break;
+        case 4: if constexpr ((CM >> 4) & 1) ls.template from_raw<4>(raw, j); break;
+        case 5: if constexpr ((CM >> 5) & 1) ls.template from_raw<5>(raw, j); break;
+        case 6: if constexpr ((CM >> 6) & 1) ls.template from_raw<6>(raw, j); break;
+        case 7: if constexpr ((CM >> 7) & 1) ls.template from_raw<7>(raw, j); break;
+        default: break;
+    }
+}
+
 __device__ __forceinline__ int sext8(uint32_t w, int e) { return (int)(int8_t)(w >> (8 * e)); }
 
 }  // namespace p8x
