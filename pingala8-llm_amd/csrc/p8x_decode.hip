@@ -19,7 +19,9 @@ namespace p8x {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = 64 * kDecWaves;
-constexpr int kDecNW = 24;   // raw words held per lane: the largest class
+constexpr int kStgRowWords = 132;   // dequant staging row: 512 bytes + 16 bytes of padding
+// raw words held per lane: the largest class of the instantiation's class set
+__host__ __device__ constexpr int dec_nw(int cm) { return cm == (1 << 3) ? 8 : 24; }
 
 struct DecodeArgs {
     const uint32_t *M; const uint16_t *S; const uint32_t *D; const uint32_t *a2; const int16_t *prm;
@@ -31,8 +33,8 @@ struct DecodeArgs {
 
 // exact ints of a decoded lane-slice of class C -> v[128] (chunk-major, element e), as float times sc
 // (FP = true) or as ints (FP = false, written through the float array's bits)
-template <int C, bool FP>
-__device__ __forceinline__ void lane_values(const AnySlice<kDecNW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
+template <int C, bool FP, int NW>
+__device__ __forceinline__ void lane_values(const AnySlice<NW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
     constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
 #pragma unroll
     for (int t = 0; t < 32; ++t) {
@@ -51,16 +53,54 @@ __device__ __forceinline__ void lane_values(const AnySlice<kDecNW> &ls, const ui
     }
 }
 
-template <bool FP>
-__device__ __forceinline__ void lane_values_any(int c, const AnySlice<kDecNW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
+// the same values from the compact 2 KB table (word (f << 1) | h): the dequantizer keeps its LDS for staging
+template <int C, int NW>
+__device__ __forceinline__ void lane_values_compact(const AnySlice<NW> &ls, const uint32_t *tab2, float sc, float (&v)[128]) {
+    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+        const uint32_t h = __builtin_amdgcn_ubfe(ls.H, t, 1);
+        const uint32_t w0 = tab2[(ls.template field<C, 0>(t) << 1) | h];
+        uint32_t w1 = 0, w2 = 0;
+        if constexpr (NST > 1) w1 = tab2[(ls.template field<C, 1>(t) << 1) | h];
+        if constexpr (NST > 2) w2 = tab2[(ls.template field<C, 2>(t) << 1) | h];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int x = sext8(w0, e) * (1 << SH1);
+            if constexpr (NST > 1) x += sext8(w1, e) * (1 << SH2);
+            if constexpr (NST > 2) x += sext8(w2, e);
+            v[4 * t + e] = (float)x * sc;
+        }
+    }
+}
+
+template <int CM, int NW>
+__device__ __forceinline__ void lane_values_compact_any(int c, const AnySlice<NW> &ls, const uint32_t *tab2, float sc, float (&v)[128]) {
     switch (c) {
-        case 1: lane_values<1, FP>(ls, tab, bankbytes, sc, v); break;
-        case 2: lane_values<2, FP>(ls, tab, bankbytes, sc, v); break;
-        case 3: lane_values<3, FP>(ls, tab, bankbytes, sc, v); break;
-        case 4: lane_values<4, FP>(ls, tab, bankbytes, sc, v); break;
-        case 5: lane_values<5, FP>(ls, tab, bankbytes, sc, v); break;
-        case 6: lane_values<6, FP>(ls, tab, bankbytes, sc, v); break;
-        case 7: lane_values<7, FP>(ls, tab, bankbytes, sc, v); break;
+        case 1: if constexpr ((CM >> 1) & 1) { lane_values_compact<1>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 2: if constexpr ((CM >> 2) & 1) { lane_values_compact<2>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 3: if constexpr ((CM >> 3) & 1) { lane_values_compact<3>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 4: if constexpr ((CM >> 4) & 1) { lane_values_compact<4>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 5: if constexpr ((CM >> 5) & 1) { lane_values_compact<5>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 6: if constexpr ((CM >> 6) & 1) { lane_values_compact<6>(ls, tab2, sc, v); break; } [[fallthrough]];
+        case 7: if constexpr ((CM >> 7) & 1) { lane_values_compact<7>(ls, tab2, sc, v); break; } [[fallthrough]];
+        default:
+#pragma unroll
+            for (int i = 0; i < 128; ++i) v[i] = 0.f;
+            break;
+    }
+}
+
+template <bool FP, int CM, int NW>
+__device__ __forceinline__ void lane_values_any(int c, const AnySlice<NW> &ls, const uint32_t *tab, uint32_t bankbytes, float sc, float (&v)[128]) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) { lane_values<1, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 2: if constexpr ((CM >> 2) & 1) { lane_values<2, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 3: if constexpr ((CM >> 3) & 1) { lane_values<3, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 4: if constexpr ((CM >> 4) & 1) { lane_values<4, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 5: if constexpr ((CM >> 5) & 1) { lane_values<5, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 6: if constexpr ((CM >> 6) & 1) { lane_values<6, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
+        case 7: if constexpr ((CM >> 7) & 1) { lane_values<7, FP>(ls, tab, bankbytes, sc, v); break; } [[fallthrough]];
         default:
 #pragma unroll
             for (int i = 0; i < 128; ++i) v[i] = 0.f;   // class 0: zero weights (0.0f and int 0 share bits)
@@ -68,42 +108,72 @@ __device__ __forceinline__ void lane_values_any(int c, const AnySlice<kDecNW> &l
     }
 }
 
-// The wave's walk over tiles tile0, tile0 + stride, ...: body(tile, g, b, class, slice) runs on each tile
-// while the next tile's raw payload loads.
-template <typename Body>
-__device__ __forceinline__ void walk_tiles(const DecodeArgs &a, size_t tile0, size_t stride, int hs, int j, Body body) {
-    if (tile0 >= a.nt) return;
-    constexpr int CM = 0xFE;
-    AnyRaw<kDecNW> raw;
-    auto issue = [&](size_t tile, int &c) {
-        const int g = (int)(tile / a.nb), b = (int)(tile % a.nb);
-        const uint32_t mt = a.M[tile];
-        c = (int)(mt >> 29);
-        load_any<CM>(raw, c, a.D + (mt & 0x1FFFFFFFu) + hs * nw_of(c) * 32, j, a.S + (size_t)b * a.rows + 32 * g);
+// Tiles are visited in block-major order (tile index b * ng + g), so a workgroup's contiguous range shares
+// few 256-column blocks; the waves of a workgroup interleave over it. While a tile is processed, the next
+// tile's payload words, scale, un-permuted row and delta bounds are already loading, and every step issues
+// that prefetch (the last tile repeats), so the wait counts stay exact: on gfx9 stores share the load counter,
+// and a wait placed after a tile's stores would otherwise also wait for their completion.
+template <int NW>
+struct TileNext {
+    AnyRaw<NW> raw;
+    int c, ro, e0, e1;
+};
+
+__device__ __forceinline__ void tile_of(const DecodeArgs &a, size_t q, int &g, int &b) {
+    b = (int)(q / a.ng);
+    g = (int)(q % a.ng);
+}
+
+template <int CM, typename Body>
+__device__ __forceinline__ void walk_tiles(const DecodeArgs &a, size_t first, size_t last, size_t stride, int hs, int j, bool want_rows, Body body) {
+    if (first >= last) return;
+    constexpr int NW = dec_nw(CM);
+    TileNext<NW> nx;
+    auto issue = [&](size_t q) {
+        int g, b;
+        tile_of(a, q, g, b);
+        const uint32_t mt = a.M[(size_t)g * a.nb + b];
+        nx.c = (int)(mt >> 29);
+        load_any<CM>(nx.raw, nx.c, a.D + (mt & 0x1FFFFFFFu) + hs * nw_of(nx.c) * 32, j, a.S + (size_t)b * a.rows + 32 * g);
+        if (want_rows) {
+            nx.ro = a.prm[32 * g + j];
+            nx.e0 = a.cp[nx.ro];
+            nx.e1 = a.cp[nx.ro + 1];
+        }
     };
-    int c;
-    issue(tile0, c);
-    for (size_t tile = tile0; tile < a.nt; tile += stride) {
-        AnySlice<kDecNW> ls;
-        prepare_any<CM>(ls, c, raw, j);   // consumes the words of this tile
-        const int cur = c;
-        if (tile + stride < a.nt) issue(tile + stride, c);   // the next tile's words load during this tile
-        body(tile, (int)(tile / a.nb), (int)(tile % a.nb), cur, ls);
+    issue(first);
+    for (size_t q = first; q < last; q += stride) {
+        AnySlice<NW> ls;
+        prepare_any<CM>(ls, nx.c, nx.raw, j);   // consumes this tile's words
+        const int c = nx.c, ro = nx.ro, e0 = nx.e0, e1 = nx.e1;
+        issue(q + stride < last ? q + stride : q);   // the next tile's words load during this tile
+        int g, b;
+        tile_of(a, q, g, b);
+        body(g, b, c, ls, ro, e0, e1);
     }
 }
 
+// a workgroup's contiguous range of the block-major tile order
+__device__ __forceinline__ void wg_range(const DecodeArgs &a, size_t &first, size_t &last) {
+    const size_t per = (a.nt + gridDim.x - 1) / gridDim.x;
+    first = (size_t)blockIdx.x * per;
+    last = first + per < a.nt ? first + per : a.nt;
+}
+
 // DT: P8X_I16 (exact ints) or P8X_F32 (int * S), sorted rows, rotated domain
-template <int DT>
+template <int DT, int CM>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_decode_rotated(const DecodeArgs a) {
+    constexpr int NW = dec_nw(CM);
     __shared__ __align__(16) uint32_t tab[kTabWords];
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hs = lane >> 5, j = lane & 31;
     const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
     build_coset_table(tab, a.a2, tid, kDecThreads);
     __syncthreads();
-    walk_tiles(a, (size_t)blockIdx.x * kDecWaves + w, (size_t)gridDim.x * kDecWaves, hs, j,
-               [&](size_t, int g, int b, int c, const AnySlice<kDecNW> &ls) {
+    size_t first, last;
+    wg_range(a, first, last);
+    walk_tiles<CM>(a, first + w, last, kDecWaves, hs, j, false, [&](int g, int b, int c, const AnySlice<NW> &ls, int, int, int) {
         float v[128];
-        lane_values_any<DT == P8X_F32>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
+        lane_values_any<DT == P8X_F32, CM>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
         const size_t o = (size_t)(32 * g + j) * a.ld + 256 * b + 128 * hs;
         if constexpr (DT == P8X_I16) {
             uint2 *dst = reinterpret_cast<uint2 *>((int16_t *)a.out + o);
@@ -121,18 +191,31 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
     });
 }
 
-// original-domain weights, DT = P8X_F32 / P8X_F16 / P8X_BF16
-template <int DT>
+// original-domain weights, DT = P8X_F32 / P8X_F16 / P8X_BF16. The tile's outputs are staged in the wave's
+// LDS rows (row stride 528 bytes: 16 bytes of padding spread the rows over the banks, and every chunk is an
+// immediate offset from one per-lane base) and stored two whole row segments per instruction, so every store
+// covers full cache lines of two output rows instead of 16 bytes of 64 rows.
+template <int DT, int CM>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_dequant(const DecodeArgs a) {
-    __shared__ __align__(16) uint32_t tab[kTabWords];
+    constexpr int NW = dec_nw(CM);
+    __shared__ uint32_t tab2[512];                         // (f << 1) | h: A[f] + h c
+    __shared__ __align__(16) float icw[kDecWaves][256];    // per wave: ic of the block it is on
+    __shared__ __align__(16) uint32_t stg[kDecWaves][32 * kStgRowWords];   // per wave: 32 rows x 512 (+16) bytes
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hs = lane >> 5, j = lane & 31;
-    const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
-    build_coset_table(tab, a.a2, tid, kDecThreads);
+    for (int i = tid; i < 512; i += kDecThreads) tab2[i] = a.a2[(i & 1) * 256 + (i >> 1)];
     __syncthreads();
-    walk_tiles(a, (size_t)blockIdx.x * kDecWaves + w, (size_t)gridDim.x * kDecWaves, hs, j,
-               [&](size_t, int g, int b, int c, const AnySlice<kDecNW> &ls) {
+    size_t first, last;
+    wg_range(a, first, last);
+    int icb = -1;
+    uint32_t *sw = stg[w];
+    walk_tiles<CM>(a, first + w, last, kDecWaves, hs, j, true, [&](int g, int b, int c, const AnySlice<NW> &ls, int ro, int e0, int e1) {
+        if (b != icb) {   // a new block for this wave: its ic into the wave's LDS row (wave-local)
+            const float4 c4 = reinterpret_cast<const float4 *>(a.ic + 256 * b)[lane];
+            reinterpret_cast<float4 *>(icw[w])[lane] = c4;
+            icb = b;
+        }
         float v[128];
-        lane_values_any<true>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
+        lane_values_compact_any<CM>(c, ls, tab2, half_to_float(ls.s), v);
 #pragma unroll
         for (int h = 1; h < 128; h <<= 1)
 #pragma unroll
@@ -143,15 +226,14 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
             const float p = __shfl_xor(v[i], 32);
             v[i] = hs ? p - v[i] : v[i] + p;
         }
-        const float *icb = a.ic + 256 * b + 128 * hs;
+        const float *icl = icw[w] + 128 * hs;
 #pragma unroll
         for (int i = 0; i < 128; i += 4) {
-            const float4 c4 = *reinterpret_cast<const float4 *>(icb + i);
+            const float4 c4 = *reinterpret_cast<const float4 *>(icl + i);
             v[i] = (v[i] * 0.0625f) * c4.x; v[i + 1] = (v[i + 1] * 0.0625f) * c4.y;
             v[i + 2] = (v[i + 2] * 0.0625f) * c4.z; v[i + 3] = (v[i + 3] * 0.0625f) * c4.w;
         }
-        const int ro = a.prm[32 * g + j];
-        for (int e = a.cp[ro]; e < a.cp[ro + 1]; ++e) {   // clamp delta (original row, column)
+        for (int e = e0; e < e1; ++e) {   // clamp delta (original row, column)
             const int col = (int)a.cc[e] - 256 * b - 128 * hs;
             if (col >= 0 && col < 128) {
                 const float dv = a.cv[e];
@@ -159,23 +241,50 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
                 for (int i = 0; i < 128; ++i) v[i] = i == col ? v[i] + dv : v[i];
             }
         }
-        const size_t o = (size_t)ro * a.ld + 256 * b + 128 * hs;
-        if constexpr (DT == P8X_F32) {
-            float4 *dst = reinterpret_cast<float4 *>((float *)a.out + o);
+        // staging: row j of the wave's buffer = the tile's row j (512 bytes: the whole fp16 row, or one f32 half)
+        auto put = [&](int chunk, uint4 val) { *reinterpret_cast<uint4 *>(sw + j * kStgRowWords + 4 * chunk) = val; };
+        auto store_rows = [&](int col0) {   // 16 instructions, each two rows x 512 bytes; col0 in output elements
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's staging writes are done
 #pragma unroll
-            for (int t = 0; t < 32; ++t) dst[t] = make_float4(v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]);
-        } else {
-            uint2 *dst = reinterpret_cast<uint2 *>((uint16_t *)a.out + o);
-#pragma unroll
-            for (int t = 0; t < 32; ++t) {
-                uint16_t hv[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (DT == P8X_F16) hv[e] = __builtin_bit_cast(uint16_t, (_Float16)v[4 * t + e]);   // v_cvt_f16_f32, RNE
-                    else hv[e] = __builtin_bit_cast(uint16_t, (__bf16)v[4 * t + e]);                            // v_cvt_pk_bf16_f32, RNE
-                }
-                dst[t] = make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
+            for (int i = 0; i < 16; ++i) {
+                const int row = 2 * i + (lane >> 5), ch = lane & 31;
+                const uint4 val = *reinterpret_cast<const uint4 *>(sw + row * kStgRowWords + 4 * ch);
+                const int rro = __shfl(ro, row);
+                if constexpr (DT == P8X_F32) *reinterpret_cast<uint4 *>((float *)a.out + (size_t)rro * a.ld + col0 + 4 * ch) = val;
+                else *reinterpret_cast<uint4 *>((uint16_t *)a.out + (size_t)rro * a.ld + col0 + 8 * ch) = val;
+                if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // 4 stores at a time: bounds the live registers
             }
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the buffer is written again
+        };
+        if constexpr (DT == P8X_F32) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {   // one half-slice per round: 128 floats = 32 chunks per lane
+                if (hs == r)
+#pragma unroll
+                    for (int t = 0; t < 32; ++t)
+                        put(t, make_uint4(__builtin_bit_cast(uint32_t, v[4 * t]), __builtin_bit_cast(uint32_t, v[4 * t + 1]),
+                                          __builtin_bit_cast(uint32_t, v[4 * t + 2]), __builtin_bit_cast(uint32_t, v[4 * t + 3])));
+                store_rows(256 * b + 128 * r);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {   // 128 halfs = 16 chunks per lane, at chunk 16 hs + t of the row
+                uint32_t wv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint16_t h0, h1;
+                    if constexpr (DT == P8X_F16) {
+                        h0 = __builtin_bit_cast(uint16_t, (_Float16)v[8 * t + 2 * q]);       // v_cvt_f16_f32, RNE
+                        h1 = __builtin_bit_cast(uint16_t, (_Float16)v[8 * t + 2 * q + 1]);
+                    } else {
+                        h0 = __builtin_bit_cast(uint16_t, (__bf16)v[8 * t + 2 * q]);         // v_cvt_pk_bf16_f32, RNE
+                        h1 = __builtin_bit_cast(uint16_t, (__bf16)v[8 * t + 2 * q + 1]);
+                    }
+                    wv[q] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                }
+                put(16 * hs + t, make_uint4(wv[0], wv[1], wv[2], wv[3]));
+            }
+            store_rows(256 * b);
         }
     });
 }
@@ -195,20 +304,37 @@ static int decode_grid(const p8x_tensor *t) {
     return (int)std::min<size_t>(wgs, (size_t)num_cus() * 2);
 }
 
+static bool only_class3(const p8x_tensor *t) {
+    for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) return false;
+    return true;
+}
+
+template <int CM>
+static void launch_rot(const p8x_tensor *t, int dtype, const DecodeArgs &a, hipStream_t st) {
+    if (dtype == P8X_I16) hipLaunchKernelGGL((k_decode_rotated<P8X_I16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_decode_rotated<P8X_F32, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+}
+
+template <int CM>
+static void launch_deq(const p8x_tensor *t, int dtype, const DecodeArgs &a, hipStream_t st) {
+    if (dtype == P8X_F32) hipLaunchKernelGGL((k_dequant<P8X_F32, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    else if (dtype == P8X_F16) hipLaunchKernelGGL((k_dequant<P8X_F16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_dequant<P8X_BF16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+}
+
 int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st) {
     if (ld % 4) return set_error(P8X_ERR_ARG, "decode: ld %zu must be a multiple of 4", ld);
     const DecodeArgs a = decode_args(t, out, ld);
-    if (dtype == P8X_I16) hipLaunchKernelGGL(k_decode_rotated<P8X_I16>, dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else hipLaunchKernelGGL(k_decode_rotated<P8X_F32>, dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    if (only_class3(t)) launch_rot<(1 << 3)>(t, dtype, a, st);
+    else launch_rot<0xFE>(t, dtype, a, st);
     return hip_check(hipGetLastError(), "k_decode_rotated launch");
 }
 
 int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st) {
     if (ld % 4) return set_error(P8X_ERR_ARG, "dequantize: ld %zu must be a multiple of 4", ld);
     const DecodeArgs a = decode_args(t, out, ld);
-    if (dtype == P8X_F32) hipLaunchKernelGGL(k_dequant<P8X_F32>, dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else if (dtype == P8X_F16) hipLaunchKernelGGL(k_dequant<P8X_F16>, dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else hipLaunchKernelGGL(k_dequant<P8X_BF16>, dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    if (only_class3(t)) launch_deq<(1 << 3)>(t, dtype, a, st);
+    else launch_deq<0xFE>(t, dtype, a, st);
     return hip_check(hipGetLastError(), "k_dequant launch");
 }
 

@@ -358,6 +358,32 @@ struct AnySlice {
         s = raw.s;
     }
 
+    // stage-S field of chunk t (W1 < 8: the label bit on top of the W1 - 1 stored bits)
+    template <int C, int S>
+    __device__ __forceinline__ uint32_t field(int t) const {
+        constexpr int W1 = w1_of(C), W2 = w2_of(C);
+        if constexpr (S == 0) {
+            if constexpr (W1 == 8) return __builtin_amdgcn_ubfe(r[t >> 2], 8 * (t & 3), 8);
+            else {
+                constexpr int W = W1 - 1;
+                const int pos = W * t, wi = 1 + (pos >> 5), bb = pos & 31;
+                uint32_t f;
+                if (bb + W <= 32) f = __builtin_amdgcn_ubfe(r[wi], bb, W);
+                else f = __builtin_amdgcn_alignbit(r[1 + (wi % W)], r[wi], bb) & ((1u << W) - 1u);
+                return f | (__builtin_amdgcn_ubfe(r[0], t, 1) << W);
+            }
+        } else if constexpr (S == 1) {
+            if constexpr (W2 == 8) return __builtin_amdgcn_ubfe(r[W1 + (t >> 2)], 8 * (t & 3), 8);
+            else {
+                const int pos = W2 * t, wi = pos >> 5, bb = pos & 31;
+                if (bb + W2 <= 32) return __builtin_amdgcn_ubfe(r[W1 + wi], bb, W2);
+                return __builtin_amdgcn_alignbit(r[W1 + (wi + 1) % W2], r[W1 + wi], bb) & ((1u << W2) - 1u);
+            }
+        } else {
+            return __builtin_amdgcn_ubfe(r[W1 + W2 + (t >> 2)], 8 * (t & 3), 8);
+        }
+    }
+
     // LDS byte address of stage S at chunk t in the replicated table (p8x_lane.h layout: (f << 8) | (h << 7) |
     // (bank << 2)); hq = coset_bytes(H, bankbytes, t >> 2) holds the (h << 7) | (bank << 2) byte of each chunk
     template <int C, int S>
