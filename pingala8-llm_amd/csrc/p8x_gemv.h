@@ -162,7 +162,10 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
     for (int s = 0; s < NST; ++s)
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
-    const uint32_t *xl = sm.xq + bl * 128 + c.xlane;
+    // the tile's activation base in one register: left to itself the compiler folds the array's LDS offset
+    // (64 KB, past the table) into every read, which then does not fit the read's offset field
+    __attribute__((address_space(3))) const uint32_t *xl = (__attribute__((address_space(3))) const uint32_t *)(sm.xq + bl * 128 + c.xlane);
+    __asm__ volatile("" : "+v"(xl));
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         uint32_t xv[NCOL][4];
