@@ -115,7 +115,7 @@ __device__ __forceinline__ void weights_chunk(const uint32_t (&w)[3], half2v s2,
 
 template <int C, int NWMAX>
 __device__ __forceinline__ half8v decode_pair(const AnySlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes, int s) {
-    const half2v s2 = {__builtin_bit_cast(_Float16, ls.s), __builtin_bit_cast(_Float16, ls.s)};
+    const half2v s2 = {__builtin_bit_cast(_Float16, (uint16_t)ls.s), __builtin_bit_cast(_Float16, (uint16_t)ls.s)};
     const uint32_t hq = coset_bytes(ls.H, bankbytes, s >> 1);
     uint32_t w0[3], w1[3];
     lookup_chunk<C>(ls, tab, 2 * s, hq, w0);
@@ -207,8 +207,8 @@ __device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const A
     if (CM == kMmCmC3 || (cl[0] == kMmMain && cl[1] == kMmMain)) {
         // software-pipelined by one step: x' operands and table words of step s + 1 are read before the 8 MFMAs of
         // step s, which then wait only for the fp16 conversion of their B operands
-        const half2v s2[2] = {{__builtin_bit_cast(_Float16, ls[0].s), __builtin_bit_cast(_Float16, ls[0].s)},
-                              {__builtin_bit_cast(_Float16, ls[1].s), __builtin_bit_cast(_Float16, ls[1].s)}};
+        const half2v s2[2] = {{__builtin_bit_cast(_Float16, (uint16_t)ls[0].s), __builtin_bit_cast(_Float16, (uint16_t)ls[0].s)},
+                              {__builtin_bit_cast(_Float16, (uint16_t)ls[1].s), __builtin_bit_cast(_Float16, (uint16_t)ls[1].s)}};
         auto lookups = [&](int s, uint32_t (&W)[2][2][3]) {
 #pragma unroll
             for (int tj = 0; tj < 2; ++tj) {

@@ -29,7 +29,9 @@ namespace p8x {
 // One GEMV of a launch. A launch walks a list of these (one entry for p8x_mul_mat_vec, many for a grouped
 // launch); tasks are numbered across the list: task = (job, octet of 8 row groups, K-chunk).
 struct GemvJob {
-    const uint32_t *M; const uint16_t *S; const uint32_t *D; const int16_t *prm;
+    const uint32_t *M;
+    const uint16_t *S;               // row scales regrouped by row group: [ng][nb][32]
+    const uint32_t *D; const int16_t *prm;
     const int *cp; const uint16_t *cc; const float *cv;
     const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32]
     const float *x; unsigned ldx;    // original activations for the clamp delta (nullptr: no delta)
@@ -138,8 +140,8 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
             if constexpr (NST > 2) isum += acc[2][n][u];
             if constexpr (PARTIALS) {
                 const int r = 32 * c.g + c.j;
-                if constexpr (ACT == P8X_ACT_Q8_128) c.J->partials[((size_t)n * c.J->rows + r) * c.J->nsl + 2 * b + c.hs] = isum;
-                else c.J->partials[((size_t)n * c.J->rows + r) * (c.J->K / 32) + 8 * b + 4 * c.hs + u] = isum;
+                if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(c.J->partials)[((size_t)n * c.J->rows + r) * c.J->nsl + 2 * b + c.hs] = isum;
+                else as_global_rw(c.J->partials)[((size_t)n * c.J->rows + r) * (c.J->K / 32) + 8 * b + 4 * c.hs + u] = isum;
             }
             const float dsc = ACT == P8X_ACT_Q8_128 ? sm.xd[n * NSC + 2 * bl + c.hs] : sm.xd[n * NSC + 8 * bl + 4 * c.hs + u];
             yacc[n] += ((float)isum * dsc) * sc;
@@ -149,23 +151,20 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const Gem
 
 // One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
 // order, only summed in another order.
-template <int NCOL, int C>
-__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const GemvSmem<NCOL, P8X_ACT_Q8_128> &sm,
-                                               const StepSlice<C> &raw, int b, float (&yacc)[NCOL]) {
+using lds_cptr = __attribute__((address_space(3))) const uint32_t *;
+
+// Integer sums of one tile in step order: lane (hs, j) reads its activation chunk (j + k) & 31 of column n at
+// xl[n * XW + k] (each 128-column half kept twice in a row), and looks up the codewords in the table at LDS 0.
+template <int NCOL, int C, int XW>
+__device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C> &raw, int j, uint32_t bankbytes, lds_cptr xl,
+                                          int (&isum)[NCOL]) {
     constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
-    constexpr int XW = kXBytes / 4 / NCOL;
-    constexpr int NSC = GemvSmem<NCOL, P8X_ACT_Q8_128>::kScales / NCOL;
-    const uint32_t H = raw.coset_bits(c.j);
-    const int bl = b - c.b0;
+    const uint32_t H = raw.coset_bits(j);
     int acc[NST][NCOL];
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
-    // the tile's activation base in one register: left to itself the compiler folds the array's LDS offset
-    // (64 KB, past the table) into every read, which then does not fit the read's offset field
-    __attribute__((address_space(3))) const uint32_t *xl = (__attribute__((address_space(3))) const uint32_t *)(sm.xq + bl * 128 + c.xlane);
-    __asm__ volatile("" : "+v"(xl));
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         uint32_t xv[NCOL][4];
@@ -173,14 +172,14 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
         for (int n = 0; n < NCOL; ++n)
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[n][e] = xl[n * XW + 4 * q + e];
-        const uint32_t hq = coset_bytes(H, c.bankbytes, q);
+        const uint32_t hq = coset_bytes(H, bankbytes, q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int k = 4 * q + e;
             uint32_t w[3];
-            w[0] = lds_word(sm.tab, raw.template addr<0>(k, hq));
-            if constexpr (NST > 1) w[1] = lds_word(sm.tab, raw.template addr<1>(k, hq));
-            if constexpr (NST > 2) w[2] = lds_word(sm.tab, raw.template addr<2>(k, hq));
+            w[0] = lds_word(tab, raw.template addr<0>(k, hq));
+            if constexpr (NST > 1) w[1] = lds_word(tab, raw.template addr<1>(k, hq));
+            if constexpr (NST > 2) w[2] = lds_word(tab, raw.template addr<2>(k, hq));
 #pragma unroll
             for (int n = 0; n < NCOL; ++n)
 #pragma unroll
@@ -188,14 +187,31 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
         }
         __asm__ volatile("" ::: "memory");   // one group of 4 steps at a time: bounds the live registers
     }
-    const float sc = half_to_float(raw.s);
 #pragma unroll
     for (int n = 0; n < NCOL; ++n) {
-        int isum = acc[0][n] * (1 << SH1);
-        if constexpr (NST > 1) isum += acc[1][n] * (1 << SH2);
-        if constexpr (NST > 2) isum += acc[2][n];
-        yacc[n] += ((float)isum * sm.xd[n * NSC + 2 * bl + c.hs]) * sc;
+        isum[n] = acc[0][n] * (1 << SH1);
+        if constexpr (NST > 1) isum[n] += acc[1][n] * (1 << SH2);
+        if constexpr (NST > 2) isum[n] += acc[2][n];
     }
+}
+
+// One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
+// order, only summed in another order.
+template <int NCOL, int C>
+__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const GemvSmem<NCOL, P8X_ACT_Q8_128> &sm,
+                                               const StepSlice<C> &raw, int b, float (&yacc)[NCOL]) {
+    constexpr int XW = kXBytes / 4 / NCOL;
+    constexpr int NSC = GemvSmem<NCOL, P8X_ACT_Q8_128>::kScales / NCOL;
+    const int bl = b - c.b0;
+    // the tile's activation base in one register: left to itself the compiler folds the array's LDS offset
+    // (64 KB, past the table) into every read, which then does not fit the read's offset field
+    lds_cptr xl = (lds_cptr)(sm.xq + bl * 128 + c.xlane);
+    __asm__ volatile("" : "+v"(xl));
+    int isum[NCOL];
+    step_isum<NCOL, C, XW>(sm.tab, raw, c.j, c.bankbytes, xl, isum);
+    const float sc = half_to_float(raw.s);
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) yacc[n] += ((float)isum[n] * sm.xd[n * NSC + 2 * bl + c.hs]) * sc;
 }
 
 // A run of consecutive tiles of class C in row group g: the run's extent is found from the tile words
@@ -214,8 +230,6 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
         e = b + 1;
         while (e < bend && (tile_word(e) >> 29) == (uint32_t)C) ++e;
     }
-    const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(J.D, J.dbytes), rs = buffer_rsrc(J.S, (uint32_t)J.nb * J.rows * 2u);
-    const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(J.D, 0u);
     constexpr bool STEP = gemv_step_order<ACT, PARTIALS>();
     using Slice = std::conditional_t<STEP, StepSlice<C>, RawSlice<C>>;
     // lane part of the payload offsets: one base (step order) or the NW rotated word offsets
@@ -225,15 +239,20 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
     const uint32_t vs = 2u * (uint32_t)c.j;
     // wn = tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
     uint32_t wn = tile_word(b);
+    // past the run's end the resources have no records: the loads read zeros without memory traffic
+    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
     auto issue = [&](Slice &r, int ta) {
         const bool ok = ta < e;
         const int tc = ok ? ta : b;
         const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
-        const uint32_t soff = ((uint32_t)tc * (uint32_t)J.rows + 32u * (uint32_t)c.g) * 2u;
-        r.load(ok ? rd : r0, toff, vo, ok ? rs : r0, soff, vs);
+        const uint32_t soff = ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
+        r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         wn = tile_word(min(ta + 1, e - 1));
     };
-    auto tile = [&](const Slice &r, int t) {
+    auto tile = [&](const Slice &r0_, int t) {
+        Slice r = r0_;
+        pin(r.w);
+        pin(r.s);
         if constexpr (STEP) gemv_tile_step<NCOL, C>(c, sm, r, t, yacc);
         else gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, r, t, yacc);
     };
@@ -259,6 +278,72 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvS
 
 // prefetch depth (register buffers) per variant
 __host__ __device__ constexpr int gemv_nbuf(int ncol, int c) { return ncol == 1 && c == 3 ? GEMV_NBUF_C3 : 2; }
+
+// The row group's sums after one K-chunk: the two half-slices meet through one cross-lane add; the K-chunks of
+// the row group meet in a fixed order (the last-arriving wave sums them), so results are deterministic; then the
+// clamp delta and the row permutation on the way out.
+template <int NCOL>
+__device__ __forceinline__ void gemv_rows_out(const GemvJob &J, int g, int ks, int lane, float (&yacc)[NCOL]) {
+    // global address-space views throughout: FLAT operations here would make the compiler wait for every
+    // vector load at once in the tile loops (a pending FLAT access forces full waits)
+    const int j = lane & 31;
+    // half-slice 1 joins half-slice 0; lanes 0..31 hold the 32 rows
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) yacc[n] += __shfl_xor(yacc[n], 32);
+    bool final_rows = J.nks == 1;
+    if (J.nks > 1) {
+        // K-chunk fix-up, no agent-scope fences (on gfx950 those write back and invalidate the XCD's whole L2):
+        // partial rows are agent-coherent stores; the wave waits for them, then bumps the row group's arrival
+        // counter; the last arrival reads the partials with agent-coherent loads and sums them in chunk order.
+        const gptr<float> wpart = as_global_rw(J.wpart);
+        const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
+        if (lane < 32)
+#pragma unroll
+            for (int n = 0; n < NCOL; ++n)
+                __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * J.rows + 32 * g + j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&wcnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        final_rows = old == (unsigned)(J.nks - 1);
+        if (final_rows) {
+            if (lane < 32)
+#pragma unroll
+                for (int n = 0; n < NCOL; ++n) {
+                    // issue 8 partial loads at a time (one memory round trip per 8 chunks), sum in chunk order
+                    float sacc = 0.f;
+                    for (int k0 = 0; k0 < J.nks; k0 += 8) {
+                        float pv[8];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            pv[i] = k0 + i < J.nks ? __hip_atomic_load(&wpart[((size_t)(k0 + i) * NCOL + n) * J.rows + 32 * g + j],
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            if (k0 + i < J.nks) sacc += pv[i];
+                    }
+                    yacc[n] = sacc;
+                }
+            if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (final_rows && lane < 32) {
+        const int ro = as_global(J.prm)[32 * g + j];
+        const gptr<const int> cp = as_global(J.cp);
+        const gptr<const uint16_t> cc = as_global(J.cc);
+        const gptr<const float> cv = as_global(J.cv);
+        const gptr<float> y = as_global_rw(J.y);
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) {
+            float v = yacc[n];
+            if (J.x) {
+                const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;
+                for (int e = cp[ro]; e < cp[ro + 1]; ++e) v += cv[e] * xr[cc[e]];
+            }
+            y[(size_t)n * J.ldy + ro] = v;
+        }
+    }
+}
 
 // MULTI: the launch walks a job array in global memory (grouped launch); else its one job is the kernel argument
 template <int NCOL, int ACT, bool PARTIALS, int CM, bool MULTI>
@@ -291,14 +376,14 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
             for (int i = tid; i < NCOL * c.nbl * 128; i += NT) {
                 const int n = i / (c.nbl * 128), wi = i % (c.nbl * 128);
                 const int src = (wi >> 7) * 64 + ((wi >> 6) & 1) * 32 + (wi & 31);
-                sm.xq[n * (kXBytes / 4 / NCOL) + wi] = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[src];
+                sm.xq[n * (kXBytes / 4 / NCOL) + wi] = as_global(reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0))[src];
             }
         } else {
             for (int i = tid; i < NCOL * c.nbl * 64; i += NT) {
                 const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);
                 uint32_t v;
-                if constexpr (ACT == P8X_ACT_Q8_128) v = reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0)[wi];
-                else v = reinterpret_cast<const uint32_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + wi / 8) * 36 + 4)[wi % 8];
+                if constexpr (ACT == P8X_ACT_Q8_128) v = as_global(reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0))[wi];
+                else v = as_global(reinterpret_cast<const uint32_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + wi / 8) * 36 + 4))[wi % 8];
                 sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
             }
         }
@@ -307,8 +392,8 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
             for (int i = tid; i < NCOL * PER * c.nbl; i += NT) {
                 const int n = i / (PER * c.nbl), si = i % (PER * c.nbl);
                 float v;
-                if constexpr (ACT == P8X_ACT_Q8_128) v = J.d[(size_t)n * J.nsl + 2 * c.b0 + si];
-                else v = half_to_float(*reinterpret_cast<const uint16_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + si) * 36));
+                if constexpr (ACT == P8X_ACT_Q8_128) v = as_global(J.d)[(size_t)n * J.nsl + 2 * c.b0 + si];
+                else v = half_to_float(*as_global(reinterpret_cast<const uint16_t *>((const uint8_t *)J.q + ((size_t)n * (J.K / 32) + 8 * c.b0 + si) * 36)));
                 sm.xd[n * NSC + si] = v;
             }
         }
@@ -333,64 +418,15 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
                     if constexpr (PARTIALS) {   // class 0: zero weights
                         const int r = 32 * c.g + c.j;
                         for (int n = 0; n < NCOL; ++n) {
-                            if constexpr (ACT == P8X_ACT_Q8_128) J.partials[((size_t)n * J.rows + r) * J.nsl + 2 * b + c.hs] = 0;
-                            else for (int u = 0; u < 4; ++u) J.partials[((size_t)n * J.rows + r) * (J.K / 32) + 8 * b + 4 * c.hs + u] = 0;
+                            if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(J.partials)[((size_t)n * J.rows + r) * J.nsl + 2 * b + c.hs] = 0;
+                            else for (int u = 0; u < 4; ++u) as_global_rw(J.partials)[((size_t)n * J.rows + r) * (J.K / 32) + 8 * b + 4 * c.hs + u] = 0;
                         }
                     }
                     ++b;
                     break;
             }
         }
-        // half-slice 1 joins half-slice 0; lanes 0..31 hold the 32 rows
-#pragma unroll
-        for (int n = 0; n < NCOL; ++n) yacc[n] += __shfl_xor(yacc[n], 32);
-        bool final_rows = J.nks == 1;
-        if (J.nks > 1) {
-            // K-chunk fix-up, no agent-scope fences (on gfx950 those write back and invalidate the XCD's whole L2):
-            // partial rows are agent-coherent stores; the wave waits for them, then bumps the row group's arrival
-            // counter; the last arrival reads the partials with agent-coherent loads and sums them in chunk order.
-            if (lane < 32)
-#pragma unroll
-                for (int n = 0; n < NCOL; ++n)
-                    __hip_atomic_store(&J.wpart[((size_t)ks * NCOL + n) * J.rows + 32 * c.g + c.j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            unsigned old = 0;
-            if (lane == 0) old = __hip_atomic_fetch_add(&J.wcnt[c.g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            old = __builtin_amdgcn_readfirstlane(old);
-            final_rows = old == (unsigned)(J.nks - 1);
-            if (final_rows) {
-                if (lane < 32)
-#pragma unroll
-                    for (int n = 0; n < NCOL; ++n) {
-                        // issue 8 partial loads at a time (one memory round trip per 8 chunks), sum in chunk order
-                        float sacc = 0.f;
-                        for (int k0 = 0; k0 < J.nks; k0 += 8) {
-                            float pv[8];
-#pragma unroll
-                            for (int i = 0; i < 8; ++i)
-                                pv[i] = k0 + i < J.nks ? __hip_atomic_load(&J.wpart[((size_t)(k0 + i) * NCOL + n) * J.rows + 32 * c.g + c.j],
-                                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-#pragma unroll
-                            for (int i = 0; i < 8; ++i)
-                                if (k0 + i < J.nks) sacc += pv[i];
-                        }
-                        yacc[n] = sacc;
-                    }
-                if (lane == 0) __hip_atomic_store(&J.wcnt[c.g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (final_rows && lane < 32) {
-            const int ro = J.prm[32 * c.g + c.j];
-#pragma unroll
-            for (int n = 0; n < NCOL; ++n) {
-                float v = yacc[n];
-                if (J.x) {
-                    const float *xr = J.x + (size_t)n * J.ldx;
-                    for (int e = J.cp[ro]; e < J.cp[ro + 1]; ++e) v += J.cv[e] * xr[J.cc[e]];
-                }
-                J.y[(size_t)n * J.ldy + ro] = v;
-            }
-        }
+        gemv_rows_out<NCOL>(J, c.g, ks, lane, yacc);
     }
 }
 
@@ -405,9 +441,175 @@ static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, in
     return hip_check(hipGetLastError(), "k_gemv launch");
 }
 
+// ------------------------------------------------------------------------------------------------ wave-independent GEMV
+// One column of 8-bit-per-128 activations (the decode-batch-1 stream). Each wave is its own worker: it takes a
+// unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and keeps the tile's
+// activation block in a private 512-byte LDS slot (loaded with the tile, written twice in a row so step-order
+// reads need no wrap). Nothing waits on another wave after the table is built, so a slow wave delays only its
+// own unit and the launch drains with at most one unit per wave. Units are numbered in job order; the job
+// list is ordered by decreasing unit length, so the long units start first.
+// Class 3 only fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; classes 6 or 2-4 8-wave workgroups at 4
+// (128 VGPRs), every class at 2.
+__host__ __device__ constexpr int wave_waves(int cm) { return cm == kCmC3 ? 16 : 8; }
+__host__ __device__ constexpr int wave_per_eu(int cm) { return cm == kCmC3 ? 8 : cm == kCmAll ? 2 : 4; }
+__host__ __device__ constexpr int wave_wg_per_cu(int cm) { return 4 * wave_per_eu(cm) / wave_waves(cm); }
+
+template <int WAVES>
+struct WaveSmem {
+    uint32_t tab[kTabWords];     // LDS address 0
+    uint32_t xs[WAVES][128];     // per wave: [half][64 words], word i = activation word (i & 31) of the half
+};
+
+// A tile's payload with its activation block: one word per lane (word `lane` of the block) and the half's scale
+template <int C>
+struct WaveSlice {
+    StepSlice<C> p;
+    uint32_t xw;
+    float xd;
+};
+
+// a run of consecutive tiles of class C in row group g, NBUF tiles in flight (the gemv_run scheme)
+template <int C, int NBUF, bool ONLY_C>
+__device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot,
+                                        int g, int b, int bend, int lane, float &yacc) {
+    const int hs = lane >> 5, j = lane & 31;
+    const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)g * J.nb;
+    int e = bend;
+    if constexpr (!ONLY_C) {
+        e = b + 1;
+        while (e < bend && (mrow[e] >> 29) == (uint32_t)C) ++e;
+    }
+    constexpr int NW = nw_of(C);
+    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)J.K, dbytes = (uint32_t)J.nsl * 4u;
+    const uint32_t vo = (uint32_t)(hs * NW * 128 + 8 * j), vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)lane, vd = 4u * (uint32_t)hs;
+    uint32_t wn = mrow[b];
+    auto issue = [&](WaveSlice<C> &r, int ta) {
+        const bool ok = ta < e;
+        const int tc = ok ? ta : b;
+        const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
+        const uint32_t soff = ((uint32_t)g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
+        // past the run's end the resources have no records: the loads read zeros without memory traffic
+        r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        r.xw = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(J.q, ok ? qbytes : 0u), vq, 256u * (uint32_t)tc, 0);
+        r.xd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(J.d, ok ? dbytes : 0u), vd, 8u * (uint32_t)tc, 0));
+        wn = mrow[min(ta + 1, e - 1)];
+    };
+    lds_cptr xl = slot + hs * 64 + j;
+    auto tile = [&](const WaveSlice<C> &r_) {
+        WaveSlice<C> r = r_;
+        pin(r.p.w);
+        pin(r.p.s);
+        pin(r.xw);
+        pin(r.xd);
+        // lanes read each other's words: the slot is this wave's alone and LDS operations of one wave run in
+        // order, so compiler barriers on both sides of the writes are all the ordering needed (without them the
+        // compiler may move reads of words other lanes write across the writes)
+        __asm__ volatile("" ::: "memory");
+        slot[hs * 64 + j] = r.xw;
+        slot[hs * 64 + 32 + j] = r.xw;
+        __asm__ volatile("" ::: "memory");
+        int isum[1];
+        step_isum<1, C, 0>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, xl, isum);
+        yacc += ((float)isum[0] * r.xd) * half_to_float(r.p.s);
+    };
+    WaveSlice<C> buf[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
+    int base = b;
+    for (; base + NBUF <= e; base += NBUF) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            issue(buf[(i + NBUF - 1) % NBUF], base + i + NBUF - 1);
+            tile(buf[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i)
+        if (base + i < e) tile(buf[i]);
+    return e;
+}
+
+// Unit scheduling. Device-scope atomics on one address serialize far from the CUs, so the units are dealt to
+// np = min(kWaveParts, workgroups) partitions (unit u to partition u % np), each with its own counter pair
+// kWaveCtrStride words apart; workgroup b serves partition b % np. A wave's first unit in its partition is its rank there (no
+// atomic); after that it takes the next from the partition's counter.
+constexpr int kWaveParts = 32, kWaveCtrStride = 64;
+constexpr size_t kWaveCtrBytes = sizeof(unsigned) * kWaveParts * kWaveCtrStride;
+
+__device__ __forceinline__ unsigned wave_atomic_add(unsigned *p, int lane) {
+    unsigned v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+// ctr[part * kWaveCtrStride + 0]: units the partition has handed out beyond the first round; + 1: waves that have
+// left. Both start at 0 and the partition's last wave to leave puts them back, so launches on one stream reuse
+// them (concurrent launches that share the counters race).
+template <int CM, bool MULTI>
+__global__ __launch_bounds__(64 * wave_waves(CM)) __attribute__((amdgpu_waves_per_eu(wave_per_eu(CM), wave_per_eu(CM))))
+void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_units, unsigned *ctr, const uint32_t *__restrict__ a2) {
+    constexpr int WAVES = wave_waves(CM);
+    __shared__ WaveSmem<WAVES> sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    build_coset_table(sm.tab, a2, tid, 64 * WAVES);
+    // the slot's base in one register (it lies past the 64 KB table, beyond the LDS offset field)
+    __attribute__((address_space(3))) uint32_t *slot = (__attribute__((address_space(3))) uint32_t *)sm.xs[w];
+    __asm__ volatile("" : "+v"(slot));
+    __syncthreads();
+    const int np = min(kWaveParts, (int)gridDim.x), part = blockIdx.x % np;
+    const int nwp = (((int)gridDim.x - 1 - part) / np + 1) * WAVES;   // waves serving this partition
+    unsigned *pc = ctr + part * kWaveCtrStride;
+    int jc = 0;
+    int k = (blockIdx.x / np) * WAVES + w;
+    // each later take waits for its atomic, which also drains the previous unit's stores: the tile loops start
+    // with loads only in flight, so their wait counts stay exact
+    for (int u = part + np * k; u < total_units; u = part + np * k) {
+        if constexpr (MULTI) {   // the last job with task0 <= u, searched from the previous unit's job
+            int hi = njobs - 1;
+            while (jc < hi) {
+                const int mid = (jc + hi + 1) >> 1;
+                if (jobs[mid].task0 <= u) jc = mid; else hi = mid - 1;
+            }
+        }
+        const GemvJob &J = MULTI ? jobs[jc] : job0;
+        const int local = u - J.task0, g = local / J.nks, ks = local % J.nks;
+        const int b0 = ks * J.kchunk, bend = min(b0 + J.kchunk, J.nb);
+        float yacc[1] = {0.f};
+        for (int b = b0; b < bend;) {
+            const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
+            switch (mt >> 29) {
+                case 1: if constexpr ((CM >> 1) & 1) { b = wave_run<1, 2, CM == (1 << 1)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = wave_run<2, 2, CM == (1 << 2)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = wave_run<3, GEMV_NBUF_C3, CM == (1 << 3)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = wave_run<4, 2, CM == (1 << 4)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = wave_run<5, 2, CM == (1 << 5)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = wave_run<6, 2, CM == (1 << 6)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = wave_run<7, 2, CM == (1 << 7)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                default: ++b; break;   // class 0: zero weights
+            }
+        }
+        gemv_rows_out<1>(J, g, ks, lane, yacc);
+        k = nwp + (int)wave_atomic_add(pc, lane);
+    }
+    const unsigned left = wave_atomic_add(pc + 1, lane);
+    if (lane == 0 && left == (unsigned)nwp - 1) {
+        __hip_atomic_store(pc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pc + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int CM>
+static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st) {
+    const int grid = wave_wg_per_cu(CM) * num_cus();
+    if (jobs) hipLaunchKernelGGL((k_gemv_wave<CM, true>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, njobs, units, ctr, a2);
+    else hipLaunchKernelGGL((k_gemv_wave<CM, false>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, njobs, units, ctr, a2);
+    return hip_check(hipGetLastError(), "k_gemv_wave launch");
+}
+
 // defined in the instantiation units
 int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
+int launch_gemv_wave(int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
 
 }  // namespace p8x

@@ -15,6 +15,7 @@
 // accumulates with float atomics, CPU.patch:4014).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -139,7 +140,7 @@ GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
 static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
                      float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int gpt, int task0) {
     g = GemvJob{};
-    g.M = t->M; g.S = t->S; g.D = t->D; g.prm = t->prm;
+    g.M = t->M; g.S = t->Sg; g.D = t->D; g.prm = t->prm;
     g.cp = t->cp; g.cc = t->cc; g.cv = t->cv;
     g.q = q; g.d = d; g.x = x; g.ldx = (unsigned)ldx; g.y = y; g.ldy = (unsigned)ldy; g.partials = partials;
     g.wpart = t->wpart; g.wcnt = t->wcnt;
@@ -212,6 +213,8 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
 
 struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
+    bool wave = false;             // one column: the wave-independent kernel
+    unsigned *ctr = nullptr;       // its unit counters (in work)
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
     p8x::ActJob *d_act = nullptr;
@@ -245,29 +248,34 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: job %d has a different codebook", i);
         for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
     }
-    // workspace layout per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows] | counters [ng]
+    // workspace layout: unit counters | per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows] |
+    // counters [ng]
     std::vector<GemvJob> jobs(njobs);
     std::vector<ActJob> act(njobs);
     std::vector<size_t> off_q(njobs), off_d(njobs), off_p(njobs), off_c(njobs);
     size_t bytes = 0;
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
-    int task0 = 0, blk0 = 0;
-    const int cm = class_set(hist), gpt = gemv_waves(ncols, P8X_ACT_Q8_128, false, cm);
+    const size_t off_ctr = take(kWaveCtrBytes);
+    int blk0 = 0;
+    const int cm = class_set(hist);
+    // one column: wave-independent units (row group, whole K); more: workgroup tasks of gpt row groups over
+    // K-chunks that fit the LDS activation buffer
+    const bool wave = ncols == 1;
+    const int gpt = wave ? 1 : gemv_waves(ncols, P8X_ACT_Q8_128, false, cm);
     for (int i = 0; i < njobs; ++i) {
         const p8x_tensor *t = tensors[i];
-        const int kc = std::min(t->nb, kchunk_max(ncols));
+        const int kc = wave ? t->nb : std::min(t->nb, kchunk_max(ncols));
         const int nks = (t->nb + kc - 1) / kc;
         off_q[i] = take((size_t)ncols * t->K);
         off_d[i] = take(4 * (size_t)ncols * t->nsl);
         off_p[i] = nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
         off_c[i] = nks > 1 ? take(4 * (size_t)t->ng) : 0;
-        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, task0);
-        task0 += jobs[i].ntasks;
+        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, 0);
         act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
         blk0 += t->nb;
     }
     p8x_gemv_batch *b = new p8x_gemv_batch();
-    b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_tasks = task0; b->total_blocks = blk0;
+    b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_blocks = blk0; b->wave = wave;
     b->a2 = tensors[0]->a2;
     int rc;
     if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||
@@ -276,6 +284,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: hipMalloc");
     }
     uint8_t *w = (uint8_t *)b->work;
+    b->ctr = (unsigned *)(w + off_ctr);
     for (int i = 0; i < njobs; ++i) {
         jobs[i].q = w + off_q[i];
         jobs[i].d = (const float *)(w + off_d[i]);
@@ -284,6 +293,13 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         if (jobs[i].nks > 1) { jobs[i].wpart = (float *)(w + off_p[i]); jobs[i].wcnt = (unsigned *)(w + off_c[i]); }
         else { jobs[i].wpart = nullptr; jobs[i].wcnt = nullptr; }
     }
+    // task numbering: longest units (most blocks per unit) first, so that dynamic scheduling ends on short ones
+    std::stable_sort(jobs.begin(), jobs.end(), [](const GemvJob &a, const GemvJob &c) {
+        return std::min(a.kchunk, a.nb) > std::min(c.kchunk, c.nb);
+    });
+    int task0 = 0;
+    for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
+    b->total_tasks = task0;
     if ((rc = hip_check(hipMemset(b->work, 0, bytes), "p8x_gemv_batch_create: clear")) ||
         (rc = hip_check(hipMemcpy(b->d_jobs, jobs.data(), sizeof(GemvJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: jobs")) ||
         (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs"))) {
@@ -303,6 +319,7 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     }
     if (stage == 1) {
         GemvJob none{};
+        if (b->wave) return launch_gemv_wave(b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->ctr, b->a2, st);
         return launch_gemv_q8(b->ncols, b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->a2, st);
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);

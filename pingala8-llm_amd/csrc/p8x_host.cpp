@@ -43,6 +43,15 @@ int num_cus() {
 
 static int nw_tile(uint32_t m) { return nw_of((int)(m >> 29)); }
 
+// row scales [nb][rows] -> [ng][nb][32], one element per thread
+__global__ void k_regroup_scales(const uint16_t *__restrict__ S, uint16_t *__restrict__ Sg, int nb, int rows, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const size_t gb = i >> 5;
+    const int j = (int)(i & 31), g = (int)(gb / nb), b = (int)(gb % nb);
+    Sg[i] = S[(size_t)b * rows + 32 * g + j];
+}
+
 }  // namespace p8x
 
 using namespace p8x;
@@ -87,7 +96,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -199,9 +208,11 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if (on_device) {
         t->base = src;
     } else {
-        if ((rc = alloc((void **)&t->owned, n, "slot"))) return fail(rc);
-        if ((rc = hip_check(hipMemcpy(t->owned, src, n, hipMemcpyHostToDevice), "p8x_prepare: upload slot"))) return fail(rc);
-        t->base = t->owned;
+        // payload tiles on 256-byte boundaries: every tile then covers whole cache lines
+        const size_t pad = (256 - offset_D(nt) % 256) % 256;
+        if ((rc = alloc((void **)&t->owned, n + pad, "slot"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->owned + pad, src, n, hipMemcpyHostToDevice), "p8x_prepare: upload slot"))) return fail(rc);
+        t->base = t->owned + pad;
     }
     t->M = (const uint32_t *)(t->base + kHeaderBytes);
     t->S = (const uint16_t *)(t->base + offset_S(nt));
@@ -217,6 +228,9 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
             }
         }
     }
+    if ((rc = alloc((void **)&t->Sg, 64 * nt, "regrouped scales"))) return fail(rc);
+    hipLaunchKernelGGL(k_regroup_scales, dim3((unsigned)((32 * nt + 255) / 256)), dim3(256), 0, 0, t->S, t->Sg, nb, rows, 32 * nt);
+    if ((rc = hip_check(hipGetLastError(), "p8x_prepare: regroup scales"))) return fail(rc);
     if ((rc = alloc((void **)&t->a2, 512 * 4, "tables"))) return fail(rc);
     if ((rc = alloc((void **)&t->ic, 4 * (size_t)K, "ic"))) return fail(rc);
     if ((rc = alloc((void **)&t->cp, 4 * (size_t)(rows + 1), "delta rows"))) return fail(rc);

@@ -15,12 +15,14 @@ struct p8x_tensor {
     size_t class_tiles[8] = {0};
     int device = 0;
     const uint8_t *base = nullptr;   // device slot bytes
-    uint8_t *owned = nullptr;        // set when the library copied host bytes
+    uint8_t *owned = nullptr;        // set when the library copied host bytes (the slot sits past a pad that puts
+                                     // the payload on a 256-byte boundary)
     // views into the slot (device)
     const uint32_t *M = nullptr;
     const uint16_t *S = nullptr;
     const uint32_t *D = nullptr;
     const int16_t *prm = nullptr;
+    uint16_t *Sg = nullptr;          // row scales regrouped [ng][nb][32]: a row group's scales in one run
     int16_t *pinv = nullptr;         // original row -> sorted row (built at prepare)
     bool prm_identity = false;
     // device metadata built at prepare

@@ -40,6 +40,8 @@ template <typename T>
 using gptr = __attribute__((address_space(1))) T *;
 template <typename T>
 __device__ __forceinline__ gptr<const T> as_global(const T *p) { return (gptr<const T>)p; }
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global_rw(T *p) { return (gptr<T>)p; }
 // constant address-space view (read-only for the kernel's lifetime): uniform loads become scalar s_load,
 // which wait on their own counter instead of behind the in-flight vector loads
 // raw buffer resources (stride 0, byte records); word 3 is the gfx9-family default for untyped access
@@ -56,6 +58,17 @@ __device__ __forceinline__ kptr<const T> as_const(const T *p) { return (kptr<con
 
 __device__ __forceinline__ uint32_t lds_word(const uint32_t *tab, uint32_t byte_addr) {
     return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(tab) + byte_addr);
+}
+
+// Ties loaded values to this point of the program: nothing computed from them moves above it, so the wait for
+// their loads sits here and the loads issued for later tiles stay in flight (left alone, the scheduler hoists
+// the next tile's label arithmetic and waits for that tile's loads too early).
+__device__ __forceinline__ void pin(uint32_t &v) { __asm__ volatile("; pin %0" : "+v"(v)); }
+__device__ __forceinline__ void pin(float &v) { __asm__ volatile("; pin %0" : "+v"(v)); }
+template <int N>
+__device__ __forceinline__ void pin(uint32_t (&w)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) __asm__ volatile("; pin %0" : "+v"(w[i]));
 }
 
 // closed form of the 8-state trellis over one 32-chunk label word (chunk order in, chunk order out)
@@ -120,7 +133,7 @@ template <int C>
 struct RawSlice {
     static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
     uint32_t w[NW];
-    uint16_t s;
+    uint32_t s;   // fp16 row scale, zero-extended by its load
 
     template <int W, int WB, int O>
     static __device__ __forceinline__ void region_offsets(uint32_t hsoff, int j, uint32_t (&vo)[NW]) {
@@ -246,7 +259,7 @@ struct StepSlice {
     static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C), NP = NW / 2;
     static constexpr int O1 = W1 == 8 ? 0 : 1, O2 = W1, O3 = W1 + W2;   // first word of each stage's fields
     uint32_t w[NW];
-    uint16_t s;
+    uint32_t s;   // fp16 row scale, zero-extended by its load
 
     // vo = hs * NW * 128 + 8 j: the lane's byte offset of word pair 0; pair p sits 256 p bytes further
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rd, uint32_t toff, uint32_t vo,
@@ -301,7 +314,7 @@ struct StepSlice {
 template <int NWMAX>
 struct AnyRaw {
     uint32_t w[NWMAX];
-    uint16_t s;
+    uint32_t s;   // fp16 row scale, zero-extended by its load
 
     template <int W, int WB>
     __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
@@ -329,7 +342,7 @@ template <int NWMAX>
 struct AnySlice {
     uint32_t r[NWMAX];
     uint32_t H;
-    uint16_t s;
+    uint32_t s;   // fp16 row scale, zero-extended by its load
 
     template <int W, int WB>
     __device__ __forceinline__ void rotate(const AnyRaw<NWMAX> &raw, int j) {

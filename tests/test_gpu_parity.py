@@ -205,3 +205,51 @@ def test_batch_matches_single(ncols):
             Y = ys[i].to_numpy(np.float32, (ncols, rows))
             for n in range(ncols):
                 assert rel_l2(Y[n], orcs[i].gemv_f64(hx[i][n])) < 1e-5, (i, n, rep)
+
+
+@pytest.mark.parametrize("cp", [(0, 0, 0, 1, 0, 0, 0, 0), (0, 0, 0, 0, 0, 0, 1, 0), (0, 0, 1, 6, 1, 0, 0, 0)])
+def test_batch_one_column_class_sets(cp):
+    """one-column grouped launches per class set (class 3, class 6, classes 2-4): units of unequal length,
+    three runs in a row (the unit counters reset themselves), bitwise equal runs, fp64 oracle per job"""
+    shapes = [(2048, 4096), (512, 4096), (1024, 14336), (96, 256), (64, 2560)]
+    rng = np.random.default_rng(sum(cp))
+    tensors, orcs, xs, ys, hx = [], [], [], [], []
+    for i, (rows, K) in enumerate(shapes):
+        slot = p8x.synth_random(500 + i, rows, K, class_p=cp, nd=2)
+        tensors.append(p8x.Tensor(slot, rows, K))
+        orcs.append(O.Oracle(slot, rows, K))
+        X = rng.standard_normal((1, K)).astype(np.float32)
+        hx.append(X)
+        xs.append(p8x.DeviceBuffer.from_numpy(X))
+        ys.append(p8x.DeviceBuffer(4 * rows))
+    batch = p8x.GemvBatch(tensors, xs, ys, ncols=1)
+    first = None
+    for rep in range(3):
+        for y in ys:
+            y.fill(0)
+        batch.run()
+        p8x.synchronize()
+        out = [y.to_numpy(np.float32, (rows,)) for y, (rows, _) in zip(ys, shapes)]
+        if first is None:
+            first = out
+            for i in range(len(shapes)):
+                assert rel_l2(out[i], orcs[i].gemv_f64(hx[i][0])) < 1e-5, i
+        else:
+            for a, c in zip(first, out):
+                assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), rep
+
+
+def test_batch_fewer_units_than_waves():
+    """a grouped launch with 3 row groups in all: most waves find no unit and leave; a second run still works"""
+    slot = p8x.synth_random(901, 96, 512, class_p=(0, 0, 0, 1, 0, 0, 0, 0), nd=1)
+    t = p8x.Tensor(slot, 96, 512)
+    orc = O.Oracle(slot, 96, 512)
+    X = np.random.default_rng(901).standard_normal((1, 512)).astype(np.float32)
+    x = p8x.DeviceBuffer.from_numpy(X)
+    y = p8x.DeviceBuffer(4 * 96)
+    batch = p8x.GemvBatch([t], [x], [y], ncols=1)
+    for rep in range(2):
+        y.fill(0)
+        batch.run()
+        p8x.synchronize()
+        assert rel_l2(y.to_numpy(np.float32, (96,)), orc.gemv_f64(X[0])) < 1e-5, rep
