@@ -101,7 +101,8 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
             if events is not None:
                 events[2 * i + 1].record(stream)
 
-    step_linear()
+    for _ in range(5):   # past the GPU's settling phase (tens of milliseconds of load)
+        step_linear()
     stream.sync()
     evs = [[p8x.Event() for _ in range(2 * len(tensors))] for _ in range(pl_steps)]
     p8x.synchronize()
@@ -141,7 +142,7 @@ def measure_gemm(steps, N=512):
         xd = p8x.DeviceBuffer.from_numpy(xb)
         yd = p8x.DeviceBuffer(4 * N * rows)
         stream = p8x.Stream()
-        for _ in range(3):
+        for _ in range(20):
             t.mul_mat_dev(xd, p8x.BF16, N, yd, stream=stream)
         stream.sync()
         ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
@@ -181,7 +182,7 @@ def measure_dequant(steps):
     t = p8x.Tensor(p8x.synth_random(99, rows, K, nd=8), rows, K)
     out = p8x.DeviceBuffer(2 * rows * K)
     stream = p8x.Stream()
-    for _ in range(3):
+    for _ in range(40):
         t.dequantize_dev(p8x.F16, out, stream=stream)
     stream.sync()
     ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
@@ -202,8 +203,10 @@ def measure_dequant(steps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    # the first few dozen back-to-back launches run slower while the GPU settles (power management); the
+    # default warmup runs past that so the timed steps see the steady state
+    ap.add_argument("--warmup", type=int, default=150)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--mix", choices=("c3", "b4"), default="c3")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)

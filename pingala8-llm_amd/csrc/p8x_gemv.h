@@ -436,8 +436,12 @@ template <int NCOL, int ACT, bool PARTIALS, int CM>
 static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
     constexpr int NT = 64 * gemv_waves(NCOL, ACT, PARTIALS, CM);
     const int grid = std::min(tasks, gemv_wg_per_cu(NCOL, ACT, PARTIALS, CM) * num_cus());
-    if (jobs) hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
-    else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
+    if (jobs) {   // grouped launches: one column runs the wave-independent kernel instead
+        if constexpr (NCOL == 1) return set_error(P8X_ERR_UNSUPPORTED, "k_gemv: one-column grouped launch");
+        else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
+    } else {
+        hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
+    }
     return hip_check(hipGetLastError(), "k_gemv launch");
 }
 

@@ -262,9 +262,27 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     // K-chunks that fit the LDS activation buffer
     const bool wave = ncols == 1;
     const int gpt = wave ? 1 : gemv_waves(ncols, P8X_ACT_Q8_128, false, cm);
+    std::vector<int> kcs(njobs);
+    for (int i = 0; i < njobs; ++i) kcs[i] = wave ? tensors[i]->nb : std::min(tensors[i]->nb, kchunk_max(ncols));
+    if (wave) {
+        // Units are handed out longest first, so the launch drains on the units of the last jobs. Those jobs are
+        // split along K (units of >= 4 blocks, partial rows summed by the fix-up) until about two rounds of the
+        // launch's waves have short units to finish on.
+        const long need = 2L * wave_wg_per_cu(cm) * num_cus() * wave_waves(cm);
+        std::vector<int> order(njobs);
+        for (int i = 0; i < njobs; ++i) order[i] = i;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return tensors[a]->nb > tensors[c]->nb; });
+        long have = 0;
+        for (int r = njobs - 1; r >= 0 && have < need; --r) {
+            const p8x_tensor *t = tensors[order[r]];
+            const int nks = std::min(4, std::max(1, t->nb / 4));
+            kcs[order[r]] = (t->nb + nks - 1) / nks;
+            have += (long)t->ng * ((t->nb + kcs[order[r]] - 1) / kcs[order[r]]);
+        }
+    }
     for (int i = 0; i < njobs; ++i) {
         const p8x_tensor *t = tensors[i];
-        const int kc = wave ? t->nb : std::min(t->nb, kchunk_max(ncols));
+        const int kc = kcs[i];
         const int nks = (t->nb + kc - 1) / kc;
         off_q[i] = take((size_t)ncols * t->K);
         off_d[i] = take(4 * (size_t)ncols * t->nsl);
