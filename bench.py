@@ -248,6 +248,7 @@ def main():
         ev[s_][0].record(stream)
         batch.run_stage(1, stream)
         ev[s_][1].record(stream)
+        batch.run_stage(2, stream)
     e1.record(stream)
     stream.sync()
     wall = time.perf_counter() - t0

@@ -446,12 +446,13 @@ static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, in
 }
 
 // ------------------------------------------------------------------------------------------------ wave-independent GEMV
-// One column of 8-bit-per-128 activations (the decode-batch-1 stream). Each wave is its own worker: it takes a
-// unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and keeps the tile's
-// activation block in a private 512-byte LDS slot (loaded with the tile, written twice in a row so step-order
-// reads need no wrap). Nothing waits on another wave after the table is built, so a slow wave delays only its
-// own unit and the launch drains with at most one unit per wave. Units are numbered in job order; the job
-// list is ordered by decreasing unit length, so the long units start first.
+// One column of 8-bit-per-128 activations (the decode-batch-1 stream), grouped launches only. Each wave is its own
+// worker: it takes a unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and
+// leaves the sorted-row partials for the finishing launch. It keeps each tile's activation block in a private
+// 512-byte LDS slot (loaded with the tile, written twice in a row so step-order reads need no wrap). Nothing
+// waits on another wave after the table is built, so a slow wave delays only its own unit and the launch
+// drains with at most one unit per wave. Units are numbered in job order; the job list is ordered by decreasing
+// unit length, so the long units start first.
 // Class 3 only fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; classes 6 or 2-4 8-wave workgroups at 4
 // (128 VGPRs), every class at 2.
 __host__ __device__ constexpr int wave_waves(int cm) { return cm == kCmC3 ? 16 : 8; }
@@ -471,6 +472,28 @@ struct WaveSlice {
     uint32_t xw;
     float xd;
 };
+
+// One tile of a wave: the activation block goes to the wave's slot, then the step-order integer sums.
+template <int C>
+__device__ __forceinline__ void wave_tile(const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot, int lane,
+                                          const WaveSlice<C> &r_, float &yacc) {
+    const int hs = lane >> 5, j = lane & 31;
+    WaveSlice<C> r = r_;
+    pin(r.p.w);
+    pin(r.p.s);
+    pin(r.xw);
+    pin(r.xd);
+    // lanes read each other's words: the slot is this wave's alone and LDS operations of one wave run in order,
+    // so compiler barriers on both sides of the writes are all the ordering needed (without them the compiler
+    // may move reads of words other lanes write across the writes)
+    __asm__ volatile("" ::: "memory");
+    slot[hs * 64 + j] = r.xw;
+    slot[hs * 64 + 32 + j] = r.xw;
+    __asm__ volatile("" ::: "memory");
+    int isum[1];
+    step_isum<1, C, 0>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, slot + hs * 64 + j, isum);
+    yacc += ((float)isum[0] * r.xd) * half_to_float(r.p.s);
+}
 
 // a run of consecutive tiles of class C in row group g, NBUF tiles in flight (the gemv_run scheme)
 template <int C, int NBUF, bool ONLY_C>
@@ -498,24 +521,7 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
         r.xd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(J.d, ok ? dbytes : 0u), vd, 8u * (uint32_t)tc, 0));
         wn = mrow[min(ta + 1, e - 1)];
     };
-    lds_cptr xl = slot + hs * 64 + j;
-    auto tile = [&](const WaveSlice<C> &r_) {
-        WaveSlice<C> r = r_;
-        pin(r.p.w);
-        pin(r.p.s);
-        pin(r.xw);
-        pin(r.xd);
-        // lanes read each other's words: the slot is this wave's alone and LDS operations of one wave run in
-        // order, so compiler barriers on both sides of the writes are all the ordering needed (without them the
-        // compiler may move reads of words other lanes write across the writes)
-        __asm__ volatile("" ::: "memory");
-        slot[hs * 64 + j] = r.xw;
-        slot[hs * 64 + 32 + j] = r.xw;
-        __asm__ volatile("" ::: "memory");
-        int isum[1];
-        step_isum<1, C, 0>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, xl, isum);
-        yacc += ((float)isum[0] * r.xd) * half_to_float(r.p.s);
-    };
+    auto tile = [&](const WaveSlice<C> &r) { wave_tile<C>(tab, slot, lane, r, yacc); };
     WaveSlice<C> buf[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
@@ -546,12 +552,22 @@ __device__ __forceinline__ unsigned wave_atomic_add(unsigned *p, int lane) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
+// A wave unit's rows: the half-slices meet through one cross-lane add, and lanes 0..31 store the row group's 32
+// sorted-row partials of K-chunk ks to wpart [nks][rows] (one 128-byte line, no loads, no atomics, so nothing
+// waits on the loads in flight). The batch's finishing launch sums the K-chunks in order, applies the clamp
+// delta and writes original rows.
+__device__ __forceinline__ void wave_rows_store(const GemvJob &J, int g, int ks, int lane, float yacc) {
+    yacc += __shfl_xor(yacc, 32);
+    if (lane < 32) as_global_rw(J.wpart)[(size_t)ks * J.rows + 32 * g + lane] = yacc;
+}
+
 // ctr[part * kWaveCtrStride + 0]: units the partition has handed out beyond the first round; + 1: waves that have
 // left. Both start at 0 and the partition's last wave to leave puts them back, so launches on one stream reuse
 // them (concurrent launches that share the counters race).
 template <int CM, bool MULTI>
 __global__ __launch_bounds__(64 * wave_waves(CM)) __attribute__((amdgpu_waves_per_eu(wave_per_eu(CM), wave_per_eu(CM))))
-void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_units, unsigned *ctr, const uint32_t *__restrict__ a2) {
+void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, const uint32_t *__restrict__ ujob, int total_units, unsigned *ctr,
+                 const uint32_t *__restrict__ a2) {
     constexpr int WAVES = wave_waves(CM);
     __shared__ WaveSmem<WAVES> sm;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -563,18 +579,11 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int 
     const int np = min(kWaveParts, (int)gridDim.x), part = blockIdx.x % np;
     const int nwp = (((int)gridDim.x - 1 - part) / np + 1) * WAVES;   // waves serving this partition
     unsigned *pc = ctr + part * kWaveCtrStride;
-    int jc = 0;
     int k = (blockIdx.x / np) * WAVES + w;
     // each later take waits for its atomic, which also drains the previous unit's stores: the tile loops start
     // with loads only in flight, so their wait counts stay exact
     for (int u = part + np * k; u < total_units; u = part + np * k) {
-        if constexpr (MULTI) {   // the last job with task0 <= u, searched from the previous unit's job
-            int hi = njobs - 1;
-            while (jc < hi) {
-                const int mid = (jc + hi + 1) >> 1;
-                if (jobs[mid].task0 <= u) jc = mid; else hi = mid - 1;
-            }
-        }
+        const int jc = MULTI ? (int)as_const(ujob)[u] : 0;
         const GemvJob &J = MULTI ? jobs[jc] : job0;
         const int local = u - J.task0, g = local / J.nks, ks = local % J.nks;
         const int b0 = ks * J.kchunk, bend = min(b0 + J.kchunk, J.nb);
@@ -592,7 +601,7 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int 
                 default: ++b; break;   // class 0: zero weights
             }
         }
-        gemv_rows_out<1>(J, g, ks, lane, yacc);
+        wave_rows_store(J, g, ks, lane, yacc[0]);
         k = nwp + (int)wave_atomic_add(pc, lane);
     }
     const unsigned left = wave_atomic_add(pc + 1, lane);
@@ -603,10 +612,11 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int 
 }
 
 template <int CM>
-static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st) {
+static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2,
+                              hipStream_t st) {
     const int grid = wave_wg_per_cu(CM) * num_cus();
-    if (jobs) hipLaunchKernelGGL((k_gemv_wave<CM, true>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, njobs, units, ctr, a2);
-    else hipLaunchKernelGGL((k_gemv_wave<CM, false>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, njobs, units, ctr, a2);
+    if (jobs) hipLaunchKernelGGL((k_gemv_wave<CM, true>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, ujob, units, ctr, a2);
+    else hipLaunchKernelGGL((k_gemv_wave<CM, false>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, ujob, units, ctr, a2);
     return hip_check(hipGetLastError(), "k_gemv_wave launch");
 }
 
@@ -614,6 +624,7 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, int njob
 int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
-int launch_gemv_wave(int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
+int launch_gemv_wave(int cm, const GemvJob *jobs, const GemvJob &job0, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2,
+                     hipStream_t st);
 
 }  // namespace p8x

@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <map>
 #include <vector>
 
 #include "p8x_gemv.h"
@@ -209,12 +210,39 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
+// Finishing launch of a one-column grouped GEMV, 256 sorted rows of one job per block: original row prm[r] of
+// sorted row r gets the K-chunk partials in chunk order plus its clamp delta (the order and arithmetic of the
+// single-launch fix-up).
+struct FinishJob {
+    const float *wpart; const int16_t *prm; const int *dsr; const uint16_t *cc; const float *cv; const float *x;
+    float *y;
+    int rows, nks, blk0;
+};
+
+__global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job) {
+    const FinishJob &J = jobs[as_const(blk_job)[blockIdx.x]];
+    const int r = ((int)blockIdx.x - J.blk0) * 256 + threadIdx.x;
+    if (r >= J.rows) return;
+    const gptr<const float> wp = as_global(J.wpart);
+    float v = 0.f;
+    for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
+    if (J.x) {
+        const int e0 = as_global(J.dsr)[2 * r], e1 = as_global(J.dsr)[2 * r + 1];
+        for (int e = e0; e < e1; ++e) v += as_global(J.cv)[e] * as_global(J.x)[as_global(J.cc)[e]];
+    }
+    as_global_rw(J.y)[as_global(J.prm)[r]] = v;
+}
+
 }  // namespace p8x
 
 struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
     bool wave = false;             // one column: the wave-independent kernel
     unsigned *ctr = nullptr;       // its unit counters (in work)
+    uint32_t *d_ujob = nullptr;    // unit -> job
+    p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
+    uint32_t *d_fblk = nullptr;        // its block -> job
+    int fin_blocks = 0;
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
     p8x::ActJob *d_act = nullptr;
@@ -229,6 +257,9 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
     if (!b) return;
     if (b->d_jobs) (void)hipFree(b->d_jobs);
     if (b->d_act) (void)hipFree(b->d_act);
+    if (b->d_ujob) (void)hipFree(b->d_ujob);
+    if (b->d_fin) (void)hipFree(b->d_fin);
+    if (b->d_fblk) (void)hipFree(b->d_fblk);
     if (b->work) (void)hipFree(b->work);
     delete b;
 }
@@ -286,8 +317,9 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         const int nks = (t->nb + kc - 1) / kc;
         off_q[i] = take((size_t)ncols * t->K);
         off_d[i] = take(4 * (size_t)ncols * t->nsl);
-        off_p[i] = nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
-        off_c[i] = nks > 1 ? take(4 * (size_t)t->ng) : 0;
+        // one column: partial rows of every job (the finishing launch reads them); more: K-chunk fix-up buffers
+        off_p[i] = wave || nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
+        off_c[i] = !wave && nks > 1 ? take(4 * (size_t)t->ng) : 0;
         fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, 0);
         act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
         blk0 += t->nb;
@@ -308,9 +340,11 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         jobs[i].d = (const float *)(w + off_d[i]);
         act[i].q = (int8_t *)(w + off_q[i]);
         act[i].d = (float *)(w + off_d[i]);
-        if (jobs[i].nks > 1) { jobs[i].wpart = (float *)(w + off_p[i]); jobs[i].wcnt = (unsigned *)(w + off_c[i]); }
-        else { jobs[i].wpart = nullptr; jobs[i].wcnt = nullptr; }
+        jobs[i].wpart = wave || jobs[i].nks > 1 ? (float *)(w + off_p[i]) : nullptr;
+        jobs[i].wcnt = !wave && jobs[i].nks > 1 ? (unsigned *)(w + off_c[i]) : nullptr;
     }
+    std::map<const uint32_t *, const int *> dsr_of;   // the sorted jobs find their tensor's delta ranges by M
+    for (int i = 0; i < njobs; ++i) dsr_of[tensors[i]->M] = tensors[i]->dsr;
     // task numbering: longest units (most blocks per unit) first, so that dynamic scheduling ends on short ones
     std::stable_sort(jobs.begin(), jobs.end(), [](const GemvJob &a, const GemvJob &c) {
         return std::min(a.kchunk, a.nb) > std::min(c.kchunk, c.nb);
@@ -318,6 +352,38 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     int task0 = 0;
     for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
     b->total_tasks = task0;
+    if (wave) {
+        // unit -> job table
+        std::vector<uint32_t> uj((size_t)task0);
+        for (int i = 0; i < njobs; ++i)
+            for (int u = 0; u < jobs[i].ntasks; ++u) uj[(size_t)jobs[i].task0 + u] = (uint32_t)i;
+        std::vector<FinishJob> fin(njobs);
+        std::vector<uint32_t> fblk;
+        for (int i = 0; i < njobs; ++i) {
+            const GemvJob &g = jobs[i];
+            fin[i] = FinishJob{g.wpart, g.prm, dsr_of[g.M], g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
+            for (int r = 0; r < g.rows; r += 256) fblk.push_back((uint32_t)i);
+        }
+        b->fin_blocks = (int)fblk.size();
+        if (hipMalloc((void **)&b->d_fin, sizeof(FinishJob) * njobs) != hipSuccess ||
+            hipMalloc((void **)&b->d_fblk, 4 * fblk.size()) != hipSuccess) {
+            p8x_gemv_batch_release(b);
+            return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: finishing jobs");
+        }
+        if ((rc = hip_check(hipMemcpy(b->d_fin, fin.data(), sizeof(FinishJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing jobs")) ||
+            (rc = hip_check(hipMemcpy(b->d_fblk, fblk.data(), 4 * fblk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing blocks"))) {
+            p8x_gemv_batch_release(b);
+            return rc;
+        }
+        if (hipMalloc((void **)&b->d_ujob, 4 * uj.size()) != hipSuccess) {
+            p8x_gemv_batch_release(b);
+            return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: unit table");
+        }
+        if ((rc = hip_check(hipMemcpy(b->d_ujob, uj.data(), 4 * uj.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: unit table"))) {
+            p8x_gemv_batch_release(b);
+            return rc;
+        }
+    }
     if ((rc = hip_check(hipMemset(b->work, 0, bytes), "p8x_gemv_batch_create: clear")) ||
         (rc = hip_check(hipMemcpy(b->d_jobs, jobs.data(), sizeof(GemvJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: jobs")) ||
         (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs"))) {
@@ -337,15 +403,21 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     }
     if (stage == 1) {
         GemvJob none{};
-        if (b->wave) return launch_gemv_wave(b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->ctr, b->a2, st);
+        if (b->wave) return launch_gemv_wave(b->cm, b->d_jobs, none, b->d_ujob, b->total_tasks, b->ctr, b->a2, st);
         return launch_gemv_q8(b->ncols, b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->a2, st);
+    }
+    if (stage == 2) {   // one column: partial rows to original rows with the clamp delta (nothing otherwise)
+        if (!b->wave) return P8X_OK;
+        hipLaunchKernelGGL(k_gemv_finish, dim3(b->fin_blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk);
+        return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
 }
 
 int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream) {
-    int rc = p8x_gemv_batch_run_stage(b, 0, stream);
-    return rc ? rc : p8x_gemv_batch_run_stage(b, 1, stream);
+    int rc = 0;
+    for (int stage = 0; stage < 3 && !rc; ++stage) rc = p8x_gemv_batch_run_stage(b, stage, stream);
+    return rc;
 }
 
 }  // extern "C"

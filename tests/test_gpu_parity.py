@@ -207,11 +207,13 @@ def test_batch_matches_single(ncols):
                 assert rel_l2(Y[n], orcs[i].gemv_f64(hx[i][n])) < 1e-5, (i, n, rep)
 
 
+@pytest.mark.parametrize("one_block", [False, True])
 @pytest.mark.parametrize("cp", [(0, 0, 0, 1, 0, 0, 0, 0), (0, 0, 0, 0, 0, 0, 1, 0), (0, 0, 1, 6, 1, 0, 0, 0)])
-def test_batch_one_column_class_sets(cp):
-    """one-column grouped launches per class set (class 3, class 6, classes 2-4): units of unequal length,
-    three runs in a row (the unit counters reset themselves), bitwise equal runs, fp64 oracle per job"""
-    shapes = [(2048, 4096), (512, 4096), (1024, 14336), (96, 256), (64, 2560)]
+def test_batch_one_column_class_sets(cp, one_block):
+    """one-column grouped launches per class set (class 3, class 6, classes 2-4): units of unequal length (split
+    along K at the end), three runs in a row (the unit counters reset themselves), bitwise equal runs, fp64 oracle
+    per job, with and without one-block units."""
+    shapes = [(2048, 4096), (512, 4096), (1024, 14336), (64, 2560)] + ([(96, 256)] if one_block else [])
     rng = np.random.default_rng(sum(cp))
     tensors, orcs, xs, ys, hx = [], [], [], [], []
     for i, (rows, K) in enumerate(shapes):
