@@ -210,27 +210,40 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
-// Finishing launch of a one-column grouped GEMV, 256 sorted rows of one job per block: original row prm[r] of
-// sorted row r gets the K-chunk partials in chunk order plus its clamp delta (the order and arithmetic of the
-// single-launch fix-up).
+// Finishing launch of a one-column grouped GEMV. The first blocks take 256 sorted rows of one job each and write
+// original row prm[r] = the K-chunk partials in chunk order; rows that carry clamp-delta entries (a bitmap says
+// which) are left to the last blocks, one thread per such row, which add the delta entries after the partials
+// (the order and arithmetic of the single-launch fix-up).
 struct FinishJob {
-    const float *wpart; const int16_t *prm; const int *dsr; const uint16_t *cc; const float *cv; const float *x;
+    const float *wpart; const int16_t *prm; const uint32_t *dbits;
+    const int *cp; const uint16_t *cc; const float *cv; const float *x;
     float *y;
     int rows, nks, blk0;
 };
 
-__global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job) {
-    const FinishJob &J = jobs[as_const(blk_job)[blockIdx.x]];
-    const int r = ((int)blockIdx.x - J.blk0) * 256 + threadIdx.x;
-    if (r >= J.rows) return;
-    const gptr<const float> wp = as_global(J.wpart);
-    float v = 0.f;
-    for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
-    if (J.x) {
-        const int e0 = as_global(J.dsr)[2 * r], e1 = as_global(J.dsr)[2 * r + 1];
-        for (int e = e0; e < e1; ++e) v += as_global(J.cv)[e] * as_global(J.x)[as_global(J.cc)[e]];
+__global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
+                                                     const int2 *__restrict__ drows, int ndrows) {
+    int r;
+    const FinishJob *J;
+    if ((int)blockIdx.x < nplain) {
+        J = &jobs[as_const(blk_job)[blockIdx.x]];
+        r = ((int)blockIdx.x - J->blk0) * 256 + threadIdx.x;
+        if (r >= J->rows || ((as_global(J->dbits)[r >> 5] >> (r & 31)) & 1u)) return;
+    } else {
+        const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
+        if (i >= ndrows) return;
+        J = &jobs[drows[i].x];
+        r = drows[i].y;
     }
-    as_global_rw(J.y)[as_global(J.prm)[r]] = v;
+    const gptr<const float> wp = as_global(J->wpart);
+    float v = 0.f;
+    for (int ks = 0; ks < J->nks; ++ks) v += wp[(size_t)ks * J->rows + r];
+    const int ro = as_global(J->prm)[r];
+    if ((int)blockIdx.x >= nplain && J->x) {
+        const gptr<const float> x = as_global(J->x);
+        for (int e = as_global(J->cp)[ro]; e < as_global(J->cp)[ro + 1]; ++e) v += as_global(J->cv)[e] * x[as_global(J->cc)[e]];
+    }
+    as_global_rw(J->y)[ro] = v;
 }
 
 }  // namespace p8x
@@ -242,7 +255,8 @@ struct p8x_gemv_batch {
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
     uint32_t *d_fblk = nullptr;        // its block -> job
-    int fin_blocks = 0;
+    int2 *d_fdrows = nullptr;          // its rows with clamp-delta entries: (job, sorted row)
+    int fin_blocks = 0, fin_ndrows = 0;
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
     p8x::ActJob *d_act = nullptr;
@@ -260,6 +274,7 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
     if (b->d_ujob) (void)hipFree(b->d_ujob);
     if (b->d_fin) (void)hipFree(b->d_fin);
     if (b->d_fblk) (void)hipFree(b->d_fblk);
+    if (b->d_fdrows) (void)hipFree(b->d_fdrows);
     if (b->work) (void)hipFree(b->work);
     delete b;
 }
@@ -343,8 +358,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         jobs[i].wpart = wave || jobs[i].nks > 1 ? (float *)(w + off_p[i]) : nullptr;
         jobs[i].wcnt = !wave && jobs[i].nks > 1 ? (unsigned *)(w + off_c[i]) : nullptr;
     }
-    std::map<const uint32_t *, const int *> dsr_of;   // the sorted jobs find their tensor's delta ranges by M
-    for (int i = 0; i < njobs; ++i) dsr_of[tensors[i]->M] = tensors[i]->dsr;
+    std::map<const uint32_t *, const p8x_tensor *> tensor_of;   // the sorted jobs find their tensor by M
+    for (int i = 0; i < njobs; ++i) tensor_of[tensors[i]->M] = tensors[i];
     // task numbering: longest units (most blocks per unit) first, so that dynamic scheduling ends on short ones
     std::stable_sort(jobs.begin(), jobs.end(), [](const GemvJob &a, const GemvJob &c) {
         return std::min(a.kchunk, a.nb) > std::min(c.kchunk, c.nb);
@@ -359,19 +374,26 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             for (int u = 0; u < jobs[i].ntasks; ++u) uj[(size_t)jobs[i].task0 + u] = (uint32_t)i;
         std::vector<FinishJob> fin(njobs);
         std::vector<uint32_t> fblk;
+        std::vector<int2> fdr;
         for (int i = 0; i < njobs; ++i) {
             const GemvJob &g = jobs[i];
-            fin[i] = FinishJob{g.wpart, g.prm, dsr_of[g.M], g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
+            const p8x_tensor *t = tensor_of[g.M];
+            fin[i] = FinishJob{g.wpart, g.prm, t->dbits, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
             for (int r = 0; r < g.rows; r += 256) fblk.push_back((uint32_t)i);
+            for (int r : t->dsorted) fdr.push_back(make_int2(i, r));
         }
         b->fin_blocks = (int)fblk.size();
+        b->fin_ndrows = (int)fdr.size();
         if (hipMalloc((void **)&b->d_fin, sizeof(FinishJob) * njobs) != hipSuccess ||
-            hipMalloc((void **)&b->d_fblk, 4 * fblk.size()) != hipSuccess) {
+            hipMalloc((void **)&b->d_fblk, 4 * fblk.size()) != hipSuccess ||
+            hipMalloc((void **)&b->d_fdrows, sizeof(int2) * std::max<size_t>(1, fdr.size())) != hipSuccess) {
             p8x_gemv_batch_release(b);
             return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: finishing jobs");
         }
         if ((rc = hip_check(hipMemcpy(b->d_fin, fin.data(), sizeof(FinishJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing jobs")) ||
-            (rc = hip_check(hipMemcpy(b->d_fblk, fblk.data(), 4 * fblk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing blocks"))) {
+            (rc = hip_check(hipMemcpy(b->d_fblk, fblk.data(), 4 * fblk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing blocks")) ||
+            (!fdr.empty() && (rc = hip_check(hipMemcpy(b->d_fdrows, fdr.data(), sizeof(int2) * fdr.size(), hipMemcpyHostToDevice),
+                                             "p8x_gemv_batch_create: finishing delta rows")))) {
             p8x_gemv_batch_release(b);
             return rc;
         }
@@ -408,7 +430,9 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     }
     if (stage == 2) {   // one column: partial rows to original rows with the clamp delta (nothing otherwise)
         if (!b->wave) return P8X_OK;
-        hipLaunchKernelGGL(k_gemv_finish, dim3(b->fin_blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk);
+        const int blocks = b->fin_blocks + (b->fin_ndrows + 255) / 256;
+        hipLaunchKernelGGL(k_gemv_finish, dim3(blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
+                           b->fin_blocks, (const int2 *)b->d_fdrows, b->fin_ndrows);
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);

@@ -96,7 +96,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->dsr, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->dbits, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -250,11 +250,12 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         if ((rc = alloc((void **)&t->pinv, 2 * (size_t)rows, "pinv"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->pinv, pinv.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: pinv"))) return fail(rc);
     }
-    {   // per sorted row: [begin, end) of its original row's clamp-delta entries
-        std::vector<int> dsr(2 * (size_t)rows);
-        for (int r = 0; r < rows; ++r) { dsr[2 * r] = cp[prm[r]]; dsr[2 * r + 1] = cp[prm[r] + 1]; }
-        if ((rc = alloc((void **)&t->dsr, 8 * (size_t)rows, "sorted-row delta ranges"))) return fail(rc);
-        if ((rc = hip_check(hipMemcpy(t->dsr, dsr.data(), 8 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: delta ranges"))) return fail(rc);
+    {   // sorted rows whose original row carries clamp-delta entries: a bitmap and the host list
+        std::vector<uint32_t> bits(((size_t)rows + 31) / 32, 0u);
+        for (int r = 0; r < rows; ++r)
+            if (cp[prm[r] + 1] > cp[prm[r]]) { bits[r >> 5] |= 1u << (r & 31); t->dsorted.push_back(r); }
+        if ((rc = alloc((void **)&t->dbits, 4 * bits.size(), "delta row bits"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->dbits, bits.data(), 4 * bits.size(), hipMemcpyHostToDevice), "p8x_prepare: delta row bits"))) return fail(rc);
     }
     std::vector<int> drows;
     for (int r = 0; r < rows; ++r) if (cp[r + 1] > cp[r]) drows.push_back(r);

@@ -386,6 +386,8 @@ class Tensor:
 class GemvBatch:
     """A grouped launch of independent GEMVs (device buffers x_i, y_i fixed at creation)."""
 
+    stages = 3   # activation prep, fused decode + GEMV, finishing (a no-op for more than one column)
+
     def __init__(self, tensors, xs, ys, ncols=1):
         n = len(tensors)
         T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
