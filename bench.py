@@ -164,7 +164,7 @@ def measured_traffic(step_bytes, layers, mix):
     """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload
     (counter KiB scaled by what the same counters read for a device copy of known size); None if absent or
     taken on another workload."""
-    path = os.path.join(ROOT, "profiles", "k_gemv_llama8b_stream.json")
+    path = os.path.join(ROOT, "profiles", "k_gemv_wave_llama8b_stream.json")
     try:
         with open(path) as f:
             prof = json.load(f)
@@ -172,7 +172,7 @@ def measured_traffic(step_bytes, layers, mix):
         return None, None
     if prof.get("stream_bytes_per_step") != step_bytes or prof.get("layers") != layers or prof.get("class_mix") != mix:
         return None, None
-    return int(prof["traffic_bytes_per_launch"]), "profiles/k_gemv_llama8b_stream.json"
+    return int(prof["traffic_bytes_per_launch"]), "profiles/k_gemv_wave_llama8b_stream.json"
 
 
 def measure_dequant(steps):

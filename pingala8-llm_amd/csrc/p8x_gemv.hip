@@ -210,40 +210,60 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
-// Finishing launch of a one-column grouped GEMV. The first blocks take 256 sorted rows of one job each and write
-// original row prm[r] = the K-chunk partials in chunk order; rows that carry clamp-delta entries (a bitmap says
-// which) are left to the last blocks, one thread per such row, which add the delta entries after the partials
-// (the order and arithmetic of the single-launch fix-up).
+// Finishing launch of a one-column grouped GEMV. The first blocks take 1024 original rows of one job each (4 per
+// thread, loads issued together): row ro gathers the K-chunk partials of its sorted row pinv[ro] in chunk order
+// and is written in place. Rows that carry clamp-delta entries (a bitmap says which) are left to the last blocks,
+// one thread per such row, which add the delta entries after the partials (the order and arithmetic of the
+// single-launch fix-up).
+constexpr int kFinRows = 1024;
+
 struct FinishJob {
-    const float *wpart; const int16_t *prm; const uint32_t *dbits;
+    const float *wpart; const int16_t *pinv; const uint32_t *dbits;
     const int *cp; const uint16_t *cc; const float *cv; const float *x;
     float *y;
     int rows, nks, blk0;
 };
 
+__device__ __forceinline__ float finish_row(const FinishJob &J, int r) {
+    const gptr<const float> wp = as_global(J.wpart);
+    float v = 0.f;
+    for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
+    return v;
+}
+
 __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
                                                      const int2 *__restrict__ drows, int ndrows) {
-    int r;
-    const FinishJob *J;
     if ((int)blockIdx.x < nplain) {
-        J = &jobs[as_const(blk_job)[blockIdx.x]];
-        r = ((int)blockIdx.x - J->blk0) * 256 + threadIdx.x;
-        if (r >= J->rows || ((as_global(J->dbits)[r >> 5] >> (r & 31)) & 1u)) return;
+        const FinishJob &J = jobs[as_const(blk_job)[blockIdx.x]];
+        const int ro0 = ((int)blockIdx.x - J.blk0) * kFinRows + threadIdx.x;
+        int r[4];
+        uint32_t bits[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ro = min(ro0 + 256 * i, J.rows - 1);
+            r[i] = as_global(J.pinv)[ro];
+            bits[i] = as_global(J.dbits)[ro >> 5];
+        }
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = finish_row(J, r[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ro = ro0 + 256 * i;
+            if (ro < J.rows && !((bits[i] >> (ro & 31)) & 1u)) as_global_rw(J.y)[ro] = v[i];
+        }
     } else {
         const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
         if (i >= ndrows) return;
-        J = &jobs[drows[i].x];
-        r = drows[i].y;
+        const FinishJob &J = jobs[drows[i].x];
+        const int ro = drows[i].y;
+        float v = finish_row(J, as_global(J.pinv)[ro]);
+        if (J.x) {
+            const gptr<const float> x = as_global(J.x);
+            for (int e = as_global(J.cp)[ro]; e < as_global(J.cp)[ro + 1]; ++e) v += as_global(J.cv)[e] * x[as_global(J.cc)[e]];
+        }
+        as_global_rw(J.y)[ro] = v;
     }
-    const gptr<const float> wp = as_global(J->wpart);
-    float v = 0.f;
-    for (int ks = 0; ks < J->nks; ++ks) v += wp[(size_t)ks * J->rows + r];
-    const int ro = as_global(J->prm)[r];
-    if ((int)blockIdx.x >= nplain && J->x) {
-        const gptr<const float> x = as_global(J->x);
-        for (int e = as_global(J->cp)[ro]; e < as_global(J->cp)[ro + 1]; ++e) v += as_global(J->cv)[e] * x[as_global(J->cc)[e]];
-    }
-    as_global_rw(J->y)[ro] = v;
 }
 
 }  // namespace p8x
@@ -255,7 +275,7 @@ struct p8x_gemv_batch {
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
     uint32_t *d_fblk = nullptr;        // its block -> job
-    int2 *d_fdrows = nullptr;          // its rows with clamp-delta entries: (job, sorted row)
+    int2 *d_fdrows = nullptr;          // its rows with clamp-delta entries: (job, original row)
     int fin_blocks = 0, fin_ndrows = 0;
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
@@ -378,9 +398,9 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         for (int i = 0; i < njobs; ++i) {
             const GemvJob &g = jobs[i];
             const p8x_tensor *t = tensor_of[g.M];
-            fin[i] = FinishJob{g.wpart, g.prm, t->dbits, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
-            for (int r = 0; r < g.rows; r += 256) fblk.push_back((uint32_t)i);
-            for (int r : t->dsorted) fdr.push_back(make_int2(i, r));
+            fin[i] = FinishJob{g.wpart, t->pinv, t->dbits, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
+            for (int r = 0; r < g.rows; r += kFinRows) fblk.push_back((uint32_t)i);
+            for (int r : t->dorig) fdr.push_back(make_int2(i, r));
         }
         b->fin_blocks = (int)fblk.size();
         b->fin_ndrows = (int)fdr.size();

@@ -250,10 +250,10 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         if ((rc = alloc((void **)&t->pinv, 2 * (size_t)rows, "pinv"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->pinv, pinv.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: pinv"))) return fail(rc);
     }
-    {   // sorted rows whose original row carries clamp-delta entries: a bitmap and the host list
+    {   // original rows that carry clamp-delta entries: a bitmap and the host list
         std::vector<uint32_t> bits(((size_t)rows + 31) / 32, 0u);
         for (int r = 0; r < rows; ++r)
-            if (cp[prm[r] + 1] > cp[prm[r]]) { bits[r >> 5] |= 1u << (r & 31); t->dsorted.push_back(r); }
+            if (cp[r + 1] > cp[r]) { bits[r >> 5] |= 1u << (r & 31); t->dorig.push_back(r); }
         if ((rc = alloc((void **)&t->dbits, 4 * bits.size(), "delta row bits"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->dbits, bits.data(), 4 * bits.size(), hipMemcpyHostToDevice), "p8x_prepare: delta row bits"))) return fail(rc);
     }
