@@ -290,12 +290,12 @@ def main():
         "dtype": "int8", "data": "synthetic (random-valid class-3 codes, N(0,1) activations)",
         "config": {"workload": "llama3.1-8b linear stack, batch 1: 32 x (q,k,v,o,gate,up,down) + lm_head as 4 x 32064 rows, "
                                "streamed by one grouped launch per step",
-                   "layers": args.layers, "class_mix": args.mix, "linears": len(tensors), "launches_per_step": 2,
+                   "layers": args.layers, "class_mix": args.mix, "linears": len(tensors), "launches_per_step": batch.stages,
                    "stream_bytes_per_step": int(step_bytes), "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
                    "activations": "q8 per 128 columns (k_vr_qx_real semantics)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel": "k_gemv<1,Q8_128,class 3> (fused decode + GEMV, grouped launch)", "launches": args.steps,
+                     "kernel": "k_gemv_wave<class 3> (fused decode + GEMV, grouped launch)", "launches": args.steps,
                      "bytes_per_launch": int(step_bytes)},
         "cpu_baseline": cpu,
         "per_linear_launches": per_linear,
