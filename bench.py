@@ -89,30 +89,29 @@ def cpu_baseline(host0, seconds, threads):
 
 
 def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
-    q = p8x.DeviceBuffer(max(t.K for t in tensors))
-    d = p8x.DeviceBuffer(4 * (max(t.K for t in tensors) // 128))
-
+    """the drop-in pattern: one p8x_mul_mat_vec call (a single launch) per linear, as a MUL_MAT hook would issue"""
     def step_linear(events=None):
         for i, t in enumerate(tensors):
-            t.quantize_q8_128_dev(xs[t.K], q, d, stream=stream)
             if events is not None:
                 events[2 * i].record(stream)
-            t.vec_dot_dev(p8x.ACT_Q8_128, q, d, ybufs[i], x=xs[t.K], stream=stream)
+            t.mul_mat_vec_dev(xs[t.K], ybufs[i], stream=stream)
             if events is not None:
                 events[2 * i + 1].record(stream)
 
     for _ in range(5):   # past the GPU's settling phase (tens of milliseconds of load)
         step_linear()
     stream.sync()
-    evs = [[p8x.Event() for _ in range(2 * len(tensors))] for _ in range(pl_steps)]
-    p8x.synchronize()
     e0, e1 = p8x.Event(), p8x.Event()
     e0.record(stream)
-    for s_ in range(pl_steps):
-        step_linear(evs[s_])
+    for _ in range(pl_steps):
+        step_linear()
     e1.record(stream)
     stream.sync()
     pl_ms = e0.elapsed_ms(e1) / pl_steps
+    evs = [[p8x.Event() for _ in range(2 * len(tensors))] for _ in range(pl_steps)]
+    for s_ in range(pl_steps):
+        step_linear(evs[s_])
+    stream.sync()
     kern_ms = np.zeros(len(tensors))
     for s_ in range(pl_steps):
         for i in range(len(tensors)):
@@ -123,11 +122,11 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
     for k in dict.fromkeys(kinds):
         idx = [i for i, kk in enumerate(kinds) if kk == k]
         per_kind[k] = {"GB/s": round(bytes_per[idx].sum() / (kern_ms[idx].sum() * 1e-3) / 1e9, 1),
-                       "us_per_launch": round(float(kern_ms[idx].mean() * 1e3), 2),
-                       "MB_per_launch": round(float(bytes_per[idx].mean() / 1e6), 3)}
-    log("per-linear launches, per kind:", json.dumps(per_kind))
+                       "us_per_call": round(float(kern_ms[idx].mean() * 1e3), 2),
+                       "MB_per_call": round(float(bytes_per[idx].mean() / 1e6), 3)}
+    log("per-linear p8x_mul_mat_vec calls, per kind:", json.dumps(per_kind))
     per_linear = {"GB/s": round(step_bytes / (pl_ms * 1e-3) / 1e9, 1), "ms_per_step": round(pl_ms, 4),
-                  "launches_per_step": 2 * len(tensors), "per_kind": per_kind}
+                  "launches_per_step": len(tensors), "per_kind": per_kind}
     return per_linear
 
 

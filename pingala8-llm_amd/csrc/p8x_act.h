@@ -1,0 +1,66 @@
+// p8x_act.h -- activation prep shared by the standalone launches and the fused single-GEMV staging:
+// x' = FWHT256(x * ic) / 16 per 256-block (CPU.patch:533-554), quantized to 8 bits per 128 columns
+// (CPU.patch:559-571). Global address-space views only (no FLAT accesses in the kernels that include this).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "p8x_lane.h"
+
+namespace p8x {
+
+// correctly rounded f32 quotient via f64 (53 >= 2*24 + 2 bits: no double-rounding error)
+__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
+
+// x' for one 256-block: lane holds 4 consecutive elements
+__device__ __forceinline__ void rotate_block_lane(const float *__restrict__ x, const float *__restrict__ ic, int lane, float (&v)[4]) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 xv = as_global(reinterpret_cast<const f32x4 *>(x))[lane];
+    const f32x4 cv = as_global(reinterpret_cast<const f32x4 *>(ic))[lane];
+    v[0] = xv.x * cv.x; v[1] = xv.y * cv.y; v[2] = xv.z * cv.z; v[3] = xv.w * cv.w;
+    // h = 1, 2 inside the lane
+    { const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3]; v[0] = a0 + b0; v[1] = a0 - b0; v[2] = a1 + b1; v[3] = a1 - b1; }
+    { const float a0 = v[0], b0 = v[2], a1 = v[1], b1 = v[3]; v[0] = a0 + b0; v[2] = a0 - b0; v[1] = a1 + b1; v[3] = a1 - b1; }
+    // h = 4 .. 128 across lanes: the lower index gets a + b, the upper a - b, with a the lower operand
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p = __shfl_xor(v[e], m);
+            v[e] = upper ? p - v[e] : v[e] + p;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= 0.0625f;
+}
+
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ __forceinline__ int half_wave_sum(int v) {
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// one 256-block to 8 bits per 128 columns: lane l gets the packed int8 of x' elements 4l..4l+3, the scale of its
+// half (max |x'| / 127, correctly rounded) and the integer sum of its four values
+__device__ __forceinline__ void quantize_block_q8_128(const float *__restrict__ x, const float *__restrict__ ic, int lane, uint32_t &packed,
+                                                      float &dd, int &sum) {
+    float v[4];
+    rotate_block_lane(x, ic, lane, v);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = half_wave_max(am);
+    dd = div_rn(am, 127.f);
+    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
+    int qi[4];
+    sum = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { qi[e] = __float2int_rn(v[e] * id); sum += qi[e]; }
+    packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+}
+
+}  // namespace p8x

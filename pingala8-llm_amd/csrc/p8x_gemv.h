@@ -15,6 +15,7 @@
 
 #include <type_traits>
 
+#include "p8x_act.h"
 #include "p8x_internal.h"
 #include "p8x_lane.h"
 
@@ -34,6 +35,8 @@ struct GemvJob {
     const uint32_t *D; const int16_t *prm;
     const int *cp; const uint16_t *cc; const float *cv;
     const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32]
+                                     // (Q8_128 with q null: each task quantizes its chunk of x itself, with ic)
+    const float *ic;
     const float *x; unsigned ldx;    // original activations for the clamp delta (nullptr: no delta)
     float *y; unsigned ldy;
     int32_t *partials;               // optional integer partials (sorted rows)
@@ -371,12 +374,28 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
         c.g = WAVES * oct + w;
         // stage this task's activations and scales
         __syncthreads();
+        bool scales_staged = false;
         if constexpr (gemv_step_order<ACT, PARTIALS>()) {
             // [n][block][half][64]: word i of a half = activation word (i & 31) of that half
-            for (int i = tid; i < NCOL * c.nbl * 128; i += NT) {
-                const int n = i / (c.nbl * 128), wi = i % (c.nbl * 128);
-                const int src = (wi >> 7) * 64 + ((wi >> 6) & 1) * 32 + (wi & 31);
-                sm.xq[n * (kXBytes / 4 / NCOL) + wi] = as_global(reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0))[src];
+            if (J.q) {
+                for (int i = tid; i < NCOL * c.nbl * 128; i += NT) {
+                    const int n = i / (c.nbl * 128), wi = i % (c.nbl * 128);
+                    const int src = (wi >> 7) * 64 + ((wi >> 6) & 1) * 32 + (wi & 31);
+                    sm.xq[n * (kXBytes / 4 / NCOL) + wi] = as_global(reinterpret_cast<const uint32_t *>((const int8_t *)J.q + (size_t)n * J.K + 256 * c.b0))[src];
+                }
+            } else {   // the chunk's blocks quantized here, one wave per (column, block): no separate prep launch
+                for (int pi = w; pi < NCOL * c.nbl; pi += WAVES) {
+                    const int n = pi / c.nbl, bl = pi % c.nbl;
+                    uint32_t packed;
+                    float dd;
+                    int qs;
+                    quantize_block_q8_128(J.x + (size_t)n * J.ldx + 256 * (c.b0 + bl), J.ic + 256 * (c.b0 + bl), lane, packed, dd, qs);
+                    uint32_t *xw = sm.xq + n * (kXBytes / 4 / NCOL) + bl * 128 + (lane >> 5) * 64 + (lane & 31);
+                    xw[0] = packed;
+                    xw[32] = packed;
+                    if ((lane & 31) == 0) sm.xd[n * NSC + 2 * bl + (lane >> 5)] = dd;
+                }
+                scales_staged = true;
             }
         } else {
             for (int i = tid; i < NCOL * c.nbl * 64; i += NT) {
@@ -387,7 +406,7 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
                 sm.xq[n * (kXBytes / 4 / NCOL) + wi] = v;
             }
         }
-        {
+        if (!scales_staged) {
             constexpr int PER = ACT == P8X_ACT_Q8_128 ? 2 : 8;
             for (int i = tid; i < NCOL * PER * c.nbl; i += NT) {
                 const int n = i / (PER * c.nbl), si = i % (PER * c.nbl);

@@ -25,57 +25,14 @@
 namespace p8x {
 
 // ------------------------------------------------------------------------------------------------ activation prep
-// correctly rounded f32 quotient via f64 (53 >= 2*24 + 2 bits: no double-rounding error)
-__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
-
-// x' for one 256-block: lane holds 4 consecutive elements
-__device__ __forceinline__ void rotate_block_lane(const float *__restrict__ x, const float *__restrict__ ic, int lane, float (&v)[4]) {
-    const float4 xv = *reinterpret_cast<const float4 *>(x + 4 * lane);
-    const float4 cv = *reinterpret_cast<const float4 *>(ic + 4 * lane);
-    v[0] = xv.x * cv.x; v[1] = xv.y * cv.y; v[2] = xv.z * cv.z; v[3] = xv.w * cv.w;
-    // h = 1, 2 inside the lane
-    { const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3]; v[0] = a0 + b0; v[1] = a0 - b0; v[2] = a1 + b1; v[3] = a1 - b1; }
-    { const float a0 = v[0], b0 = v[2], a1 = v[1], b1 = v[3]; v[0] = a0 + b0; v[2] = a0 - b0; v[1] = a1 + b1; v[3] = a1 - b1; }
-    // h = 4 .. 128 across lanes: the lower index gets a + b, the upper a - b, with a the lower operand
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool upper = (lane & m) != 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float p = __shfl_xor(v[e], m);
-            v[e] = upper ? p - v[e] : v[e] + p;
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] *= 0.0625f;
-}
-
-__device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-
-__device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m);
-    return v;
-}
-
 // grid (nb, ncols), block 64
 __global__ __launch_bounds__(64) void k_act_q8_128(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
                                                    int8_t *__restrict__ q, float *__restrict__ d, int32_t *__restrict__ sum) {
     const int b = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    float v[4];
-    rotate_block_lane(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane, v);
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = half_wave_max(am);
-    const float dd = div_rn(am, 127.f);
-    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
-    int qi[4], s = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { qi[e] = __float2int_rn(v[e] * id); s += qi[e]; }
-    const uint32_t packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+    uint32_t packed;
+    float dd;
+    int s;
+    quantize_block_q8_128(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane, packed, dd, s);
     reinterpret_cast<uint32_t *>(q + (size_t)n * K + 256 * b)[lane] = packed;
     s = half_wave_sum(s);
     const int nsl = K / 128;
@@ -148,6 +105,7 @@ static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float
     g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl;
     g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + gpt - 1) / gpt) * nks;
     g.dbytes = (unsigned)(t->kbytes - offset_D(t->nt));
+    g.ic = t->ic;
 }
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
@@ -196,16 +154,10 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
     }
     const ActJob J = jobs[lo];
     const int b = gb - J.blk0;
-    float v[4];
-    rotate_block_lane(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane, v);
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = half_wave_max(am);
-    const float dd = div_rn(am, 127.f);
-    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
-    int qi[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) qi[e] = __float2int_rn(v[e] * id);
-    const uint32_t packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+    uint32_t packed;
+    float dd;
+    int s;
+    quantize_block_q8_128(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane, packed, dd, s);
     reinterpret_cast<uint32_t *>(J.q + (size_t)n * J.K + 256 * b)[lane] = packed;
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }

@@ -331,10 +331,8 @@ int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols,
         return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: ldx %zu ldy %zu (x 16-byte aligned, ldx %% 4 == 0)", ldx, ldy);
     hipStream_t st = (hipStream_t)stream;
     int rc;
-    if (act == P8X_ACT_Q8_128) {
-        if ((rc = launch_act_q8_128(t, x, ncols, ldx, t->wq, t->wd, nullptr, st))) return rc;
-        return launch_gemv(t, act, t->wq, t->wd, ncols, x, ldx, y, ldy, nullptr, st);
-    }
+    if (act == P8X_ACT_Q8_128)   // one launch: every task quantizes its chunk of x itself (same arithmetic as the prep)
+        return launch_gemv(t, act, nullptr, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
     if (act == P8X_ACT_Q8_1) {
         if ((rc = launch_act_q8_1(t, x, ncols, ldx, t->wq81, st))) return rc;
         return launch_gemv(t, act, t->wq81, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
