@@ -11,11 +11,20 @@ namespace p8x {
 // correctly rounded f32 quotient via f64 (53 >= 2*24 + 2 bits: no double-rounding error)
 __device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 
-// x' for one 256-block: lane holds 4 consecutive elements
-__device__ __forceinline__ void rotate_block_lane(const float *__restrict__ x, const float *__restrict__ ic, int lane, float (&v)[4]) {
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-    const f32x4 xv = as_global(reinterpret_cast<const f32x4 *>(x))[lane];
-    const f32x4 cv = as_global(reinterpret_cast<const f32x4 *>(ic))[lane];
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// the lane's 4 consecutive elements of one 256-block of x and of ic
+struct BlockLane {
+    f32x4 x, c;
+    __device__ __forceinline__ void load(const float *__restrict__ xb, const float *__restrict__ icb, int lane) {
+        x = as_global(reinterpret_cast<const f32x4 *>(xb))[lane];
+        c = as_global(reinterpret_cast<const f32x4 *>(icb))[lane];
+    }
+};
+
+// x' for one 256-block from its loaded elements: lane holds 4 consecutive elements
+__device__ __forceinline__ void rotate_block_lane(const BlockLane &in, int lane, float (&v)[4]) {
+    const f32x4 xv = in.x, cv = in.c;
     v[0] = xv.x * cv.x; v[1] = xv.y * cv.y; v[2] = xv.z * cv.z; v[3] = xv.w * cv.w;
     // h = 1, 2 inside the lane
     { const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3]; v[0] = a0 + b0; v[1] = a0 - b0; v[2] = a1 + b1; v[3] = a1 - b1; }
@@ -48,10 +57,9 @@ __device__ __forceinline__ int half_wave_sum(int v) {
 
 // one 256-block to 8 bits per 128 columns: lane l gets the packed int8 of x' elements 4l..4l+3, the scale of its
 // half (max |x'| / 127, correctly rounded) and the integer sum of its four values
-__device__ __forceinline__ void quantize_block_q8_128(const float *__restrict__ x, const float *__restrict__ ic, int lane, uint32_t &packed,
-                                                      float &dd, int &sum) {
+__device__ __forceinline__ void quantize_loaded_q8_128(const BlockLane &in, int lane, uint32_t &packed, float &dd, int &sum) {
     float v[4];
-    rotate_block_lane(x, ic, lane, v);
+    rotate_block_lane(in, lane, v);
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     am = half_wave_max(am);
     dd = div_rn(am, 127.f);
@@ -61,6 +69,13 @@ __device__ __forceinline__ void quantize_block_q8_128(const float *__restrict__ 
 #pragma unroll
     for (int e = 0; e < 4; ++e) { qi[e] = __float2int_rn(v[e] * id); sum += qi[e]; }
     packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+}
+
+__device__ __forceinline__ void quantize_block_q8_128(const float *__restrict__ x, const float *__restrict__ ic, int lane, uint32_t &packed,
+                                                      float &dd, int &sum) {
+    BlockLane in;
+    in.load(x, ic, lane);
+    quantize_loaded_q8_128(in, lane, packed, dd, sum);
 }
 
 }  // namespace p8x

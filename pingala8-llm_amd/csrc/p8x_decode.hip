@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
     __shared__ __align__(16) uint32_t tab[kTabWords];
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hs = lane >> 5, j = lane & 31;
     const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
-    build_coset_table(tab, a.a2, tid, kDecThreads);
+    build_coset_table<kDecThreads>(tab, a.a2, tid);
     __syncthreads();
     size_t first, last;
     wg_range(a, first, last);

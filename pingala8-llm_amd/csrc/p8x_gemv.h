@@ -33,6 +33,7 @@ struct GemvJob {
     const uint32_t *M;
     const uint16_t *S;               // row scales regrouped by row group: [ng][nb][32]
     const uint32_t *D; const int16_t *prm;
+    const uint16_t *prmd;            // prm with bit 15 set on rows that carry clamp-delta entries
     const int *cp; const uint16_t *cc; const float *cv;
     const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32]
                                      // (Q8_128 with q null: each task quantizes its chunk of x itself, with ic)
@@ -57,6 +58,7 @@ __host__ __device__ constexpr int kchunk_max(int ncol) { return kXBytes / (512 *
 template <int NCOL, int ACT>
 struct GemvSmem {
     static constexpr int kScales = NCOL * (ACT == P8X_ACT_Q8_128 ? 2 : 8) * kchunk_max(NCOL);
+    static constexpr int kXW = kXBytes / 4 / NCOL, kNSC = kScales / NCOL;   // per-column strides of xq, xd
     uint32_t tab[kTabWords];   // first member: LDS address 0, so table addresses need no base add
     uint32_t xq[kXBytes / 4];  // [ncol][kchunk][2][64] words (step order) or [ncol][kchunk][64] words
     float xd[kScales];         // [ncol][scales of the chunk]
@@ -91,13 +93,12 @@ struct TaskCtx {
 template <int ACT, bool PARTIALS>
 __host__ __device__ constexpr bool gemv_step_order() { return ACT == P8X_ACT_Q8_128 && !PARTIALS; }
 
-template <int NCOL, int ACT, bool PARTIALS, int C>
-__device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, const RawSlice<C> &raw,
-                                          int b, float (&yacc)[NCOL]) {
+template <int NCOL, int ACT, bool PARTIALS, int C, typename SM>
+__device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const SM &sm, const RawSlice<C> &raw, int b, float (&yacc)[NCOL]) {
     constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
     constexpr int NSUB = ACT == P8X_ACT_Q8_128 ? 1 : 4;   // integer sums per lane-slice
-    constexpr int XW = kXBytes / 4 / NCOL;                 // LDS words per column
-    constexpr int NSC = GemvSmem<NCOL, ACT>::kScales / NCOL;
+    constexpr int XW = SM::kXW;                            // LDS words per column
+    constexpr int NSC = SM::kNSC;
     LaneSlice<C> ls;
     ls.from_raw(raw, c.j);
     ls.prepare(c.bankbytes);
@@ -200,11 +201,11 @@ __device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C
 
 // One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
 // order, only summed in another order.
-template <int NCOL, int C>
-__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const GemvSmem<NCOL, P8X_ACT_Q8_128> &sm,
-                                               const StepSlice<C> &raw, int b, float (&yacc)[NCOL]) {
-    constexpr int XW = kXBytes / 4 / NCOL;
-    constexpr int NSC = GemvSmem<NCOL, P8X_ACT_Q8_128>::kScales / NCOL;
+template <int NCOL, int C, typename SM>
+__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const SM &sm, const StepSlice<C> &raw, int b,
+                                               float (&yacc)[NCOL]) {
+    constexpr int XW = SM::kXW;
+    constexpr int NSC = SM::kNSC;
     const int bl = b - c.b0;
     // the tile's activation base in one register: left to itself the compiler folds the array's LDS offset
     // (64 KB, past the table) into every read, which then does not fit the read's offset field
@@ -222,8 +223,8 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
 // one is decoded. Every step issues its prefetch (past the run's end through an empty resource, which reads
 // zeros without memory traffic), so the loop body is straight-line and the wait counts stay exact.
 // Returns the first block after the run.
-template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C>
-__device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const GemvSmem<NCOL, ACT> &sm, int b, int bend, float (&yacc)[NCOL]) {
+template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C, typename SM>
+__device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const SM &sm, int b, int bend, float (&yacc)[NCOL]) {
     constexpr int NW = nw_of(C);
     const GemvJob &J = *c.J;
     const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)c.g * J.nb;   // tile words: scalar loads
@@ -361,7 +362,7 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
-    build_coset_table(sm.tab, a2, tid, NT);
+    build_coset_table<NT>(sm.tab, a2, tid);
     int jc = 0;
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
         if constexpr (MULTI)
@@ -462,6 +463,104 @@ static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, in
         hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
     }
     return hip_check(hipGetLastError(), "k_gemv launch");
+}
+
+// ------------------------------------------------------------------------------------------------ single GEMV, latency path
+// One column of 8-bit-per-128 activations, one linear per launch (the drop-in p8x_mul_mat_vec call). Such a
+// launch has few tiles, so latency rules: a workgroup takes whole 32-row groups over the whole K, quantizes the
+// activations itself into LDS once (the prep's arithmetic, one wave per block), its waves split K into
+// contiguous block ranges, and the partial rows meet in LDS in a fixed order: no cross-workgroup fix-up.
+constexpr int kRgWaves = 16;
+constexpr int kRgMaxBlocks = 112;                   // K up to 28672
+constexpr int kRgQ = kRgMaxBlocks / kRgWaves;       // activation blocks per wave at most
+
+struct RgSmem {
+    static constexpr int kXW = kRgMaxBlocks * 128, kNSC = 2 * kRgMaxBlocks;
+    uint32_t tab[kTabWords];             // LDS address 0
+    uint32_t xq[kRgMaxBlocks * 128];     // [block][half][64 words] (step order)
+    float xd[2 * kRgMaxBlocks];          // [block][half]
+    float red[2][kRgWaves][32];          // per wave: its K range's row sums (two sets, alternating row groups)
+};
+
+template <int CM>
+__global__ __launch_bounds__(64 * kRgWaves) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
+    __shared__ RgSmem sm;
+    const GemvJob &J = job;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    TaskCtx<1, P8X_ACT_Q8_128> c;
+    c.J = &J;
+    c.hs = lane >> 5; c.j = lane & 31;
+    c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
+    c.xlane = c.hs * 64 + c.j;
+    c.b0 = 0; c.nbl = J.nb;
+    // the wave's activation blocks: every load first, the table meanwhile, then the quantization
+    BlockLane in[kRgQ];
+#pragma unroll
+    for (int i = 0; i < kRgQ; ++i)
+        if (w + i * kRgWaves < J.nb) in[i].load(J.x + 256 * (w + i * kRgWaves), J.ic + 256 * (w + i * kRgWaves), lane);
+    build_coset_table<64 * kRgWaves>(sm.tab, a2, tid);
+#pragma unroll
+    for (int i = 0; i < kRgQ; ++i) {
+        const int bl = w + i * kRgWaves;
+        if (bl < J.nb) {
+            uint32_t packed;
+            float dd;
+            int qs;
+            quantize_loaded_q8_128(in[i], lane, packed, dd, qs);
+            uint32_t *xw = sm.xq + bl * 128 + (lane >> 5) * 64 + (lane & 31);
+            xw[0] = packed;
+            xw[32] = packed;
+            if ((lane & 31) == 0) sm.xd[2 * bl + (lane >> 5)] = dd;
+        }
+    }
+    __syncthreads();
+    const int per = J.nb / kRgWaves, rem = J.nb % kRgWaves;
+    const int b0 = w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);
+    int set = 0;
+    for (int g = blockIdx.x; g < J.ng; g += gridDim.x, set ^= 1) {
+        c.g = g;
+        // the output row, read before the tile loads so that the epilogue finds it in a register
+        int ro = 0;
+        if (w == 0 && lane < 32) ro = as_global(J.prmd)[32 * g + lane];
+        float yacc[1] = {0.f};
+        for (int b = b0; b < b1;) {
+            const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
+            switch (mt >> 29) {
+                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 1, gemv_nbuf(1, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 2, gemv_nbuf(1, 2), CM == (1 << 2)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 3, gemv_nbuf(1, 3), CM == (1 << 3)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 4, gemv_nbuf(1, 4), CM == (1 << 4)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 5, gemv_nbuf(1, 5), CM == (1 << 5)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 6, gemv_nbuf(1, 6), CM == (1 << 6)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 7, gemv_nbuf(1, 7), CM == (1 << 7)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                default: ++b; break;   // class 0: zero weights
+            }
+        }
+        yacc[0] += __shfl_xor(yacc[0], 32);
+        if (lane < 32) sm.red[set][w][lane] = yacc[0];
+        // one barrier per row group: a wave writes this set again two groups later, after wave 0 has passed the
+        // next group's barrier, so wave 0 has read it by then
+        __syncthreads();
+        if (w == 0 && lane < 32) {
+            float v = 0.f;
+            for (int i = 0; i < kRgWaves; ++i) v += sm.red[set][i][lane];
+            const int r = ro & 0x7FFF;
+            if (ro & 0x8000) {
+                const gptr<const float> xr = as_global(J.x);
+                for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) v += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
+            }
+            as_global_rw(J.y)[r] = v;
+        }
+    }
+}
+
+template <int CM>
+static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
+    // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups, one per CU
+    const int per = (ng + num_cus() - 1) / num_cus();
+    hipLaunchKernelGGL((k_gemv_rg<CM>), dim3((ng + per - 1) / per), dim3(64 * kRgWaves), 0, st, job, a2);
+    return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 
 // ------------------------------------------------------------------------------------------------ wave-independent GEMV
@@ -590,7 +689,7 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, const uint32_t 
     constexpr int WAVES = wave_waves(CM);
     __shared__ WaveSmem<WAVES> sm;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    build_coset_table(sm.tab, a2, tid, 64 * WAVES);
+    build_coset_table<64 * WAVES>(sm.tab, a2, tid);
     // the slot's base in one register (it lies past the 64 KB table, beyond the LDS offset field)
     __attribute__((address_space(3))) uint32_t *slot = (__attribute__((address_space(3))) uint32_t *)sm.xs[w];
     __asm__ volatile("" : "+v"(slot));
@@ -643,6 +742,7 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, const ui
 int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
+int launch_gemv_rg(int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
 int launch_gemv_wave(int cm, const GemvJob *jobs, const GemvJob &job0, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2,
                      hipStream_t st);
 

@@ -46,8 +46,10 @@ __global__ __launch_bounds__(64) void k_act_q8_128(const float *__restrict__ x, 
 __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
                                                  uint8_t *__restrict__ blocks) {
     const int b = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    BlockLane in;
+    in.load(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane);
     float v[4];
-    rotate_block_lane(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane, v);
+    rotate_block_lane(in, lane, v);
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
@@ -98,7 +100,7 @@ GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
 static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
                      float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int gpt, int task0) {
     g = GemvJob{};
-    g.M = t->M; g.S = t->Sg; g.D = t->D; g.prm = t->prm;
+    g.M = t->M; g.S = t->Sg; g.D = t->D; g.prm = t->prm; g.prmd = t->prmd;
     g.cp = t->cp; g.cc = t->cc; g.cv = t->cv;
     g.q = q; g.d = d; g.x = x; g.ldx = (unsigned)ldx; g.y = y; g.ldy = (unsigned)ldy; g.partials = partials;
     g.wpart = t->wpart; g.wcnt = t->wcnt;
@@ -128,6 +130,11 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
             if (rc) return rc;
         }
         return P8X_OK;
+    }
+    if (ncols == 1 && act == P8X_ACT_Q8_128 && !q && t->nb <= kRgMaxBlocks) {   // one linear, x quantized in the launch
+        GemvJob job0;
+        fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, 1, t->nb, 1, 0);
+        return launch_gemv_rg(cm, job0, t->ng, t->a2, st);
     }
     const GemvPlan p = gemv_plan(t, ncols, act, false);
     if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");

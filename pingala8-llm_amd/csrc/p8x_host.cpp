@@ -97,7 +97,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
     for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->dbits, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
-                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->wx16, (void *)t->wmm})
+                    (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
 }
@@ -256,6 +256,12 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
             if (cp[r + 1] > cp[r]) { bits[r >> 5] |= 1u << (r & 31); t->dorig.push_back(r); }
         if ((rc = alloc((void **)&t->dbits, 4 * bits.size(), "delta row bits"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->dbits, bits.data(), 4 * bits.size(), hipMemcpyHostToDevice), "p8x_prepare: delta row bits"))) return fail(rc);
+    }
+    {   // sorted row -> original row with the delta flag: the single-GEMV epilogue needs one load per row
+        std::vector<uint16_t> pd(rows);
+        for (int r = 0; r < rows; ++r) pd[r] = (uint16_t)((uint16_t)prm[r] | (cp[prm[r] + 1] > cp[prm[r]] ? 0x8000u : 0u));
+        if ((rc = alloc((void **)&t->prmd, 2 * (size_t)rows, "flagged permutation"))) return fail(rc);
+        if ((rc = hip_check(hipMemcpy(t->prmd, pd.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: flagged permutation"))) return fail(rc);
     }
     std::vector<int> drows;
     for (int r = 0; r < rows; ++r) if (cp[r + 1] > cp[r]) drows.push_back(r);

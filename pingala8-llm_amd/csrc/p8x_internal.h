@@ -24,6 +24,7 @@ struct p8x_tensor {
     const int16_t *prm = nullptr;
     uint16_t *Sg = nullptr;          // row scales regrouped [ng][nb][32]: a row group's scales in one run
     int16_t *pinv = nullptr;         // original row -> sorted row (built at prepare)
+    uint16_t *prmd = nullptr;        // sorted row -> original row, bit 15 set when that row carries clamp-delta entries
     bool prm_identity = false;
     // device metadata built at prepare
     uint32_t *a2 = nullptr;          // [2][256]: A[f] + h c (bytewise), h-major

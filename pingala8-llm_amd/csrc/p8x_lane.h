@@ -25,13 +25,20 @@ constexpr int kTabWords = 256 * 64;   // 64 KB coset table
 constexpr int kTabBytes = kTabWords * 4;
 
 // Fill the replicated table from a2 = [h][256] words (h-major), all threads of the block.
-__device__ __forceinline__ void build_coset_table(uint32_t *tab, const uint32_t *__restrict__ a2, int tid, int nthreads) {
+template <int NT>
+__device__ __forceinline__ void build_coset_table(uint32_t *tab, const uint32_t *__restrict__ a2, int tid) {
+    static_assert((kTabWords / 4) % NT == 0, "table build: threads must divide the table's 16-byte entries");
+    constexpr int PER = kTabWords / 4 / NT;
     uint4 *t4 = reinterpret_cast<uint4 *>(tab);
-    for (int i = tid; i < kTabWords / 4; i += nthreads) {
-        const int f = i >> 4, h = (i >> 3) & 1;
-        const uint32_t v = a2[h * 256 + f];
-        t4[i] = make_uint4(v, v, v, v);
+    // every load first, then the stores: one memory round trip for the whole table
+    uint32_t v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = tid + k * NT;
+        v[k] = ((const __attribute__((address_space(1))) uint32_t *)a2)[((i >> 3) & 1) * 256 + (i >> 4)];
     }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) t4[tid + k * NT] = make_uint4(v[k], v[k], v[k], v[k]);
 }
 
 // global address-space views: pointers read out of descriptors are generic; these make loads global_load
