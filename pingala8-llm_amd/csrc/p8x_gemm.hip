@@ -31,7 +31,6 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 constexpr int kMmRows = 256;     // weight rows per workgroup tile (4 waves x 2 row groups)
 constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles of 32)
 constexpr int kMmThreads = 256;
-constexpr int kXcds = 8;          // MI355X: 8 accelerator dies, each with its own L2
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the

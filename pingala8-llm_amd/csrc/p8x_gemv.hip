@@ -151,15 +151,12 @@ struct ActJob {
     int blk0;              // first 256-block of this job in the launch
 };
 
-// grid (total blocks, ncols), block 64: the k_act_q8_128 body for a list of jobs
-__global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restrict__ jobs, int njobs) {
-    const int gb = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    int lo = 0, hi = njobs - 1;   // last job with blk0 <= gb
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (jobs[mid].blk0 <= gb) lo = mid; else hi = mid - 1;
-    }
-    const ActJob J = jobs[lo];
+// grid (ceil(total blocks / 4), ncols), block 256: the k_act_q8_128 body for a list of jobs, one 256-block per
+// wave; blk_job gives each block's job
+__global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int total) {
+    const int gb = 4 * blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = blockIdx.y, lane = threadIdx.x & 63;
+    if (gb >= total) return;
+    const ActJob &J = jobs[as_const(blk_job)[gb]];
     const int b = gb - J.blk0;
     uint32_t packed;
     float dd;
@@ -169,54 +166,56 @@ __global__ __launch_bounds__(64) void k_act_q8_128_batch(const ActJob *__restric
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
-// Finishing launch of a one-column grouped GEMV. The first blocks take 1024 original rows of one job each (4 per
-// thread, loads issued together): row ro gathers the K-chunk partials of its sorted row pinv[ro] in chunk order
-// and is written in place. Rows that carry clamp-delta entries (a bitmap says which) are left to the last blocks,
-// one thread per such row, which add the delta entries after the partials (the order and arithmetic of the
-// single-launch fix-up).
+// Finishing launch of a one-column grouped GEMV. The first blocks take 1024 sorted rows of one job each (4 per
+// thread, loads issued together): sorted row r sums its K-chunk partials in chunk order (coalesced reads) and is
+// written to its original row prmd[r] (a scatter inside the job's output). Rows that carry clamp-delta entries
+// (bit 15 of prmd) are left to the last blocks, one thread per such row, which add the delta entries after the
+// partials (the order and arithmetic of the single-launch fix-up).
+// Every block of a job runs on one XCD (workgroups go to XCDs round robin by index: block 8k + x runs on XCD x),
+// so the job's output lines fill in one L2. Block table entries: job | 1024-row block of the job << 24, or
+// kFinNone for padding.
 constexpr int kFinRows = 1024;
+constexpr uint32_t kFinNone = 0xFFFFFFFFu;
 
 struct FinishJob {
-    const float *wpart; const int16_t *pinv; const uint32_t *dbits;
+    const float *wpart; const int16_t *pinv; const uint16_t *prmd;
     const int *cp; const uint16_t *cc; const float *cv; const float *x;
     float *y;
-    int rows, nks, blk0;
+    int rows, nks;
 };
-
-__device__ __forceinline__ float finish_row(const FinishJob &J, int r) {
-    const gptr<const float> wp = as_global(J.wpart);
-    float v = 0.f;
-    for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
-    return v;
-}
 
 __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
                                                      const int2 *__restrict__ drows, int ndrows) {
     if ((int)blockIdx.x < nplain) {
-        const FinishJob &J = jobs[as_const(blk_job)[blockIdx.x]];
-        const int ro0 = ((int)blockIdx.x - J.blk0) * kFinRows + threadIdx.x;
+        const uint32_t e = as_const(blk_job)[blockIdx.x];
+        if (e == kFinNone) return;
+        const FinishJob &J = jobs[e & 0xFFFFFFu];
+        const int r0 = (int)(e >> 24) * kFinRows + threadIdx.x;
+        const gptr<const float> wp = as_global(J.wpart);
         int r[4];
-        uint32_t bits[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ro = min(ro0 + 256 * i, J.rows - 1);
-            r[i] = as_global(J.pinv)[ro];
-            bits[i] = as_global(J.dbits)[ro >> 5];
-        }
+        uint32_t pd[4];
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = finish_row(J, r[i]);
-#pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int ro = ro0 + 256 * i;
-            if (ro < J.rows && !((bits[i] >> (ro & 31)) & 1u)) as_global_rw(J.y)[ro] = v[i];
+            r[i] = min(r0 + 256 * i, J.rows - 1);
+            pd[i] = as_global(J.prmd)[r[i]];
+            v[i] = 0.f;
         }
+        for (int ks = 0; ks < J.nks; ++ks)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += wp[(size_t)ks * J.rows + r[i]];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[pd[i]] = v[i];
     } else {
         const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
         if (i >= ndrows) return;
         const FinishJob &J = jobs[drows[i].x];
         const int ro = drows[i].y;
-        float v = finish_row(J, as_global(J.pinv)[ro]);
+        const int r = as_global(J.pinv)[ro];
+        const gptr<const float> wp = as_global(J.wpart);
+        float v = 0.f;
+        for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
         if (J.x) {
             const gptr<const float> x = as_global(J.x);
             for (int e = as_global(J.cp)[ro]; e < as_global(J.cp)[ro + 1]; ++e) v += as_global(J.cv)[e] * x[as_global(J.cc)[e]];
@@ -239,6 +238,7 @@ struct p8x_gemv_batch {
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
     p8x::ActJob *d_act = nullptr;
+    uint32_t *d_ablk = nullptr;        // activation prep: 256-block -> job
     void *work = nullptr;   // activations, partial rows and counters of every job
 };
 
@@ -250,6 +250,7 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
     if (!b) return;
     if (b->d_jobs) (void)hipFree(b->d_jobs);
     if (b->d_act) (void)hipFree(b->d_act);
+    if (b->d_ablk) (void)hipFree(b->d_ablk);
     if (b->d_ujob) (void)hipFree(b->d_ujob);
     if (b->d_fin) (void)hipFree(b->d_fin);
     if (b->d_fblk) (void)hipFree(b->d_fblk);
@@ -261,6 +262,7 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
 int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                           float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out) {
     if (!tensors || !x || !ldx || !y || !ldy || !out || njobs < 1) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: bad arguments");
+    if (njobs >= (1 << 24)) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: %d jobs (at most %d)", njobs, (1 << 24) - 1);
     if (ncols < 1 || ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: ncols %d", ncols);
     *out = nullptr;
     size_t hist[8] = {0};
@@ -282,6 +284,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
     const size_t off_ctr = take(kWaveCtrBytes);
     int blk0 = 0;
+    std::vector<uint32_t> ablk;   // activation prep: 256-block -> job
     const int cm = class_set(hist);
     // one column: wave-independent units (row group, whole K); more: workgroup tasks of gpt row groups over
     // K-chunks that fit the LDS activation buffer
@@ -317,13 +320,14 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, 0);
         act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
         blk0 += t->nb;
+        ablk.insert(ablk.end(), (size_t)t->nb, (uint32_t)i);
     }
     p8x_gemv_batch *b = new p8x_gemv_batch();
     b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_blocks = blk0; b->wave = wave;
     b->a2 = tensors[0]->a2;
     int rc;
     if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||
-        hipMalloc((void **)&b->d_act, sizeof(ActJob) * njobs) != hipSuccess) {
+        hipMalloc((void **)&b->d_act, sizeof(ActJob) * njobs) != hipSuccess || hipMalloc((void **)&b->d_ablk, 4 * (size_t)blk0) != hipSuccess) {
         p8x_gemv_batch_release(b);
         return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: hipMalloc");
     }
@@ -352,13 +356,27 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         for (int i = 0; i < njobs; ++i)
             for (int u = 0; u < jobs[i].ntasks; ++u) uj[(size_t)jobs[i].task0 + u] = (uint32_t)i;
         std::vector<FinishJob> fin(njobs);
-        std::vector<uint32_t> fblk;
         std::vector<int2> fdr;
+        // jobs to XCDs, largest first onto the least loaded; then block 8k + x = the k-th block of XCD x's jobs
+        std::vector<std::vector<uint32_t>> xb(kXcds);
+        std::vector<int> order(njobs);
+        for (int i = 0; i < njobs; ++i) order[i] = i;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return jobs[a].rows > jobs[c].rows; });
+        for (int i : order) {
+            const GemvJob &g = jobs[i];
+            size_t x = 0;
+            for (size_t k = 1; k < xb.size(); ++k) if (xb[k].size() < xb[x].size()) x = k;
+            for (int r = 0, s = 0; r < g.rows; r += kFinRows, ++s) xb[x].push_back((uint32_t)i | ((uint32_t)s << 24));
+        }
+        size_t per = 0;
+        for (const auto &l : xb) per = std::max(per, l.size());
+        std::vector<uint32_t> fblk(kXcds * per, kFinNone);
+        for (int x = 0; x < kXcds; ++x)
+            for (size_t k = 0; k < xb[x].size(); ++k) fblk[kXcds * k + x] = xb[x][k];
         for (int i = 0; i < njobs; ++i) {
             const GemvJob &g = jobs[i];
             const p8x_tensor *t = tensor_of[g.M];
-            fin[i] = FinishJob{g.wpart, t->pinv, t->dbits, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks, (int)fblk.size()};
-            for (int r = 0; r < g.rows; r += kFinRows) fblk.push_back((uint32_t)i);
+            fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks};
             for (int r : t->dorig) fdr.push_back(make_int2(i, r));
         }
         b->fin_blocks = (int)fblk.size();
@@ -387,7 +405,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     }
     if ((rc = hip_check(hipMemset(b->work, 0, bytes), "p8x_gemv_batch_create: clear")) ||
         (rc = hip_check(hipMemcpy(b->d_jobs, jobs.data(), sizeof(GemvJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: jobs")) ||
-        (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs"))) {
+        (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs")) ||
+        (rc = hip_check(hipMemcpy(b->d_ablk, ablk.data(), 4 * ablk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: act blocks"))) {
         p8x_gemv_batch_release(b);
         return rc;
     }
@@ -399,7 +418,8 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     if (!b) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run: null batch");
     hipStream_t st = (hipStream_t)stream;
     if (stage == 0) {
-        hipLaunchKernelGGL(k_act_q8_128_batch, dim3(b->total_blocks, b->ncols), dim3(64), 0, st, (const ActJob *)b->d_act, b->njobs);
+        hipLaunchKernelGGL(k_act_q8_128_batch, dim3((b->total_blocks + 3) / 4, b->ncols), dim3(256), 0, st, (const ActJob *)b->d_act,
+                           (const uint32_t *)b->d_ablk, b->total_blocks);
         return hip_check(hipGetLastError(), "k_act_q8_128_batch launch");
     }
     if (stage == 1) {

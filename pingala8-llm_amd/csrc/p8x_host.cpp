@@ -96,7 +96,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->dbits, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -250,13 +250,6 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         if ((rc = alloc((void **)&t->pinv, 2 * (size_t)rows, "pinv"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->pinv, pinv.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: pinv"))) return fail(rc);
     }
-    {   // original rows that carry clamp-delta entries: a bitmap and the host list
-        std::vector<uint32_t> bits(((size_t)rows + 31) / 32, 0u);
-        for (int r = 0; r < rows; ++r)
-            if (cp[r + 1] > cp[r]) { bits[r >> 5] |= 1u << (r & 31); t->dorig.push_back(r); }
-        if ((rc = alloc((void **)&t->dbits, 4 * bits.size(), "delta row bits"))) return fail(rc);
-        if ((rc = hip_check(hipMemcpy(t->dbits, bits.data(), 4 * bits.size(), hipMemcpyHostToDevice), "p8x_prepare: delta row bits"))) return fail(rc);
-    }
     {   // sorted row -> original row with the delta flag: the single-GEMV epilogue needs one load per row
         std::vector<uint16_t> pd(rows);
         for (int r = 0; r < rows; ++r) pd[r] = (uint16_t)((uint16_t)prm[r] | (cp[prm[r] + 1] > cp[prm[r]] ? 0x8000u : 0u));
@@ -266,6 +259,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     std::vector<int> drows;
     for (int r = 0; r < rows; ++r) if (cp[r + 1] > cp[r]) drows.push_back(r);
     t->ndrows = (int)drows.size();
+    t->dorig = drows;
     if ((rc = alloc((void **)&t->drows, 4 * std::max<size_t>(1, drows.size()), "delta row list"))) return fail(rc);
     if (!drows.empty() && (rc = hip_check(hipMemcpy(t->drows, drows.data(), 4 * drows.size(), hipMemcpyHostToDevice), "p8x_prepare: delta rows")))
         return fail(rc);

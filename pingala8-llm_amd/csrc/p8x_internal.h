@@ -41,7 +41,6 @@ struct p8x_tensor {
     size_t wpart_floats = 0;
     unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
     int *drows = nullptr;            // original rows that carry clamp-delta entries [ndrows]
-    uint32_t *dbits = nullptr;       // one bit per original row: the row carries clamp-delta entries [ceil(rows / 32)]
     std::vector<int> dorig;          // host: those original rows
     int ndrows = 0;
     uint16_t *wx16 = nullptr;        // prompt GEMM: rotated fp16 activations [N][K] (grown on demand)

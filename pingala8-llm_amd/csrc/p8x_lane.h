@@ -22,6 +22,8 @@
 namespace p8x {
 
 constexpr int kTabWords = 256 * 64;   // 64 KB coset table
+// gfx950 has 8 XCDs, each with its own L2; workgroups of a launch go to them round robin by index
+constexpr int kXcds = 8;
 constexpr int kTabBytes = kTabWords * 4;
 
 // Fill the replicated table from a2 = [h][256] words (h-major), all threads of the block.
