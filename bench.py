@@ -32,6 +32,10 @@ MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16/bf16 MFMA, MI355X
 LLAMA_LAYER = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096), ("attn_output", 4096, 4096),
                ("ffn_gate", 14336, 4096), ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
 HEAD_SHARDS = [("lm_head", 32064, 4096)] * 4
+QWEN3_14B_LAYER = [("attn_q", 5120, 5120), ("attn_k", 1024, 5120), ("attn_v", 1024, 5120), ("attn_output", 5120, 5120),
+                   ("ffn_gate", 17408, 5120), ("ffn_up", 17408, 5120), ("ffn_down", 5120, 17408)]
+QWEN3_4B_LAYER = [("attn_q", 4096, 2560), ("attn_k", 1024, 2560), ("attn_v", 1024, 2560), ("attn_output", 2560, 4096),
+                  ("ffn_gate", 9728, 2560), ("ffn_up", 9728, 2560), ("ffn_down", 2560, 9728)]
 CLASS_C3 = (0, 0, 0, 1, 0, 0, 0, 0)
 # B4 class mix per tensor kind (logs/cs_lfull_transcode.log): attn_v class 6, ffn_down 78.1% c3 / 12.5% c4 / 9.4% c2
 CLASS_B4 = {"attn_v": (0, 0, 0, 0, 0, 0, 1, 0), "ffn_down": (0, 0, 0.094, 0.781, 0.125, 0, 0, 0)}
@@ -86,6 +90,83 @@ def cpu_baseline(host0, seconds, threads):
     return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
             "sample": f"layer 0 of the stack (7 linears, {nbytes / 1e6:.1f} MB packed), {n} passes in {dt:.1f} s, "
                       f"q8 activations, reference core vr-native-cpu-core.h built {core.isa}"}
+
+
+def timed_steps(run, stream, warmup, steps):
+    """ms per call of run(), calls back to back after warmup, HIP events around the whole run"""
+    for _ in range(warmup):
+        run()
+    stream.sync()
+    e0, e1 = p8x.Event(), p8x.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        run()
+    e1.record(stream)
+    stream.sync()
+    return e0.elapsed_ms(e1) / steps
+
+
+def measure_qwen14b_columns(stream, steps, col_list=(1, 2, 4, 8)):
+    """Qwen3-14B (40 layers, 280 linears, all class 3) streamed by one grouped launch per step at 1/2/4/8
+    activation columns sharing the weights: GB/s of the weight stream and columns (tokens) per second"""
+    plan = [(r, K) for _ in range(40) for (_, r, K) in QWEN3_14B_LAYER]
+    tensors = [p8x.Tensor(p8x.synth_random(1000 + i, r, K, nd=1), r, K) for i, (r, K) in enumerate(plan)]
+    stream_bytes = sum(t.stream_bytes for t in tensors)
+    rng = np.random.default_rng(5)
+    out = {"workload": "qwen3-14b linear stack: 40 x (q,k,v,o,gate,up,down), class 3, one grouped launch per step",
+           "stream_bytes_per_step": int(stream_bytes)}
+    for n in col_list:
+        xs = {K: p8x.DeviceBuffer.from_numpy(rng.standard_normal(n * K).astype(np.float32)) for K in sorted({t.K for t in tensors})}
+        ys = [p8x.DeviceBuffer(4 * n * t.rows) for t in tensors]
+        batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ys, ncols=n)
+        ms = timed_steps(lambda: batch.run(stream), stream, 40, steps)
+        out[f"batch_{n}"] = {"ms_per_step": round(ms, 4), "GB/s": round(stream_bytes / (ms * 1e-3) / 1e9, 1),
+                             "tokens_per_s": round(n / (ms * 1e-3), 1)}
+        log(f"qwen3-14b batch {n}: {ms * 1e3:.1f} us/step, {stream_bytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+        batch.release()
+        for b in list(xs.values()) + ys:
+            b.free()
+    for t in tensors:
+        t.release()
+    return out
+
+
+def measure_qwen4b_layer(stream, steps, copies=20):
+    """Qwen3-4B one layer (7 linears, 26 MB), batch 1, rotating over 20 distinct copies (> 512 MB, so the MALL
+    does not hold the weights): one grouped launch per layer, and one p8x_mul_mat_vec call per linear"""
+    tensors = [[p8x.Tensor(p8x.synth_random(5000 + 7 * c + i, r, K, nd=1), r, K) for i, (_, r, K) in enumerate(QWEN3_4B_LAYER)]
+               for c in range(copies)]
+    layer_bytes = sum(t.stream_bytes for t in tensors[0])
+    rng = np.random.default_rng(6)
+    xs = {K: p8x.DeviceBuffer.from_numpy(rng.standard_normal(K).astype(np.float32)) for K in (2560, 4096, 9728)}
+    ys = [[p8x.DeviceBuffer(4 * t.rows) for t in layer] for layer in tensors]
+    batches = [p8x.GemvBatch(layer, [xs[t.K] for t in layer], y) for layer, y in zip(tensors, ys)]
+
+    def grouped():
+        for b in batches:
+            b.run(stream)
+
+    def per_linear():
+        for layer, y in zip(tensors, ys):
+            for t, yb in zip(layer, y):
+                t.mul_mat_vec_dev(xs[t.K], yb, stream=stream)
+
+    g_ms = timed_steps(grouped, stream, 10, steps) / copies
+    l_ms = timed_steps(per_linear, stream, 10, steps) / copies
+    log(f"qwen3-4b layer: grouped {g_ms * 1e3:.1f} us, per-linear {l_ms * 1e3:.1f} us per layer")
+    for b in batches:
+        b.release()
+    for layer, y in zip(tensors, ys):
+        for t in layer:
+            t.release()
+        for b in y:
+            b.free()
+    for b in xs.values():
+        b.free()
+    return {"workload": f"qwen3-4b one layer (q,k,v,o,gate,up,down), batch 1, {copies} distinct copies in rotation",
+            "stream_bytes_per_layer": int(layer_bytes),
+            "grouped_launch": {"us_per_layer": round(g_ms * 1e3, 2), "GB/s": round(layer_bytes / (g_ms * 1e-3) / 1e9, 1)},
+            "per_linear_launches": {"us_per_layer": round(l_ms * 1e3, 2), "GB/s": round(layer_bytes / (l_ms * 1e-3) / 1e9, 1)}}
 
 
 def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
@@ -212,6 +293,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM measurement")
+    ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -277,6 +359,13 @@ def main():
     per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
+    qwen14b = qwen4b = None
+    if not args.no_qwen:
+        batch.release()
+        for t in tensors:
+            t.release()
+        qwen14b = measure_qwen14b_columns(stream, max(10, args.steps // 4))
+        qwen4b = measure_qwen4b_layer(stream, max(10, args.steps // 4))
     cpu = None
     if not args.no_cpu and host0:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -300,6 +389,8 @@ def main():
         "per_linear_launches": per_linear,
         "prompt_gemm": gemm,
         "dequantize_f16": deq,
+        "qwen3_14b_columns": qwen14b,
+        "qwen3_4b_layer": qwen4b,
         "host_wall_s": round(wall, 3),
     }
     print(json.dumps(out), flush=True)

@@ -83,7 +83,7 @@ __host__ __device__ constexpr int gemv_wg_per_cu(int ncol, int act, bool partial
 
 template <int NCOL, int ACT>
 struct TaskCtx {
-    const GemvJob *J;   // the descriptor in place (kernel argument or the launch's job array): never copied
+    const GemvJob *J;   // the task's descriptor (kernel argument, or a copy of the launch's job array entry)
     int g, b0, nbl, hs, j;
     uint32_t bankbytes;
     int xlane;          // step order: the lane's word offset hs * 64 + j in a block's activation words
@@ -349,11 +349,10 @@ __device__ __forceinline__ void gemv_rows_out(const GemvJob &J, int g, int ks, i
     }
 }
 
-// MULTI: the launch walks a job array in global memory (grouped launch); else its one job is the kernel argument
-template <int NCOL, int ACT, bool PARTIALS, int CM, bool MULTI>
+template <int NCOL, int ACT, bool PARTIALS, int CM>
 __global__ __launch_bounds__(64 * gemv_waves(NCOL, ACT, PARTIALS, CM))
 __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu(NCOL, ACT, PARTIALS, CM), gemv_waves_per_eu(NCOL, ACT, PARTIALS, CM))))
-void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total_tasks, const uint32_t *__restrict__ a2) {
+void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
     __shared__ GemvSmem<NCOL, ACT> sm;   // static: the table sits at LDS address 0 at compile time
     constexpr int WAVES = gemv_waves(NCOL, ACT, PARTIALS, CM), NT = 64 * WAVES;
     constexpr int NSC = GemvSmem<NCOL, ACT>::kScales / NCOL;
@@ -363,11 +362,8 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
     build_coset_table<NT>(sm.tab, a2, tid);
-    int jc = 0;
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
-        if constexpr (MULTI)
-            while (task >= jobs[jc].task0 + jobs[jc].ntasks) ++jc;
-        const GemvJob &J = MULTI ? jobs[jc] : job0;
+        const GemvJob &J = job0;
         c.J = &J;
         const int local = task - J.task0, oct = local / J.nks, ks = local % J.nks;
         c.b0 = ks * J.kchunk;
@@ -453,15 +449,10 @@ void k_gemv(const GemvJob *__restrict__ jobs, GemvJob job0, int njobs, int total
 
 
 template <int NCOL, int ACT, bool PARTIALS, int CM>
-static int launch_gemv_t(const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+static int launch_gemv_t(const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
     constexpr int NT = 64 * gemv_waves(NCOL, ACT, PARTIALS, CM);
     const int grid = std::min(tasks, gemv_wg_per_cu(NCOL, ACT, PARTIALS, CM) * num_cus());
-    if (jobs) {   // grouped launches: one column runs the wave-independent kernel instead
-        if constexpr (NCOL == 1) return set_error(P8X_ERR_UNSUPPORTED, "k_gemv: one-column grouped launch");
-        else hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, true>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
-    } else {
-        hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM, false>), dim3(grid), dim3(NT), 0, st, jobs, job0, njobs, tasks, a2);
-    }
+    hipLaunchKernelGGL((k_gemv<NCOL, ACT, PARTIALS, CM>), dim3(grid), dim3(NT), 0, st, job0, tasks, a2);
     return hip_check(hipGetLastError(), "k_gemv launch");
 }
 
@@ -564,59 +555,72 @@ static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipS
 }
 
 // ------------------------------------------------------------------------------------------------ wave-independent GEMV
-// One column of 8-bit-per-128 activations (the decode-batch-1 stream), grouped launches only. Each wave is its own
-// worker: it takes a unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and
-// leaves the sorted-row partials for the finishing launch. It keeps each tile's activation block in a private
-// 512-byte LDS slot (loaded with the tile, written twice in a row so step-order reads need no wrap). Nothing
+// 1..8 columns of 8-bit-per-128 activations, grouped launches (the decode stream). Each wave is its own worker:
+// it takes a unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and leaves
+// the sorted-row partials for the finishing launch. It keeps each tile's activation blocks (one per column) in
+// a private LDS slot (loaded with the tile, written twice in a row so step-order reads need no wrap). Nothing
 // waits on another wave after the table is built, so a slow wave delays only its own unit and the launch
 // drains with at most one unit per wave. Units are numbered in job order; the job list is ordered by decreasing
 // unit length, so the long units start first.
-// Class 3 only fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; classes 6 or 2-4 8-wave workgroups at 4
-// (128 VGPRs), every class at 2.
-__host__ __device__ constexpr int wave_waves(int cm) { return cm == kCmC3 ? 16 : 8; }
-__host__ __device__ constexpr int wave_per_eu(int cm) { return cm == kCmC3 ? 8 : cm == kCmAll ? 2 : 4; }
-__host__ __device__ constexpr int wave_wg_per_cu(int cm) { return 4 * wave_per_eu(cm) / wave_waves(cm); }
+// One column of class 3 fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; one column of classes 6 or 2-4
+// 8-wave workgroups at 4 (128 VGPRs), every class at 2. Two to four columns: 16-wave workgroups (one per CU,
+// the slots take NCOL x 8 KB) at 4 waves per SIMD; five to eight columns (more than 128 VGPRs) and every class:
+// 8-wave workgroups at 2.
+__host__ __device__ constexpr int wave_waves(int cm, int ncol = 1) { return ncol > 4 ? 8 : cm == kCmC3 || (ncol > 1 && cm != kCmAll) ? 16 : 8; }
+__host__ __device__ constexpr int wave_per_eu(int cm, int ncol = 1) {
+    return ncol > 4 ? 2 : ncol > 1 ? (cm == kCmAll ? 2 : 4) : cm == kCmC3 ? 8 : cm == kCmAll ? 2 : 4;
+}
+__host__ __device__ constexpr int wave_wg_per_cu(int cm, int ncol = 1) { return 4 * wave_per_eu(cm, ncol) / wave_waves(cm, ncol); }
+// prefetch depth of the class-3 runs (register buffers hold NCOL activation words and scales each)
+__host__ __device__ constexpr int wave_nbuf_c3(int ncol) { return ncol == 1 ? GEMV_NBUF_C3 : 2; }
 
-template <int WAVES>
+template <int WAVES, int NCOL>
 struct WaveSmem {
-    uint32_t tab[kTabWords];     // LDS address 0
-    uint32_t xs[WAVES][128];     // per wave: [half][64 words], word i = activation word (i & 31) of the half
+    uint32_t tab[kTabWords];            // LDS address 0
+    uint32_t xs[WAVES][NCOL * 128];     // per wave: [column][half][64 words], word i = activation word (i & 31)
 };
 
-// A tile's payload with its activation block: one word per lane (word `lane` of the block) and the half's scale
-template <int C>
+// A tile's payload with its activation blocks: per column one word per lane (word `lane` of the block) and the
+// lane's half's scale
+template <int C, int NCOL>
 struct WaveSlice {
     StepSlice<C> p;
-    uint32_t xw;
-    float xd;
+    uint32_t xw[NCOL];
+    float xd[NCOL];
 };
 
-// One tile of a wave: the activation block goes to the wave's slot, then the step-order integer sums.
-template <int C>
+// One tile of a wave: the activation blocks go to the wave's slot, then the step-order integer sums.
+template <int C, int NCOL>
 __device__ __forceinline__ void wave_tile(const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot, int lane,
-                                          const WaveSlice<C> &r_, float &yacc) {
+                                          const WaveSlice<C, NCOL> &r_, float (&yacc)[NCOL]) {
     const int hs = lane >> 5, j = lane & 31;
-    WaveSlice<C> r = r_;
+    WaveSlice<C, NCOL> r = r_;
     pin(r.p.w);
     pin(r.p.s);
     pin(r.xw);
-    pin(r.xd);
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) pin(r.xd[n]);
     // lanes read each other's words: the slot is this wave's alone and LDS operations of one wave run in order,
     // so compiler barriers on both sides of the writes are all the ordering needed (without them the compiler
     // may move reads of words other lanes write across the writes)
     __asm__ volatile("" ::: "memory");
-    slot[hs * 64 + j] = r.xw;
-    slot[hs * 64 + 32 + j] = r.xw;
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) {
+        slot[n * 128 + hs * 64 + j] = r.xw[n];
+        slot[n * 128 + hs * 64 + 32 + j] = r.xw[n];
+    }
     __asm__ volatile("" ::: "memory");
-    int isum[1];
-    step_isum<1, C, 0>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, slot + hs * 64 + j, isum);
-    yacc += ((float)isum[0] * r.xd) * half_to_float(r.p.s);
+    int isum[NCOL];
+    step_isum<NCOL, C, 128>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, slot + hs * 64 + j, isum);
+    const float sc = half_to_float(r.p.s);
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) yacc[n] += ((float)isum[n] * r.xd[n]) * sc;
 }
 
 // a run of consecutive tiles of class C in row group g, NBUF tiles in flight (the gemv_run scheme)
-template <int C, int NBUF, bool ONLY_C>
+template <int C, int NBUF, bool ONLY_C, int NCOL>
 __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot,
-                                        int g, int b, int bend, int lane, float &yacc) {
+                                        int g, int b, int bend, int lane, float (&yacc)[NCOL]) {
     const int hs = lane >> 5, j = lane & 31;
     const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)g * J.nb;
     int e = bend;
@@ -625,22 +629,27 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
         while (e < bend && (mrow[e] >> 29) == (uint32_t)C) ++e;
     }
     constexpr int NW = nw_of(C);
-    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)J.K, dbytes = (uint32_t)J.nsl * 4u;
+    // activations [NCOL][K] int8 and scales [NCOL][K / 128]
+    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.K), dbytes = (uint32_t)(NCOL * J.nsl) * 4u;
     const uint32_t vo = (uint32_t)(hs * NW * 128 + 8 * j), vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)lane, vd = 4u * (uint32_t)hs;
     uint32_t wn = mrow[b];
-    auto issue = [&](WaveSlice<C> &r, int ta) {
+    auto issue = [&](WaveSlice<C, NCOL> &r, int ta) {
         const bool ok = ta < e;
         const int tc = ok ? ta : b;
         const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
         const uint32_t soff = ((uint32_t)g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
         // past the run's end the resources have no records: the loads read zeros without memory traffic
         r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
-        r.xw = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(J.q, ok ? qbytes : 0u), vq, 256u * (uint32_t)tc, 0);
-        r.xd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(J.d, ok ? dbytes : 0u), vd, 8u * (uint32_t)tc, 0));
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u), rd = buffer_rsrc(J.d, ok ? dbytes : 0u);
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) {
+            r.xw[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
+            r.xd[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vd, 8u * (uint32_t)tc + 4u * (uint32_t)(n * J.nsl), 0));
+        }
         wn = mrow[min(ta + 1, e - 1)];
     };
-    auto tile = [&](const WaveSlice<C> &r) { wave_tile<C>(tab, slot, lane, r, yacc); };
-    WaveSlice<C> buf[NBUF];
+    auto tile = [&](const WaveSlice<C, NCOL> &r) { wave_tile<C, NCOL>(tab, slot, lane, r, yacc); };
+    WaveSlice<C, NCOL> buf[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
     int base = b;
@@ -671,23 +680,27 @@ __device__ __forceinline__ unsigned wave_atomic_add(unsigned *p, int lane) {
 }
 
 // A wave unit's rows: the half-slices meet through one cross-lane add, and lanes 0..31 store the row group's 32
-// sorted-row partials of K-chunk ks to wpart [nks][rows] (one 128-byte line, no loads, no atomics, so nothing
-// waits on the loads in flight). The batch's finishing launch sums the K-chunks in order, applies the clamp
-// delta and writes original rows.
-__device__ __forceinline__ void wave_rows_store(const GemvJob &J, int g, int ks, int lane, float yacc) {
-    yacc += __shfl_xor(yacc, 32);
-    if (lane < 32) as_global_rw(J.wpart)[(size_t)ks * J.rows + 32 * g + lane] = yacc;
+// sorted-row partials of K-chunk ks to wpart [nks][NCOL][rows] (one 128-byte line per column, no loads, no
+// atomics, so nothing waits on the loads in flight). The batch's finishing launch sums the K-chunks in order,
+// applies the clamp delta and writes original rows.
+template <int NCOL>
+__device__ __forceinline__ void wave_rows_store(const GemvJob &J, int g, int ks, int lane, float (&yacc)[NCOL]) {
+#pragma unroll
+    for (int n = 0; n < NCOL; ++n) {
+        const float v = yacc[n] + __shfl_xor(yacc[n], 32);
+        if (lane < 32) as_global_rw(J.wpart)[((size_t)ks * NCOL + n) * J.rows + 32 * g + lane] = v;
+    }
 }
 
 // ctr[part * kWaveCtrStride + 0]: units the partition has handed out beyond the first round; + 1: waves that have
 // left. Both start at 0 and the partition's last wave to leave puts them back, so launches on one stream reuse
 // them (concurrent launches that share the counters race).
-template <int CM, bool MULTI>
-__global__ __launch_bounds__(64 * wave_waves(CM)) __attribute__((amdgpu_waves_per_eu(wave_per_eu(CM), wave_per_eu(CM))))
-void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, const uint32_t *__restrict__ ujob, int total_units, unsigned *ctr,
+template <int CM, int NCOL>
+__global__ __launch_bounds__(64 * wave_waves(CM, NCOL)) __attribute__((amdgpu_waves_per_eu(wave_per_eu(CM, NCOL), wave_per_eu(CM, NCOL))))
+void k_gemv_wave(const GemvJob *__restrict__ jobs, const uint32_t *__restrict__ ujob, int total_units, unsigned *ctr,
                  const uint32_t *__restrict__ a2) {
-    constexpr int WAVES = wave_waves(CM);
-    __shared__ WaveSmem<WAVES> sm;
+    constexpr int WAVES = wave_waves(CM, NCOL);
+    __shared__ WaveSmem<WAVES, NCOL> sm;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     build_coset_table<64 * WAVES>(sm.tab, a2, tid);
     // the slot's base in one register (it lies past the 64 KB table, beyond the LDS offset field)
@@ -701,25 +714,27 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, const uint32_t 
     // each later take waits for its atomic, which also drains the previous unit's stores: the tile loops start
     // with loads only in flight, so their wait counts stay exact
     for (int u = part + np * k; u < total_units; u = part + np * k) {
-        const int jc = MULTI ? (int)as_const(ujob)[u] : 0;
-        const GemvJob &J = MULTI ? jobs[jc] : job0;
+        const int jc = (int)as_const(ujob)[u];
+        const GemvJob &J = jobs[jc];
         const int local = u - J.task0, g = local / J.nks, ks = local % J.nks;
         const int b0 = ks * J.kchunk, bend = min(b0 + J.kchunk, J.nb);
-        float yacc[1] = {0.f};
+        float yacc[NCOL];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
         for (int b = b0; b < bend;) {
             const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
             switch (mt >> 29) {
-                case 1: if constexpr ((CM >> 1) & 1) { b = wave_run<1, 2, CM == (1 << 1)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 2: if constexpr ((CM >> 2) & 1) { b = wave_run<2, 2, CM == (1 << 2)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 3: if constexpr ((CM >> 3) & 1) { b = wave_run<3, GEMV_NBUF_C3, CM == (1 << 3)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 4: if constexpr ((CM >> 4) & 1) { b = wave_run<4, 2, CM == (1 << 4)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 5: if constexpr ((CM >> 5) & 1) { b = wave_run<5, 2, CM == (1 << 5)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 6: if constexpr ((CM >> 6) & 1) { b = wave_run<6, 2, CM == (1 << 6)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
-                case 7: if constexpr ((CM >> 7) & 1) { b = wave_run<7, 2, CM == (1 << 7)>(J, sm.tab, slot, g, b, bend, lane, yacc[0]); break; } [[fallthrough]];
+                case 1: if constexpr ((CM >> 1) & 1) { b = wave_run<1, 2, CM == (1 << 1), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = wave_run<2, 2, CM == (1 << 2), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = wave_run<3, wave_nbuf_c3(NCOL), CM == (1 << 3), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = wave_run<4, 2, CM == (1 << 4), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = wave_run<5, 2, CM == (1 << 5), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = wave_run<6, 2, CM == (1 << 6), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = wave_run<7, 2, CM == (1 << 7), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
                 default: ++b; break;   // class 0: zero weights
             }
         }
-        wave_rows_store(J, g, ks, lane, yacc[0]);
+        wave_rows_store<NCOL>(J, g, ks, lane, yacc);
         k = nwp + (int)wave_atomic_add(pc, lane);
     }
     const unsigned left = wave_atomic_add(pc + 1, lane);
@@ -729,21 +744,18 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, GemvJob job0, const uint32_t 
     }
 }
 
-template <int CM>
-static int launch_gemv_wave_t(const GemvJob *jobs, const GemvJob &job0, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2,
-                              hipStream_t st) {
-    const int grid = wave_wg_per_cu(CM) * num_cus();
-    if (jobs) hipLaunchKernelGGL((k_gemv_wave<CM, true>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, ujob, units, ctr, a2);
-    else hipLaunchKernelGGL((k_gemv_wave<CM, false>), dim3(grid), dim3(64 * wave_waves(CM)), 0, st, jobs, job0, ujob, units, ctr, a2);
+template <int CM, int NCOL>
+static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st) {
+    const int grid = wave_wg_per_cu(CM, NCOL) * num_cus();
+    hipLaunchKernelGGL((k_gemv_wave<CM, NCOL>), dim3(grid), dim3(64 * wave_waves(CM, NCOL)), 0, st, jobs, ujob, units, ctr, a2);
     return hip_check(hipGetLastError(), "k_gemv_wave launch");
 }
 
 // defined in the instantiation units
-int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
-int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
+int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
+int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
 int launch_gemv_rg(int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
-int launch_gemv_wave(int cm, const GemvJob *jobs, const GemvJob &job0, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2,
-                     hipStream_t st);
+int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
 
 }  // namespace p8x

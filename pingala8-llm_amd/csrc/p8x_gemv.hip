@@ -140,8 +140,8 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
     if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
     GemvJob job0;
     fill_job(job0, t, q, d, x, ldx, y, ldy, nullptr, p.nks, p.bpk, p.gpt, 0);
-    if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, nullptr, job0, 1, job0.ntasks, t->a2, st);
-    return launch_gemv_q81(ncols, nullptr, job0, 1, job0.ntasks, t->a2, st);
+    if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, job0, job0.ntasks, t->a2, st);
+    return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
 }
 
 // ------------------------------------------------------------------------------------------------ grouped launches
@@ -166,8 +166,8 @@ __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restri
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
-// Finishing launch of a one-column grouped GEMV. The first blocks take 1024 sorted rows of one job each (4 per
-// thread, loads issued together): sorted row r sums its K-chunk partials in chunk order (coalesced reads) and is
+// Finishing launch of a grouped GEMV. The first blocks take 1024 sorted rows of one job each (4 per thread, loads
+// issued together): per column, sorted row r sums its K-chunk partials in chunk order (coalesced reads) and is
 // written to its original row prmd[r] (a scatter inside the job's output). Rows that carry clamp-delta entries
 // (bit 15 of prmd) are left to the last blocks, one thread per such row, which add the delta entries after the
 // partials (the order and arithmetic of the single-launch fix-up).
@@ -181,7 +181,8 @@ struct FinishJob {
     const float *wpart; const int16_t *pinv; const uint16_t *prmd;
     const int *cp; const uint16_t *cc; const float *cv; const float *x;
     float *y;
-    int rows, nks;
+    unsigned ldx, ldy;   // column strides of x and y
+    int rows, nks, ncol;
 };
 
 __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
@@ -194,19 +195,20 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
         const gptr<const float> wp = as_global(J.wpart);
         int r[4];
         uint32_t pd[4];
-        float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             r[i] = min(r0 + 256 * i, J.rows - 1);
             pd[i] = as_global(J.prmd)[r[i]];
-            v[i] = 0.f;
         }
-        for (int ks = 0; ks < J.nks; ++ks)
+        for (int n = 0; n < J.ncol; ++n) {
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < J.nks; ++ks)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] += wp[(size_t)ks * J.rows + r[i]];
+                for (int i = 0; i < 4; ++i) v[i] += wp[((size_t)ks * J.ncol + n) * J.rows + r[i]];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[pd[i]] = v[i];
+            for (int i = 0; i < 4; ++i)
+                if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[(size_t)n * J.ldy + pd[i]] = v[i];
+        }
     } else {
         const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
         if (i >= ndrows) return;
@@ -214,13 +216,15 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
         const int ro = drows[i].y;
         const int r = as_global(J.pinv)[ro];
         const gptr<const float> wp = as_global(J.wpart);
-        float v = 0.f;
-        for (int ks = 0; ks < J.nks; ++ks) v += wp[(size_t)ks * J.rows + r];
-        if (J.x) {
-            const gptr<const float> x = as_global(J.x);
-            for (int e = as_global(J.cp)[ro]; e < as_global(J.cp)[ro + 1]; ++e) v += as_global(J.cv)[e] * x[as_global(J.cc)[e]];
+        for (int n = 0; n < J.ncol; ++n) {
+            float v = 0.f;
+            for (int ks = 0; ks < J.nks; ++ks) v += wp[((size_t)ks * J.ncol + n) * J.rows + r];
+            if (J.x) {
+                const gptr<const float> x = as_global(J.x) + (size_t)n * J.ldx;
+                for (int e = as_global(J.cp)[ro]; e < as_global(J.cp)[ro + 1]; ++e) v += as_global(J.cv)[e] * x[as_global(J.cc)[e]];
+            }
+            as_global_rw(J.y)[(size_t)n * J.ldy + ro] = v;
         }
-        as_global_rw(J.y)[ro] = v;
     }
 }
 
@@ -228,7 +232,6 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
 
 struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
-    bool wave = false;             // one column: the wave-independent kernel
     unsigned *ctr = nullptr;       // its unit counters (in work)
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
@@ -275,28 +278,24 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: job %d has a different codebook", i);
         for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
     }
-    // workspace layout: unit counters | per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows] |
-    // counters [ng]
+    // workspace layout: unit counters | per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows]
     std::vector<GemvJob> jobs(njobs);
     std::vector<ActJob> act(njobs);
-    std::vector<size_t> off_q(njobs), off_d(njobs), off_p(njobs), off_c(njobs);
+    std::vector<size_t> off_q(njobs), off_d(njobs), off_p(njobs);
     size_t bytes = 0;
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
     const size_t off_ctr = take(kWaveCtrBytes);
     int blk0 = 0;
     std::vector<uint32_t> ablk;   // activation prep: 256-block -> job
     const int cm = class_set(hist);
-    // one column: wave-independent units (row group, whole K); more: workgroup tasks of gpt row groups over
-    // K-chunks that fit the LDS activation buffer
-    const bool wave = ncols == 1;
-    const int gpt = wave ? 1 : gemv_waves(ncols, P8X_ACT_Q8_128, false, cm);
+    // wave-independent units: (row group, whole K)
     std::vector<int> kcs(njobs);
-    for (int i = 0; i < njobs; ++i) kcs[i] = wave ? tensors[i]->nb : std::min(tensors[i]->nb, kchunk_max(ncols));
-    if (wave) {
+    for (int i = 0; i < njobs; ++i) kcs[i] = tensors[i]->nb;
+    {
         // Units are handed out longest first, so the launch drains on the units of the last jobs. Those jobs are
-        // split along K (units of >= 4 blocks, partial rows summed by the fix-up) until about two rounds of the
-        // launch's waves have short units to finish on.
-        const long need = 2L * wave_wg_per_cu(cm) * num_cus() * wave_waves(cm);
+        // split along K (units of >= 4 blocks, partial rows summed by the finishing launch) until about two
+        // rounds of the launch's waves have short units to finish on.
+        const long need = 2L * wave_wg_per_cu(cm, ncols) * num_cus() * wave_waves(cm, ncols);
         std::vector<int> order(njobs);
         for (int i = 0; i < njobs; ++i) order[i] = i;
         std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return tensors[a]->nb > tensors[c]->nb; });
@@ -314,16 +313,14 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         const int nks = (t->nb + kc - 1) / kc;
         off_q[i] = take((size_t)ncols * t->K);
         off_d[i] = take(4 * (size_t)ncols * t->nsl);
-        // one column: partial rows of every job (the finishing launch reads them); more: K-chunk fix-up buffers
-        off_p[i] = wave || nks > 1 ? take(4 * (size_t)nks * ncols * t->rows) : 0;
-        off_c[i] = !wave && nks > 1 ? take(4 * (size_t)t->ng) : 0;
-        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, gpt, 0);
+        off_p[i] = take(4 * (size_t)nks * ncols * t->rows);   // partial rows (the finishing launch reads them)
+        fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, 1, 0);
         act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
         blk0 += t->nb;
         ablk.insert(ablk.end(), (size_t)t->nb, (uint32_t)i);
     }
     p8x_gemv_batch *b = new p8x_gemv_batch();
-    b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_blocks = blk0; b->wave = wave;
+    b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_blocks = blk0;
     b->a2 = tensors[0]->a2;
     int rc;
     if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||
@@ -338,8 +335,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         jobs[i].d = (const float *)(w + off_d[i]);
         act[i].q = (int8_t *)(w + off_q[i]);
         act[i].d = (float *)(w + off_d[i]);
-        jobs[i].wpart = wave || jobs[i].nks > 1 ? (float *)(w + off_p[i]) : nullptr;
-        jobs[i].wcnt = !wave && jobs[i].nks > 1 ? (unsigned *)(w + off_c[i]) : nullptr;
+        jobs[i].wpart = (float *)(w + off_p[i]);
+        jobs[i].wcnt = nullptr;
     }
     std::map<const uint32_t *, const p8x_tensor *> tensor_of;   // the sorted jobs find their tensor by M
     for (int i = 0; i < njobs; ++i) tensor_of[tensors[i]->M] = tensors[i];
@@ -350,7 +347,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     int task0 = 0;
     for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
     b->total_tasks = task0;
-    if (wave) {
+    {
         // unit -> job table
         std::vector<uint32_t> uj((size_t)task0);
         for (int i = 0; i < njobs; ++i)
@@ -376,7 +373,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         for (int i = 0; i < njobs; ++i) {
             const GemvJob &g = jobs[i];
             const p8x_tensor *t = tensor_of[g.M];
-            fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.rows, g.nks};
+            fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.ldx, g.ldy, g.rows, g.nks, ncols};
             for (int r : t->dorig) fdr.push_back(make_int2(i, r));
         }
         b->fin_blocks = (int)fblk.size();
@@ -423,12 +420,9 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
         return hip_check(hipGetLastError(), "k_act_q8_128_batch launch");
     }
     if (stage == 1) {
-        GemvJob none{};
-        if (b->wave) return launch_gemv_wave(b->cm, b->d_jobs, none, b->d_ujob, b->total_tasks, b->ctr, b->a2, st);
-        return launch_gemv_q8(b->ncols, b->cm, b->d_jobs, none, b->njobs, b->total_tasks, b->a2, st);
+        return launch_gemv_wave(b->ncols, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st);
     }
-    if (stage == 2) {   // one column: partial rows to original rows with the clamp delta (nothing otherwise)
-        if (!b->wave) return P8X_OK;
+    if (stage == 2) {   // partial rows to original rows with the clamp delta
         const int blocks = b->fin_blocks + (b->fin_ndrows + 255) / 256;
         hipLaunchKernelGGL(k_gemv_finish, dim3(blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
                            b->fin_blocks, (const int2 *)b->d_fdrows, b->fin_ndrows);

@@ -4,19 +4,19 @@
 namespace p8x {
 
 template <int NCOL>
-static int q8_cm(int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
-    if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(jobs, job0, njobs, tasks, a2, st);
-    if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(jobs, job0, njobs, tasks, a2, st);
-    if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(jobs, job0, njobs, tasks, a2, st);
-    return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
+static int q8_cm(int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
+    if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(job0, tasks, a2, st);
+    if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(job0, tasks, a2, st);
+    if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(job0, tasks, a2, st);
+    return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(job0, tasks, a2, st);
 }
 
-int launch_gemv_q8_lo(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+int launch_gemv_q8_lo(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
     switch (ncols) {
-        case 1: return q8_cm<1>(cm, jobs, job0, njobs, tasks, a2, st);
-        case 2: return q8_cm<2>(cm, jobs, job0, njobs, tasks, a2, st);
-        case 3: return q8_cm<3>(cm, jobs, job0, njobs, tasks, a2, st);
-        default: return q8_cm<4>(cm, jobs, job0, njobs, tasks, a2, st);
+        case 1: return q8_cm<1>(cm, job0, tasks, a2, st);
+        case 2: return q8_cm<2>(cm, job0, tasks, a2, st);
+        case 3: return q8_cm<3>(cm, job0, tasks, a2, st);
+        default: return q8_cm<4>(cm, job0, tasks, a2, st);
     }
 }
 

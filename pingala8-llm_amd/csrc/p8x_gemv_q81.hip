@@ -3,22 +3,22 @@
 
 namespace p8x {
 
-int launch_gemv_q81(int ncols, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
     switch (ncols) {
-        case 1: return launch_gemv_t<1, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 2: return launch_gemv_t<2, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 3: return launch_gemv_t<3, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 4: return launch_gemv_t<4, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 5: return launch_gemv_t<5, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 6: return launch_gemv_t<6, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        case 7: return launch_gemv_t<7, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
-        default: return launch_gemv_t<8, P8X_ACT_Q8_1, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
+        case 1: return launch_gemv_t<1, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 2: return launch_gemv_t<2, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 3: return launch_gemv_t<3, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 4: return launch_gemv_t<4, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 5: return launch_gemv_t<5, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 6: return launch_gemv_t<6, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        case 7: return launch_gemv_t<7, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
+        default: return launch_gemv_t<8, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
     }
 }
 
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st) {
-    if (act == P8X_ACT_Q8_128) return launch_gemv_t<1, P8X_ACT_Q8_128, true, kCmAll>(nullptr, job0, 1, job0.ntasks, a2, st);
-    return launch_gemv_t<1, P8X_ACT_Q8_1, true, kCmAll>(nullptr, job0, 1, job0.ntasks, a2, st);
+    if (act == P8X_ACT_Q8_128) return launch_gemv_t<1, P8X_ACT_Q8_128, true, kCmAll>(job0, job0.ntasks, a2, st);
+    return launch_gemv_t<1, P8X_ACT_Q8_1, true, kCmAll>(job0, job0.ntasks, a2, st);
 }
 
 }  // namespace p8x

@@ -4,22 +4,22 @@
 namespace p8x {
 
 template <int NCOL>
-static int q8_cm(int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
-    if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(jobs, job0, njobs, tasks, a2, st);
-    if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(jobs, job0, njobs, tasks, a2, st);
-    if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(jobs, job0, njobs, tasks, a2, st);
-    return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(jobs, job0, njobs, tasks, a2, st);
+static int q8_cm(int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
+    if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(job0, tasks, a2, st);
+    if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(job0, tasks, a2, st);
+    if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(job0, tasks, a2, st);
+    return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(job0, tasks, a2, st);
 }
 
-int launch_gemv_q8_lo(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st);
+int launch_gemv_q8_lo(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 
-int launch_gemv_q8(int ncols, int cm, const GemvJob *jobs, const GemvJob &job0, int njobs, int tasks, const uint32_t *a2, hipStream_t st) {
+int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
     switch (ncols) {
-        case 5: return q8_cm<5>(cm, jobs, job0, njobs, tasks, a2, st);
-        case 6: return q8_cm<6>(cm, jobs, job0, njobs, tasks, a2, st);
-        case 7: return q8_cm<7>(cm, jobs, job0, njobs, tasks, a2, st);
-        case 8: return q8_cm<8>(cm, jobs, job0, njobs, tasks, a2, st);
-        default: return launch_gemv_q8_lo(ncols, cm, jobs, job0, njobs, tasks, a2, st);
+        case 5: return q8_cm<5>(cm, job0, tasks, a2, st);
+        case 6: return q8_cm<6>(cm, job0, tasks, a2, st);
+        case 7: return q8_cm<7>(cm, job0, tasks, a2, st);
+        case 8: return q8_cm<8>(cm, job0, tasks, a2, st);
+        default: return launch_gemv_q8_lo(ncols, cm, job0, tasks, a2, st);
     }
 }
 
