@@ -128,8 +128,8 @@ typedef struct p8x_gemv_batch p8x_gemv_batch;
 int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                           float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out);
 int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
-/* the launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV, 2 = (one
- * column) K-chunk partials to original rows with the clamp delta; a no-op for more columns */
+/* the launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV (sorted-row
+ * partials per K-chunk and column), 2 = partials to original rows with the clamp delta */
 int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream);
 void p8x_gemv_batch_release(p8x_gemv_batch *b);
 

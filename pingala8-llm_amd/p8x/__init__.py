@@ -386,7 +386,7 @@ class Tensor:
 class GemvBatch:
     """A grouped launch of independent GEMVs (device buffers x_i, y_i fixed at creation)."""
 
-    stages = 3   # activation prep, fused decode + GEMV, finishing (a no-op for more than one column)
+    stages = 3   # activation prep, fused decode + GEMV, finishing (original rows, clamp delta)
 
     def __init__(self, tensors, xs, ys, ncols=1):
         n = len(tensors)
