@@ -171,6 +171,10 @@ def measure_qwen4b_layer(stream, steps, copies=20):
 
 def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
     """the drop-in pattern: one p8x_mul_mat_vec call (a single launch) per linear, as a MUL_MAT hook would issue"""
+    def step_linear_on(s):
+        for i, t in enumerate(tensors):
+            t.mul_mat_vec_dev(xs[t.K], ybufs[i], stream=s)
+
     def step_linear(events=None):
         for i, t in enumerate(tensors):
             if events is not None:
@@ -206,8 +210,14 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
                        "us_per_call": round(float(kern_ms[idx].mean() * 1e3), 2),
                        "MB_per_call": round(float(bytes_per[idx].mean() / 1e6), 3)}
     log("per-linear p8x_mul_mat_vec calls, per kind:", json.dumps(per_kind))
+    # the same step captured once in a HIP graph and replayed (how a graph-capturing host issues it)
+    graph = p8x.Graph(lambda s: step_linear_on(s), stream)
+    g_ms = timed_steps(lambda: graph.launch(stream), stream, 5, pl_steps)
+    graph.release()
+    log(f"per-linear calls replayed from a HIP graph: {g_ms * 1e3:.0f} us/step")
     per_linear = {"GB/s": round(step_bytes / (pl_ms * 1e-3) / 1e9, 1), "ms_per_step": round(pl_ms, 4),
-                  "launches_per_step": len(tensors), "per_kind": per_kind}
+                  "launches_per_step": len(tensors), "per_kind": per_kind,
+                  "graph_replay": {"GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1), "ms_per_step": round(g_ms, 4)}}
     return per_linear
 
 

@@ -199,6 +199,32 @@ class Stream:
         hip_check(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
 
 
+class Graph:
+    """A HIP graph of the work `enqueue(stream)` issues on `stream`, captured once (global capture mode: a call
+    that is not capture-safe fails the capture) and replayed with launch()."""
+
+    def __init__(self, enqueue, stream):
+        H = hip()
+        self.g, self.x = ctypes.c_void_p(), ctypes.c_void_p()
+        hip_check(H.hipStreamBeginCapture(stream.h, 0), "hipStreamBeginCapture")
+        try:
+            enqueue(stream)
+        finally:
+            hip_check(H.hipStreamEndCapture(stream.h, ctypes.byref(self.g)), "hipStreamEndCapture")
+        hip_check(H.hipGraphInstantiate(ctypes.byref(self.x), self.g, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self, stream):
+        hip_check(hip().hipGraphLaunch(self.x, stream.h), "hipGraphLaunch")
+
+    def release(self):
+        if self.x:
+            hip().hipGraphExecDestroy(self.x)
+            self.x = ctypes.c_void_p()
+        if self.g:
+            hip().hipGraphDestroy(self.g)
+            self.g = ctypes.c_void_p()
+
+
 class Event:
     def __init__(self):
         self.h = ctypes.c_void_p()
