@@ -22,6 +22,37 @@ struct BlockLane {
     }
 };
 
+// The 32-bit value held by lane (lane ^ M). M = 1, 2, 4, 8 stay inside 16-lane rows and use DPP row moves (VALU,
+// no LDS traffic): quad_perm [1,0,3,2] and [2,3,0,1], row_ror:8, and for M = 4 row_ror:12 (lane i reads lane
+// (i + 4) mod 16, the partner of lanes with bit 2 clear) or row_ror:4 (lane i - 4, for bit 2 set). Larger M:
+// ds_bpermute. Only the data movement differs from __shfl_xor; the arithmetic on the values is unchanged.
+template <int M, typename T>
+__device__ __forceinline__ T lane_xor(T v, int lane) {
+    static_assert(sizeof(T) == 4, "32-bit values");
+    const int iv = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (M == 1) r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M == 4) {
+        const int up = __builtin_amdgcn_update_dpp(0, iv, 0x12C, 0xF, 0xF, false);
+        const int down = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false);
+        r = (lane & 4) ? down : up;
+    } else if constexpr (M == 8) r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false);
+    else r = __shfl_xor(iv, M);
+    return __builtin_bit_cast(T, r);
+}
+
+// one butterfly stage across lanes: the lower index gets a + b, the upper a - b, with a the lower operand
+template <int M>
+__device__ __forceinline__ void fwht_lane_stage(float (&v)[4], int lane) {
+    const bool upper = (lane & M) != 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float p = lane_xor<M>(v[e], lane);
+        v[e] = upper ? p - v[e] : v[e] + p;
+    }
+}
+
 // x' for one 256-block from its loaded elements: lane holds 4 consecutive elements
 __device__ __forceinline__ void rotate_block_lane(const BlockLane &in, int lane, float (&v)[4]) {
     const f32x4 xv = in.x, cv = in.c;
@@ -29,30 +60,31 @@ __device__ __forceinline__ void rotate_block_lane(const BlockLane &in, int lane,
     // h = 1, 2 inside the lane
     { const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3]; v[0] = a0 + b0; v[1] = a0 - b0; v[2] = a1 + b1; v[3] = a1 - b1; }
     { const float a0 = v[0], b0 = v[2], a1 = v[1], b1 = v[3]; v[0] = a0 + b0; v[2] = a0 - b0; v[1] = a1 + b1; v[3] = a1 - b1; }
-    // h = 4 .. 128 across lanes: the lower index gets a + b, the upper a - b, with a the lower operand
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool upper = (lane & m) != 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float p = __shfl_xor(v[e], m);
-            v[e] = upper ? p - v[e] : v[e] + p;
-        }
-    }
+    // h = 4 .. 128 across lanes
+    fwht_lane_stage<1>(v, lane);
+    fwht_lane_stage<2>(v, lane);
+    fwht_lane_stage<4>(v, lane);
+    fwht_lane_stage<8>(v, lane);
+    fwht_lane_stage<16>(v, lane);
+    fwht_lane_stage<32>(v, lane);
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] *= 0.0625f;
 }
 
-__device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+__device__ __forceinline__ float half_wave_max(float v, int lane) {
+    v = fmaxf(v, lane_xor<1>(v, lane));
+    v = fmaxf(v, lane_xor<2>(v, lane));
+    v = fmaxf(v, lane_xor<4>(v, lane));
+    v = fmaxf(v, lane_xor<8>(v, lane));
+    return fmaxf(v, lane_xor<16>(v, lane));
 }
 
-__device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m);
-    return v;
+__device__ __forceinline__ int half_wave_sum(int v, int lane) {
+    v += lane_xor<1>(v, lane);
+    v += lane_xor<2>(v, lane);
+    v += lane_xor<4>(v, lane);
+    v += lane_xor<8>(v, lane);
+    return v + lane_xor<16>(v, lane);
 }
 
 // one 256-block to 8 bits per 128 columns: lane l gets the packed int8 of x' elements 4l..4l+3, the scale of its
@@ -61,7 +93,7 @@ __device__ __forceinline__ void quantize_loaded_q8_128(const BlockLane &in, int 
     float v[4];
     rotate_block_lane(in, lane, v);
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = half_wave_max(am);
+    am = half_wave_max(am, lane);
     dd = div_rn(am, 127.f);
     const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
     int qi[4];

@@ -473,6 +473,32 @@ struct RgSmem {
     float red[2][kRgWaves][32];          // per wave: its K range's row sums (two sets, alternating row groups)
 };
 
+// quantize the wave's blocks w, w + 16, ... (loaded in `in`) into the LDS activation layout, G blocks at a time
+template <int G>
+__device__ __forceinline__ void rg_quantize(const GemvJob &J, RgSmem &sm, const BlockLane (&in)[kRgQ], int w, int lane) {
+#pragma unroll
+    for (int i0 = 0; i0 < kRgQ; i0 += G) {
+        if (w + i0 * kRgWaves >= J.nb) break;
+        uint32_t packed[G];
+        float dd[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            int qs;
+            if (i0 + g < kRgQ) quantize_loaded_q8_128(in[i0 + g], lane, packed[g], dd[g], qs);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int bl = w + (i0 + g) * kRgWaves;
+            if (i0 + g < kRgQ && bl < J.nb) {
+                uint32_t *xw = sm.xq + bl * 128 + (lane >> 5) * 64 + (lane & 31);
+                xw[0] = packed[g];
+                xw[32] = packed[g];
+                if ((lane & 31) == 0) sm.xd[2 * bl + (lane >> 5)] = dd[g];
+            }
+        }
+    }
+}
+
 template <int CM>
 __global__ __launch_bounds__(64 * kRgWaves) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
@@ -488,23 +514,16 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     // the wave's activation blocks: every load first, the table meanwhile, then the quantization
     BlockLane in[kRgQ];
 #pragma unroll
-    for (int i = 0; i < kRgQ; ++i)
-        if (w + i * kRgWaves < J.nb) in[i].load(J.x + 256 * (w + i * kRgWaves), J.ic + 256 * (w + i * kRgWaves), lane);
-    build_coset_table<64 * kRgWaves>(sm.tab, a2, tid);
-#pragma unroll
     for (int i = 0; i < kRgQ; ++i) {
-        const int bl = w + i * kRgWaves;
-        if (bl < J.nb) {
-            uint32_t packed;
-            float dd;
-            int qs;
-            quantize_loaded_q8_128(in[i], lane, packed, dd, qs);
-            uint32_t *xw = sm.xq + bl * 128 + (lane >> 5) * 64 + (lane & 31);
-            xw[0] = packed;
-            xw[32] = packed;
-            if ((lane & 31) == 0) sm.xd[2 * bl + (lane >> 5)] = dd;
-        }
+        if (w + i * kRgWaves < J.nb) in[i].load(J.x + 256 * (w + i * kRgWaves), J.ic + 256 * (w + i * kRgWaves), lane);
+        else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
+    build_coset_table<64 * kRgWaves>(sm.tab, a2, tid);
+    // the blocks of a wave are independent: quantized G at a time in straight-line code, so their cross-lane
+    // chains overlap (one at a time they cost a full chain latency each)
+    if (J.nb <= kRgWaves) rg_quantize<1>(J, sm, in, w, lane);
+    else if (J.nb <= 2 * kRgWaves) rg_quantize<2>(J, sm, in, w, lane);
+    else rg_quantize<4>(J, sm, in, w, lane);
     __syncthreads();
     const int per = J.nb / kRgWaves, rem = J.nb % kRgWaves;
     const int b0 = w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);

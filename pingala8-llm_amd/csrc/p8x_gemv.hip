@@ -34,7 +34,7 @@ __global__ __launch_bounds__(64) void k_act_q8_128(const float *__restrict__ x, 
     int s;
     quantize_block_q8_128(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane, packed, dd, s);
     reinterpret_cast<uint32_t *>(q + (size_t)n * K + 256 * b)[lane] = packed;
-    s = half_wave_sum(s);
+    s = half_wave_sum(s, lane);
     const int nsl = K / 128;
     if ((lane & 31) == 0) {
         d[(size_t)n * nsl + 2 * b + (lane >> 5)] = dd;

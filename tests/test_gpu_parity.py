@@ -115,7 +115,8 @@ def test_gemv_multicolumn(ncols):
         assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
 
 
-@pytest.mark.parametrize("rows,K,classes", [(4096, 4096, (3,)), (1024, 14336, (2, 3, 4)), (2048, 1024, tuple(range(8)))])
+@pytest.mark.parametrize("rows,K,classes", [(4096, 4096, (3,)), (1024, 14336, (2, 3, 4)), (2048, 1024, tuple(range(8))),
+                                            (512, 6144, (3,)), (256, 28672, (3, 6)), (64, 30720, (3,))])
 def test_large_shapes(rows, K, classes):
     p = [0.0] * 8
     for c in classes:
