@@ -169,7 +169,7 @@ def measure_qwen4b_layer(stream, steps, copies=20):
             "per_linear_launches": {"us_per_layer": round(l_ms * 1e3, 2), "GB/s": round(layer_bytes / (l_ms * 1e-3) / 1e9, 1)}}
 
 
-def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
+def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps, graph_replay=True):
     """the drop-in pattern: one p8x_mul_mat_vec call (a single launch) per linear, as a MUL_MAT hook would issue"""
     def step_linear_on(s):
         for i, t in enumerate(tensors):
@@ -210,14 +210,15 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps):
                        "us_per_call": round(float(kern_ms[idx].mean() * 1e3), 2),
                        "MB_per_call": round(float(bytes_per[idx].mean() / 1e6), 3)}
     log("per-linear p8x_mul_mat_vec calls, per kind:", json.dumps(per_kind))
-    # the same step captured once in a HIP graph and replayed (how a graph-capturing host issues it)
-    graph = p8x.Graph(lambda s: step_linear_on(s), stream)
-    g_ms = timed_steps(lambda: graph.launch(stream), stream, 5, pl_steps)
-    graph.release()
-    log(f"per-linear calls replayed from a HIP graph: {g_ms * 1e3:.0f} us/step")
     per_linear = {"GB/s": round(step_bytes / (pl_ms * 1e-3) / 1e9, 1), "ms_per_step": round(pl_ms, 4),
-                  "launches_per_step": len(tensors), "per_kind": per_kind,
-                  "graph_replay": {"GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1), "ms_per_step": round(g_ms, 4)}}
+                  "launches_per_step": len(tensors), "per_kind": per_kind}
+    if graph_replay:
+        # the same step captured once in a HIP graph and replayed (how a graph-capturing host issues it)
+        graph = p8x.Graph(lambda s: step_linear_on(s), stream)
+        g_ms = timed_steps(lambda: graph.launch(stream), stream, 5, pl_steps)
+        graph.release()
+        log(f"per-linear calls replayed from a HIP graph: {g_ms * 1e3:.0f} us/step")
+        per_linear["graph_replay"] = {"GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1), "ms_per_step": round(g_ms, 4)}
     return per_linear
 
 
@@ -304,6 +305,8 @@ def main():
     ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM measurement")
     ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay of the per-linear step "
+                    "(rocprofv3 --kernel-trace ended in a host segmentation fault during graph replays)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -366,7 +369,8 @@ def main():
         log(f"copy calibration: {n} bytes device to device")
 
     # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
-    per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3)) if not args.no_per_linear else None
+    per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3),
+                                    not args.no_graph) if not args.no_per_linear else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
     qwen14b = qwen4b = None

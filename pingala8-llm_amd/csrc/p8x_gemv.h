@@ -222,62 +222,80 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
 // first, then NBUF register buffers rotate so that NBUF - 1 following tiles are in flight while the current
 // one is decoded. Every step issues its prefetch (past the run's end through an empty resource, which reads
 // zeros without memory traffic), so the loop body is straight-line and the wait counts stay exact.
-// Returns the first block after the run.
-template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C, typename SM>
-__device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const SM &sm, int b, int bend, float (&yacc)[NCOL]) {
-    constexpr int NW = nw_of(C);
-    const GemvJob &J = *c.J;
-    const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)c.g * J.nb;   // tile words: scalar loads
-    auto tile_word = [&](int bb) { return mrow[bb]; };
-    int e = bend;   // ONLY_C: every tile of the tensor has class C
-    if constexpr (!ONLY_C) {
-        e = b + 1;
-        while (e < bend && (tile_word(e) >> 29) == (uint32_t)C) ++e;
-    }
-    constexpr bool STEP = gemv_step_order<ACT, PARTIALS>();
+// begin() finds the run and issues its first NBUF - 1 tiles; finish() decodes the run and returns the first
+// block after it. Between the two the caller may do other work (the loads stay in flight).
+template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C>
+struct GemvRun {
+    static constexpr int NW = nw_of(C);
+    static constexpr bool STEP = gemv_step_order<ACT, PARTIALS>();
     using Slice = std::conditional_t<STEP, StepSlice<C>, RawSlice<C>>;
+    Slice buf[NBUF];
+    int b, e;
+    uint32_t wn;   // tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
     // lane part of the payload offsets: one base (step order) or the NW rotated word offsets
     std::conditional_t<STEP, uint32_t, uint32_t[NW]> vo;
-    if constexpr (STEP) vo = (uint32_t)(c.hs * NW * 128 + 8 * c.j);
-    else RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
-    const uint32_t vs = 2u * (uint32_t)c.j;
-    // wn = tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
-    uint32_t wn = tile_word(b);
-    // past the run's end the resources have no records: the loads read zeros without memory traffic
-    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
-    auto issue = [&](Slice &r, int ta) {
+    uint32_t vs;
+
+    __device__ __forceinline__ kptr<const uint32_t> mrow(const TaskCtx<NCOL, ACT> &c) const {
+        return as_const(c.J->M) + (size_t)c.g * c.J->nb;   // tile words: scalar loads
+    }
+    __device__ __forceinline__ void issue(const TaskCtx<NCOL, ACT> &c, Slice &r, int ta) {
+        const GemvJob &J = *c.J;
         const bool ok = ta < e;
         const int tc = ok ? ta : b;
         const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
         const uint32_t soff = ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
+        const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
         r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
-        wn = tile_word(min(ta + 1, e - 1));
-    };
-    auto tile = [&](const Slice &r0_, int t) {
+        wn = mrow(c)[min(ta + 1, e - 1)];
+    }
+    __device__ __forceinline__ void begin(const TaskCtx<NCOL, ACT> &c, int b_, int bend) {
+        b = b_;
+        e = bend;   // ONLY_C: every tile of the tensor has class C
+        if constexpr (!ONLY_C) {
+            e = b + 1;
+            while (e < bend && (mrow(c)[e] >> 29) == (uint32_t)C) ++e;
+        }
+        if constexpr (STEP) vo = (uint32_t)(c.hs * NW * 128 + 8 * c.j);
+        else RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
+        vs = 2u * (uint32_t)c.j;
+        wn = mrow(c)[b];
+#pragma unroll
+        for (int i = 0; i < NBUF - 1; ++i) issue(c, buf[i], b + i);
+    }
+    template <typename SM>
+    __device__ __forceinline__ void tile(const TaskCtx<NCOL, ACT> &c, const SM &sm, const Slice &r0_, int t, float (&yacc)[NCOL]) {
         Slice r = r0_;
         pin(r.w);
         pin(r.s);
         if constexpr (STEP) gemv_tile_step<NCOL, C>(c, sm, r, t, yacc);
         else gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, r, t, yacc);
-    };
-    Slice buf[NBUF];
-#pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
-    // whole groups of NBUF tiles: the loop body is straight-line, so the same loads are in flight at every
-    // back edge
-    int base = b;
-    for (; base + NBUF <= e; base += NBUF) {
-#pragma unroll
-        for (int i = 0; i < NBUF; ++i) {
-            issue(buf[(i + NBUF - 1) % NBUF], base + i + NBUF - 1);
-            tile(buf[i], base + i);
-        }
     }
-    // the last e - base < NBUF tiles are already in flight in buf[0 ..]
+    template <typename SM>
+    __device__ __forceinline__ int finish(const TaskCtx<NCOL, ACT> &c, const SM &sm, float (&yacc)[NCOL]) {
+        // whole groups of NBUF tiles: the loop body is straight-line, so the same loads are in flight at every
+        // back edge
+        int base = b;
+        for (; base + NBUF <= e; base += NBUF) {
 #pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i)
-        if (base + i < e) tile(buf[i], base + i);
-    return e;
+            for (int i = 0; i < NBUF; ++i) {
+                issue(c, buf[(i + NBUF - 1) % NBUF], base + i + NBUF - 1);
+                tile(c, sm, buf[i], base + i, yacc);
+            }
+        }
+        // the last e - base < NBUF tiles are already in flight in buf[0 ..]
+#pragma unroll
+        for (int i = 0; i < NBUF - 1; ++i)
+            if (base + i < e) tile(c, sm, buf[i], base + i, yacc);
+        return e;
+    }
+};
+
+template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C, typename SM>
+__device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const SM &sm, int b, int bend, float (&yacc)[NCOL]) {
+    GemvRun<NCOL, ACT, PARTIALS, C, NBUF, ONLY_C> run;
+    run.begin(c, b, bend);
+    return run.finish(c, sm, yacc);
 }
 
 // prefetch depth (register buffers) per variant
@@ -511,6 +529,8 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
     c.b0 = 0; c.nbl = J.nb;
+    const int per = J.nb / kRgWaves, rem = J.nb % kRgWaves;
+    const int b0 = w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);   // the wave's K range
     // the wave's activation blocks: every load first, the table meanwhile, then the quantization
     BlockLane in[kRgQ];
 #pragma unroll
@@ -525,8 +545,6 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     else if (J.nb <= 2 * kRgWaves) rg_quantize<2>(J, sm, in, w, lane);
     else rg_quantize<4>(J, sm, in, w, lane);
     __syncthreads();
-    const int per = J.nb / kRgWaves, rem = J.nb % kRgWaves;
-    const int b0 = w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);
     int set = 0;
     for (int g = blockIdx.x; g < J.ng; g += gridDim.x, set ^= 1) {
         c.g = g;
