@@ -65,8 +65,9 @@ struct GemvSmem {
 };
 
 // class sets with their own instantiations: class 3 only (the 2-bit bulk), class 6 only (4-bit attn_v),
-// classes 2-4 (mixed ffn_down), everything
-constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmAll = 0xFE;
+// classes 2-4 (mixed ffn_down), classes 2-4 and 6 (a whole model of the B4 mix), everything. The one-class sets
+// decode every tile of a run as that class; the others read each tile's class (class 0 tiles are skipped).
+constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmC2346 = kCmC234 | (1 << 6), kCmAll = 0xFE;
 
 // Waves per workgroup (each owns one row group of a task) and the waves per SIMD the registers are sized for.
 // LDS holds two workgroups per CU; a variant that fits 64 VGPRs (one column, class 3, step order) runs
@@ -600,12 +601,14 @@ static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipS
 // drains with at most one unit per wave. Units are numbered in job order; the job list is ordered by decreasing
 // unit length, so the long units start first.
 // One column of class 3 fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; one column of classes 6 or 2-4
-// 8-wave workgroups at 4 (128 VGPRs), every class at 2. Two to four columns: 16-wave workgroups (one per CU,
-// the slots take NCOL x 8 KB) at 4 waves per SIMD; five to eight columns (more than 128 VGPRs) and every class:
-// 8-wave workgroups at 2.
-__host__ __device__ constexpr int wave_waves(int cm, int ncol = 1) { return ncol > 4 ? 8 : cm == kCmC3 || (ncol > 1 && cm != kCmAll) ? 16 : 8; }
+// 8-wave workgroups at 4 (128 VGPRs), every class at 2. Two to four columns of one class: 16-wave workgroups
+// (one per CU, the slots take NCOL x 8 KB) at 4 waves per SIMD; five to eight columns or mixed classes (more
+// than 128 VGPRs): 8-wave workgroups at 2.
+__host__ __device__ constexpr int wave_waves(int cm, int ncol = 1) {
+    return ncol == 1 ? (cm == kCmC3 ? 16 : 8) : ncol <= 4 && (cm == kCmC3 || cm == kCmC6) ? 16 : 8;
+}
 __host__ __device__ constexpr int wave_per_eu(int cm, int ncol = 1) {
-    return ncol > 4 ? 2 : ncol > 1 ? (cm == kCmAll ? 2 : 4) : cm == kCmC3 ? 8 : cm == kCmAll ? 2 : 4;
+    return ncol == 1 ? (cm == kCmC3 ? 8 : cm == kCmAll ? 2 : 4) : ncol <= 4 && (cm == kCmC3 || cm == kCmC6) ? 4 : 2;
 }
 __host__ __device__ constexpr int wave_wg_per_cu(int cm, int ncol = 1) { return 4 * wave_per_eu(cm, ncol) / wave_waves(cm, ncol); }
 // prefetch depth of the class-3 runs (register buffers hold NCOL activation words and scales each)

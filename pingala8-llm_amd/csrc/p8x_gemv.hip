@@ -74,7 +74,11 @@ __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, si
 int class_set(const size_t hist[8]) {
     int m = 0;
     for (int c = 1; c < 8; ++c) if (hist[c]) m |= 1 << c;
-    for (int cm : {kCmC3, kCmC6, kCmC234})
+    // a one-class set decodes whole runs as its class: only when no tile is class 0 (all-zero, skipped)
+    if (!hist[0])
+        for (int cm : {kCmC3, kCmC6})
+            if ((m & ~cm) == 0) return cm;
+    for (int cm : {kCmC234, kCmC2346})
         if ((m & ~cm) == 0) return cm;
     return kCmAll;
 }

@@ -8,6 +8,7 @@ static int q8_cm(int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hip
     if (cm == kCmC3) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC3>(job0, tasks, a2, st);
     if (cm == kCmC6) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC6>(job0, tasks, a2, st);
     if (cm == kCmC234) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC234>(job0, tasks, a2, st);
+    if (cm == kCmC2346) return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmC2346>(job0, tasks, a2, st);
     return launch_gemv_t<NCOL, P8X_ACT_Q8_128, false, kCmAll>(job0, tasks, a2, st);
 }
 

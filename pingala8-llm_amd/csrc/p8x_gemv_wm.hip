@@ -8,6 +8,7 @@ static int wave_cm(int cm, const GemvJob *jobs, const uint32_t *ujob, int units,
     if (cm == kCmC3) return launch_gemv_wave_t<kCmC3, NCOL>(jobs, ujob, units, ctr, a2, st);
     if (cm == kCmC6) return launch_gemv_wave_t<kCmC6, NCOL>(jobs, ujob, units, ctr, a2, st);
     if (cm == kCmC234) return launch_gemv_wave_t<kCmC234, NCOL>(jobs, ujob, units, ctr, a2, st);
+    if (cm == kCmC2346) return launch_gemv_wave_t<kCmC2346, NCOL>(jobs, ujob, units, ctr, a2, st);
     return launch_gemv_wave_t<kCmAll, NCOL>(jobs, ujob, units, ctr, a2, st);
 }
 

@@ -256,3 +256,29 @@ def test_batch_fewer_units_than_waves():
         batch.run()
         p8x.synchronize()
         assert rel_l2(y.to_numpy(np.float32, (96,)), orc.gemv_f64(X[0])) < 1e-5, rep
+
+
+@pytest.mark.parametrize("cp", [(1, 0, 0, 1, 0, 0, 0, 0), (1, 0, 1, 6, 1, 0, 1, 0), (0, 0, 1, 6, 1, 0, 1, 0)])
+def test_class_zero_tiles_and_mixed_sets(cp):
+    """tensors with all-zero (class 0) tiles among class-3 tiles, and the classes 2-4 + 6 set: single calls
+    (one and three columns) and a grouped launch against the fp64 oracle"""
+    rows, K = 512, 4096
+    slot = p8x.synth_random(808, rows, K, class_p=cp, nd=5)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((3, K)).astype(np.float32)
+    assert rel_l2(t.mul_mat_vec(X[0])[0], orc.gemv_f64(X[0])) < 1e-5
+    Y = t.mul_mat_vec(X)
+    for n in range(3):
+        assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
+    for ncols in (1, 2):
+        xb = p8x.DeviceBuffer.from_numpy(X[:ncols].copy())
+        yb = p8x.DeviceBuffer(4 * ncols * rows)
+        batch = p8x.GemvBatch([t], [xb], [yb], ncols=ncols)
+        batch.run()
+        p8x.synchronize()
+        Yb = yb.to_numpy(np.float32, (ncols, rows))
+        for n in range(ncols):
+            assert rel_l2(Yb[n], orc.gemv_f64(X[n])) < 1e-5, (ncols, n)
+        batch.release()
