@@ -477,9 +477,12 @@ static int launch_gemv_t(const GemvJob &job0, int tasks, const uint32_t *a2, hip
 
 // ------------------------------------------------------------------------------------------------ single GEMV, latency path
 // One column of 8-bit-per-128 activations, one linear per launch (the drop-in p8x_mul_mat_vec call). Such a
-// launch has few tiles, so latency rules: a workgroup takes whole 32-row groups over the whole K, quantizes the
-// activations itself into LDS once (the prep's arithmetic, one wave per block), its waves split K into
-// contiguous block ranges, and the partial rows meet in LDS in a fixed order: no cross-workgroup fix-up.
+// launch has few tiles, so latency rules: a workgroup takes whole 32-row groups over its K-chunk (the whole K,
+// or one of J.nks chunks when the tensor has too few row groups to fill the CUs), quantizes that part of the
+// activations itself into LDS once (the prep's arithmetic, one wave per block), its waves split the chunk into
+// contiguous block ranges, and the partial rows meet in LDS in a fixed order. K-chunks of a row group meet
+// through the fixed-order fix-up of the multi-column kernel (agent-coherent partial rows, an arrival counter,
+// the last arrival sums the chunks in order).
 constexpr int kRgWaves = 16;
 constexpr int kRgMaxBlocks = 112;                   // K up to 28672
 constexpr int kRgQ = kRgMaxBlocks / kRgWaves;       // activation blocks per wave at most
@@ -494,10 +497,10 @@ struct RgSmem {
 
 // quantize the wave's blocks w, w + 16, ... (loaded in `in`) into the LDS activation layout, G blocks at a time
 template <int G>
-__device__ __forceinline__ void rg_quantize(const GemvJob &J, RgSmem &sm, const BlockLane (&in)[kRgQ], int w, int lane) {
+__device__ __forceinline__ void rg_quantize(int nbk, RgSmem &sm, const BlockLane (&in)[kRgQ], int w, int lane) {
 #pragma unroll
     for (int i0 = 0; i0 < kRgQ; i0 += G) {
-        if (w + i0 * kRgWaves >= J.nb) break;
+        if (w + i0 * kRgWaves >= nbk) break;
         uint32_t packed[G];
         float dd[G];
 #pragma unroll
@@ -507,8 +510,8 @@ __device__ __forceinline__ void rg_quantize(const GemvJob &J, RgSmem &sm, const 
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const int bl = w + (i0 + g) * kRgWaves;
-            if (i0 + g < kRgQ && bl < J.nb) {
+            const int bl = w + (i0 + g) * kRgWaves;   // block of the chunk
+            if (i0 + g < kRgQ && bl < nbk) {
                 uint32_t *xw = sm.xq + bl * 128 + (lane >> 5) * 64 + (lane & 31);
                 xw[0] = packed[g];
                 xw[32] = packed[g];
@@ -518,7 +521,8 @@ __device__ __forceinline__ void rg_quantize(const GemvJob &J, RgSmem &sm, const 
     }
 }
 
-template <int CM>
+// SPLIT: J.nks K-chunks (else the whole K, J.nks == 1)
+template <int CM, bool SPLIT>
 __global__ __launch_bounds__(64 * kRgWaves) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     __shared__ RgSmem sm;
@@ -529,25 +533,30 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
-    c.b0 = 0; c.nbl = J.nb;
-    const int per = J.nb / kRgWaves, rem = J.nb % kRgWaves;
-    const int b0 = w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);   // the wave's K range
+    // workgroup b: K-chunk ks = b % nks of row groups b / nks, b / nks + gridDim.x / nks, ...
+    const int nks = SPLIT ? J.nks : 1;
+    const int ks = SPLIT ? (int)blockIdx.x % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
+    c.b0 = ks * J.kchunk; c.nbl = nbk;
+    const int per = nbk / kRgWaves, rem = nbk % kRgWaves;
+    const int b0 = c.b0 + w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);   // the wave's K range
     // the wave's activation blocks: every load first, the table meanwhile, then the quantization
     BlockLane in[kRgQ];
 #pragma unroll
     for (int i = 0; i < kRgQ; ++i) {
-        if (w + i * kRgWaves < J.nb) in[i].load(J.x + 256 * (w + i * kRgWaves), J.ic + 256 * (w + i * kRgWaves), lane);
+        const int bk = c.b0 + w + i * kRgWaves;   // the chunk's block w + 16 i
+        if (w + i * kRgWaves < nbk) in[i].load(J.x + 256 * bk, J.ic + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
     build_coset_table<64 * kRgWaves>(sm.tab, a2, tid);
     // the blocks of a wave are independent: quantized G at a time in straight-line code, so their cross-lane
     // chains overlap (one at a time they cost a full chain latency each)
-    if (J.nb <= kRgWaves) rg_quantize<1>(J, sm, in, w, lane);
-    else if (J.nb <= 2 * kRgWaves) rg_quantize<2>(J, sm, in, w, lane);
-    else rg_quantize<4>(J, sm, in, w, lane);
+    if (nbk <= kRgWaves) rg_quantize<1>(nbk, sm, in, w, lane);
+    else if (nbk <= 2 * kRgWaves) rg_quantize<2>(nbk, sm, in, w, lane);
+    else rg_quantize<4>(nbk, sm, in, w, lane);
     __syncthreads();
     int set = 0;
-    for (int g = blockIdx.x; g < J.ng; g += gridDim.x, set ^= 1) {
+    const int gstep = (int)gridDim.x / nks;
+    for (int g = (int)blockIdx.x / nks; g < J.ng; g += gstep, set ^= 1) {
         c.g = g;
         // the output row, read before the tile loads so that the epilogue finds it in a register
         int ro = 0;
@@ -571,24 +580,43 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
         // one barrier per row group: a wave writes this set again two groups later, after wave 0 has passed the
         // next group's barrier, so wave 0 has read it by then
         __syncthreads();
-        if (w == 0 && lane < 32) {
+        if (w == 0) {
             float v = 0.f;
-            for (int i = 0; i < kRgWaves; ++i) v += sm.red[set][i][lane];
-            const int r = ro & 0x7FFF;
-            if (ro & 0x8000) {
-                const gptr<const float> xr = as_global(J.x);
-                for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) v += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
+            if (lane < 32)
+                for (int i = 0; i < kRgWaves; ++i) v += sm.red[set][i][lane];
+            if constexpr (SPLIT) {   // K-chunks: the last arrival sums them in chunk order
+                const gptr<float> wpart = as_global_rw(J.wpart);
+                const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
+                if (lane < 32) __hip_atomic_store(&wpart[(size_t)ks * J.rows + 32 * g + lane], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                unsigned old = 0;
+                if (lane == 0) old = __hip_atomic_fetch_add(&wcnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                old = __builtin_amdgcn_readfirstlane(old);
+                if (old != (unsigned)(nks - 1)) continue;
+                v = 0.f;
+                if (lane < 32)
+                    for (int k = 0; k < nks; ++k)
+                        v += __hip_atomic_load(&wpart[(size_t)k * J.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            as_global_rw(J.y)[r] = v;
+            if (lane < 32) {
+                const int r = ro & 0x7FFF;
+                if (ro & 0x8000) {
+                    const gptr<const float> xr = as_global(J.x);
+                    for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) v += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
+                }
+                as_global_rw(J.y)[r] = v;
+            }
         }
     }
 }
 
 template <int CM>
 static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
-    // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups, one per CU
+    // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups per K-chunk, one per CU
     const int per = (ng + num_cus() - 1) / num_cus();
-    hipLaunchKernelGGL((k_gemv_rg<CM>), dim3((ng + per - 1) / per), dim3(64 * kRgWaves), 0, st, job, a2);
+    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true>), dim3((ng + per - 1) / per * job.nks), dim3(64 * kRgWaves), 0, st, job, a2);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false>), dim3((ng + per - 1) / per), dim3(64 * kRgWaves), 0, st, job, a2);
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 

@@ -136,8 +136,10 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
         return P8X_OK;
     }
     if (ncols == 1 && act == P8X_ACT_Q8_128 && !q && t->nb <= kRgMaxBlocks) {   // one linear, x quantized in the launch
+        // two K-chunks when the row groups fill at most half the CUs and K is long (e.g. ffn_down)
+        const int nks = 2 * t->ng <= num_cus() && t->nb >= 2 * kRgWaves && (size_t)2 * t->rows <= t->wpart_floats ? 2 : 1;
         GemvJob job0;
-        fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, 1, t->nb, 1, 0);
+        fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, nks, (t->nb + nks - 1) / nks, 1, 0);
         return launch_gemv_rg(cm, job0, t->ng, t->a2, st);
     }
     const GemvPlan p = gemv_plan(t, ncols, act, false);
