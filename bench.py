@@ -131,6 +131,33 @@ def measure_qwen14b_columns(stream, steps, col_list=(1, 2, 4, 8)):
     return out
 
 
+def measure_quantized_4096(stream, steps, copies=128):
+    """one 4096 x 4096 W quantized by the host encoder (N(0, 0.02^2) with 0.1% of entries x10, seeded c16 in
+    [0.5, 2) and Hadamard signs, clamp delta above fp16(1.001 max|W|)); single p8x_mul_mat_vec calls back to back
+    over 128 distinct device copies (555 MB, so the MALL does not hold the weights)"""
+    rng = np.random.default_rng(1)
+    W = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    W[rng.random(W.shape) < 0.001] *= 10
+    c16 = rng.uniform(0.5, 2.0, 4096).astype(np.float16).view(np.uint16)
+    slot = p8x.quantize_tensor(W, c16=c16, sign_seed=3)
+    tensors = [p8x.Tensor(slot, 4096, 4096) for _ in range(copies)]
+    x = p8x.DeviceBuffer.from_numpy(rng.standard_normal(4096).astype(np.float32))
+    y = p8x.DeviceBuffer(4 * 4096)
+
+    def rnd():
+        for t in tensors:
+            t.mul_mat_vec_dev(x, y, stream=stream)
+
+    ms = timed_steps(rnd, stream, 5, steps) / copies
+    b = tensors[0].stream_bytes
+    for t in tensors:
+        t.release()
+    log(f"quantized 4096x4096: {ms * 1e3:.2f} us per call")
+    return {"workload": f"one 4096 x 4096 class-3 tensor from the host encoder, {copies} device copies in rotation, "
+                        "single p8x_mul_mat_vec calls back to back", "stream_bytes": int(b),
+            "us_per_call": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1)}
+
+
 def measure_qwen4b_layer(stream, steps, copies=20):
     """Qwen3-4B one layer (7 linears, 26 MB), batch 1, rotating over 20 distinct copies (> 512 MB, so the MALL
     does not hold the weights): one grouped launch per layer, and one p8x_mul_mat_vec call per linear"""
@@ -373,13 +400,14 @@ def main():
                                     not args.no_graph) if not args.no_per_linear else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
-    qwen14b = qwen4b = None
+    qwen14b = qwen4b = quant4096 = None
     if not args.no_qwen:
         batch.release()
         for t in tensors:
             t.release()
         qwen14b = measure_qwen14b_columns(stream, max(10, args.steps // 4))
         qwen4b = measure_qwen4b_layer(stream, max(10, args.steps // 4))
+        quant4096 = measure_quantized_4096(stream, max(10, args.steps // 10))
     cpu = None
     if not args.no_cpu and host0:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -405,6 +433,7 @@ def main():
         "dequantize_f16": deq,
         "qwen3_14b_columns": qwen14b,
         "qwen3_4b_layer": qwen4b,
+        "quantized_4096": quant4096,
         "host_wall_s": round(wall, 3),
     }
     print(json.dumps(out), flush=True)
