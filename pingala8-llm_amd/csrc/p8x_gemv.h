@@ -483,52 +483,57 @@ static int launch_gemv_t(const GemvJob &job0, int tasks, const uint32_t *a2, hip
 // contiguous block ranges, and the partial rows meet in LDS in a fixed order. K-chunks of a row group meet
 // through the fixed-order fix-up of the multi-column kernel (agent-coherent partial rows, an arrival counter,
 // the last arrival sums the chunks in order).
-constexpr int kRgWaves = 16;
-constexpr int kRgMaxBlocks = 112;                   // K up to 28672
-constexpr int kRgQ = kRgMaxBlocks / kRgWaves;       // activation blocks per wave at most
+constexpr int kRgMaxBlocks = 112;   // activation blocks in LDS (columns x blocks of the K-chunk)
+// up to two columns: 16 waves at 128 VGPRs; more: 8 waves at 256
+__host__ __device__ constexpr int rg_waves(int ncol) { return ncol <= 2 ? 16 : 8; }
 
+template <int NCOL, int WAVES = rg_waves(NCOL)>
 struct RgSmem {
-    static constexpr int kXW = kRgMaxBlocks * 128, kNSC = 2 * kRgMaxBlocks;
+    static constexpr int kXW = kRgMaxBlocks * 128 / NCOL, kNSC = 2 * kRgMaxBlocks / NCOL;   // per-column strides
     uint32_t tab[kTabWords];             // LDS address 0
-    uint32_t xq[kRgMaxBlocks * 128];     // [block][half][64 words] (step order)
-    float xd[2 * kRgMaxBlocks];          // [block][half]
-    float red[2][kRgWaves][32];          // per wave: its K range's row sums (two sets, alternating row groups)
+    uint32_t xq[kRgMaxBlocks * 128];     // [column][block][half][64 words] (step order)
+    float xd[2 * kRgMaxBlocks];          // [column][block][half]
+    float red[2][WAVES][NCOL][32];       // per wave: its K range's row sums (two sets, alternating row groups)
 };
 
-// quantize the wave's blocks w, w + 16, ... (loaded in `in`) into the LDS activation layout, G blocks at a time
-template <int G>
-__device__ __forceinline__ void rg_quantize(int nbk, RgSmem &sm, const BlockLane (&in)[kRgQ], int w, int lane) {
+// quantize the wave's items w, w + 16, ... (item i = column i / nbk, block i % nbk of the chunk; loaded in `in`)
+// into the LDS activation layout, G items at a time
+template <int G, int NCOL, int WAVES = rg_waves(NCOL), int RQ = kRgMaxBlocks / WAVES>
+__device__ __forceinline__ void rg_quantize(int nbk, RgSmem<NCOL> &sm, const BlockLane (&in)[RQ], int w, int lane) {
 #pragma unroll
-    for (int i0 = 0; i0 < kRgQ; i0 += G) {
-        if (w + i0 * kRgWaves >= nbk) break;
+    for (int i0 = 0; i0 < RQ; i0 += G) {
+        if (w + i0 * WAVES >= NCOL * nbk) break;
         uint32_t packed[G];
         float dd[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             int qs;
-            if (i0 + g < kRgQ) quantize_loaded_q8_128(in[i0 + g], lane, packed[g], dd[g], qs);
+            if (i0 + g < RQ) quantize_loaded_q8_128(in[i0 + g], lane, packed[g], dd[g], qs);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const int bl = w + (i0 + g) * kRgWaves;   // block of the chunk
-            if (i0 + g < kRgQ && bl < nbk) {
-                uint32_t *xw = sm.xq + bl * 128 + (lane >> 5) * 64 + (lane & 31);
+            const int it = w + (i0 + g) * WAVES;
+            if (i0 + g < RQ && it < NCOL * nbk) {
+                const int n = it / nbk, bl = it % nbk;   // column, block of the chunk
+                uint32_t *xw = sm.xq + n * RgSmem<NCOL>::kXW + bl * 128 + (lane >> 5) * 64 + (lane & 31);
                 xw[0] = packed[g];
                 xw[32] = packed[g];
-                if ((lane & 31) == 0) sm.xd[2 * bl + (lane >> 5)] = dd[g];
+                if ((lane & 31) == 0) sm.xd[n * RgSmem<NCOL>::kNSC + 2 * bl + (lane >> 5)] = dd[g];
             }
         }
     }
 }
 
-// SPLIT: J.nks K-chunks (else the whole K, J.nks == 1)
-template <int CM, bool SPLIT>
-__global__ __launch_bounds__(64 * kRgWaves) __attribute__((amdgpu_waves_per_eu(4, 4)))
+// SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
+// NCOL x (blocks of a chunk) <= kRgMaxBlocks.
+template <int CM, bool SPLIT, int NCOL>
+__global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
 void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
-    __shared__ RgSmem sm;
+    constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
+    __shared__ RgSmem<NCOL> sm;
     const GemvJob &J = job;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    TaskCtx<1, P8X_ACT_Q8_128> c;
+    TaskCtx<NCOL, P8X_ACT_Q8_128> c;
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
@@ -537,22 +542,22 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     const int nks = SPLIT ? J.nks : 1;
     const int ks = SPLIT ? (int)blockIdx.x % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
     c.b0 = ks * J.kchunk; c.nbl = nbk;
-    const int per = nbk / kRgWaves, rem = nbk % kRgWaves;
+    const int per = nbk / WAVES, rem = nbk % WAVES;
     const int b0 = c.b0 + w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);   // the wave's K range
     // the wave's activation blocks: every load first, the table meanwhile, then the quantization
-    BlockLane in[kRgQ];
+    BlockLane in[RQ];
 #pragma unroll
-    for (int i = 0; i < kRgQ; ++i) {
-        const int bk = c.b0 + w + i * kRgWaves;   // the chunk's block w + 16 i
-        if (w + i * kRgWaves < nbk) in[i].load(J.x + 256 * bk, J.ic + 256 * bk, lane);
+    for (int i = 0; i < RQ; ++i) {
+        const int it = w + i * WAVES, n = it / nbk, bk = c.b0 + it % nbk;   // column, block of the tensor
+        if (it < NCOL * nbk) in[i].load(J.x + (size_t)n * J.ldx + 256 * bk, J.ic + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
-    build_coset_table<64 * kRgWaves>(sm.tab, a2, tid);
+    build_coset_table<64 * WAVES>(sm.tab, a2, tid);
     // the blocks of a wave are independent: quantized G at a time in straight-line code, so their cross-lane
     // chains overlap (one at a time they cost a full chain latency each)
-    if (nbk <= kRgWaves) rg_quantize<1>(nbk, sm, in, w, lane);
-    else if (nbk <= 2 * kRgWaves) rg_quantize<2>(nbk, sm, in, w, lane);
-    else rg_quantize<4>(nbk, sm, in, w, lane);
+    if (NCOL * nbk <= WAVES) rg_quantize<1, NCOL>(nbk, sm, in, w, lane);
+    else if (NCOL * nbk <= 2 * WAVES) rg_quantize<2, NCOL>(nbk, sm, in, w, lane);
+    else rg_quantize<4, NCOL>(nbk, sm, in, w, lane);
     __syncthreads();
     int set = 0;
     const int gstep = (int)gridDim.x / nks;
@@ -561,62 +566,81 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
         // the output row, read before the tile loads so that the epilogue finds it in a register
         int ro = 0;
         if (w == 0 && lane < 32) ro = as_global(J.prmd)[32 * g + lane];
-        float yacc[1] = {0.f};
+        float yacc[NCOL];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
         for (int b = b0; b < b1;) {
             const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
             switch (mt >> 29) {
-                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 1, gemv_nbuf(1, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 2, gemv_nbuf(1, 2), CM == (1 << 2)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 3, gemv_nbuf(1, 3), CM == (1 << 3)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 4, gemv_nbuf(1, 4), CM == (1 << 4)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 5, gemv_nbuf(1, 5), CM == (1 << 5)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 6, gemv_nbuf(1, 6), CM == (1 << 6)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
-                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 7, gemv_nbuf(1, 7), CM == (1 << 7)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 2, gemv_nbuf(NCOL, 2), CM == (1 << 2)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 3, gemv_nbuf(NCOL, 3), CM == (1 << 3)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 4, gemv_nbuf(NCOL, 4), CM == (1 << 4)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 5, gemv_nbuf(NCOL, 5), CM == (1 << 5)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 6, gemv_nbuf(NCOL, 6), CM == (1 << 6)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 7, gemv_nbuf(NCOL, 7), CM == (1 << 7)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
                 default: ++b; break;   // class 0: zero weights
             }
         }
-        yacc[0] += __shfl_xor(yacc[0], 32);
-        if (lane < 32) sm.red[set][w][lane] = yacc[0];
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) {
+            yacc[n] += __shfl_xor(yacc[n], 32);
+            if (lane < 32) sm.red[set][w][n][lane] = yacc[n];
+        }
         // one barrier per row group: a wave writes this set again two groups later, after wave 0 has passed the
         // next group's barrier, so wave 0 has read it by then
         __syncthreads();
         if (w == 0) {
-            float v = 0.f;
-            if (lane < 32)
-                for (int i = 0; i < kRgWaves; ++i) v += sm.red[set][i][lane];
+            float v[NCOL];
+#pragma unroll
+            for (int n = 0; n < NCOL; ++n) {
+                v[n] = 0.f;
+                if (lane < 32)
+                    for (int i = 0; i < WAVES; ++i) v[n] += sm.red[set][i][n][lane];
+            }
             if constexpr (SPLIT) {   // K-chunks: the last arrival sums them in chunk order
                 const gptr<float> wpart = as_global_rw(J.wpart);
                 const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
-                if (lane < 32) __hip_atomic_store(&wpart[(size_t)ks * J.rows + 32 * g + lane], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane < 32)
+#pragma unroll
+                    for (int n = 0; n < NCOL; ++n)
+                        __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * J.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 unsigned old = 0;
                 if (lane == 0) old = __hip_atomic_fetch_add(&wcnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 old = __builtin_amdgcn_readfirstlane(old);
                 if (old != (unsigned)(nks - 1)) continue;
-                v = 0.f;
                 if (lane < 32)
-                    for (int k = 0; k < nks; ++k)
-                        v += __hip_atomic_load(&wpart[(size_t)k * J.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (int n = 0; n < NCOL; ++n) {
+                        v[n] = 0.f;
+                        for (int k = 0; k < nks; ++k)
+                            v[n] += __hip_atomic_load(&wpart[((size_t)k * NCOL + n) * J.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             if (lane < 32) {
                 const int r = ro & 0x7FFF;
-                if (ro & 0x8000) {
-                    const gptr<const float> xr = as_global(J.x);
-                    for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) v += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
+#pragma unroll
+                for (int n = 0; n < NCOL; ++n) {
+                    float vn = v[n];
+                    if (ro & 0x8000) {
+                        const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;
+                        for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) vn += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
+                    }
+                    as_global_rw(J.y)[(size_t)n * J.ldy + r] = vn;
                 }
-                as_global_rw(J.y)[r] = v;
             }
         }
     }
 }
 
-template <int CM>
+template <int CM, int NCOL>
 static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
     // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups per K-chunk, one per CU
     const int per = (ng + num_cus() - 1) / num_cus();
-    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true>), dim3((ng + per - 1) / per * job.nks), dim3(64 * kRgWaves), 0, st, job, a2);
-    else hipLaunchKernelGGL((k_gemv_rg<CM, false>), dim3((ng + per - 1) / per), dim3(64 * kRgWaves), 0, st, job, a2);
+    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL>), dim3((ng + per - 1) / per * job.nks), dim3(64 * rg_waves(NCOL)), 0, st, job, a2);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2);
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 
@@ -823,7 +847,7 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int uni
 int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
-int launch_gemv_rg(int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
+int launch_gemv_rg(int ncols, int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
 
 }  // namespace p8x

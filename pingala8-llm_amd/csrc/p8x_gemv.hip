@@ -83,6 +83,16 @@ int class_set(const size_t hist[8]) {
     return kCmAll;
 }
 
+// K-chunks: enough that a chunk's activations (columns x blocks) fit the LDS buffer; one column also splits in
+// two when the row groups fill at most half the CUs and K is long (e.g. ffn_down)
+int rg_plan(const p8x_tensor *t, int ncols, int *kc) {
+    const int kmax = kRgMaxBlocks / ncols;
+    int nks = (t->nb + kmax - 1) / kmax;
+    if (ncols == 1 && nks == 1 && 2 * t->ng <= num_cus() && t->nb >= 32) nks = 2;
+    *kc = (t->nb + nks - 1) / nks;
+    return (t->nb + *kc - 1) / *kc;
+}
+
 GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
     GemvPlan p;
     const int cm = partials || act != P8X_ACT_Q8_128 ? kCmAll : class_set(t->class_tiles);
@@ -135,12 +145,17 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
         }
         return P8X_OK;
     }
-    if (ncols == 1 && act == P8X_ACT_Q8_128 && !q && t->nb <= kRgMaxBlocks) {   // one linear, x quantized in the launch
-        // two K-chunks when the row groups fill at most half the CUs and K is long (e.g. ffn_down)
-        const int nks = 2 * t->ng <= num_cus() && t->nb >= 2 * kRgWaves && (size_t)2 * t->rows <= t->wpart_floats ? 2 : 1;
-        GemvJob job0;
-        fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, nks, (t->nb + nks - 1) / nks, 1, 0);
-        return launch_gemv_rg(cm, job0, t->ng, t->a2, st);
+    // the row-group kernel: one column, or two columns of a one-class tensor with K <= 8192 (measured faster
+    // than the multi-column task kernel there, slower for longer K and more columns)
+    if (act == P8X_ACT_Q8_128 && !q && (ncols == 1 || (ncols == 2 && t->nb <= 32 && (cm == kCmC3 || cm == kCmC6)))) {
+        // one linear, x quantized in the launch
+        int kc;
+        const int nks = rg_plan(t, ncols, &kc);
+        if (nks == 1 || (size_t)nks * ncols * t->rows <= t->wpart_floats) {
+            GemvJob job0;
+            fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, nks, kc, 1, 0);
+            return launch_gemv_rg(ncols, cm, job0, t->ng, t->a2, st);
+        }
     }
     const GemvPlan p = gemv_plan(t, ncols, act, false);
     if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");

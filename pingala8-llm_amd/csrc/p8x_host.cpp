@@ -222,6 +222,9 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         for (int act : {P8X_ACT_Q8_128, P8X_ACT_Q8_1}) {
             const GemvPlan plan = gemv_plan(t, nc, act, false);
             if (plan.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)plan.nks * nc * rows);
+            int kc;
+            const int rn = rg_plan(t, nc, &kc);
+            if (rn > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)rn * nc * rows);
             if (nc == 1) {
                 const GemvPlan pp = gemv_plan(t, 1, act, true);
                 if (pp.nks > 1) t->wpart_floats = std::max(t->wpart_floats, (size_t)pp.nks * rows);

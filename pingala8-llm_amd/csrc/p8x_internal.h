@@ -60,6 +60,8 @@ struct GemvPlan {
     int bpk, nks, grid, items, gpt;   // gpt: row groups per task (waves per workgroup)
 };
 GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials);
+// K-chunks of the single-call row-group kernel (8-bit-per-128 activations); *kc = blocks per chunk
+int rg_plan(const p8x_tensor *t, int ncols, int *kc);
 
 // launchers (p8x_gemv.hip, p8x_decode.hip, p8x_gemm.hip)
 int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st);

@@ -282,3 +282,20 @@ def test_class_zero_tiles_and_mixed_sets(cp):
         for n in range(ncols):
             assert rel_l2(Yb[n], orc.gemv_f64(X[n])) < 1e-5, (ncols, n)
         batch.release()
+
+
+@pytest.mark.parametrize("rows,K,cp,ncols", [(1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 2), (1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 3),
+                                             (1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 8), (2048, 4096, (0, 0, 0, 1, 0, 0, 0, 0), 2),
+                                             (512, 8192, (0, 0, 0, 0, 0, 0, 1, 0), 2), (256, 30720, (0, 0, 0, 1, 0, 0, 0, 0), 1),
+                                             (512, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 4), (256, 28672, (0, 0, 0, 1, 0, 0, 0, 0), 7)])
+def test_single_call_columns_row_group_kernel(rows, K, cp, ncols):
+    """single calls on one-class tensors: two columns with K <= 8192 and one column of any K (K-chunks past 112
+    blocks) run the row-group kernel, the others the multi-column task kernel; all against fp64"""
+    slot = p8x.synth_random(rows * 7 + K, rows, K, class_p=cp, nd=6)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    X = np.random.default_rng(ncols).standard_normal((ncols, K)).astype(np.float32)
+    for rep in range(2):   # the K-chunk arrival counters are put back for the next call
+        Y = t.mul_mat_vec(X)
+        for n in range(ncols):
+            assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, (rep, n)
