@@ -339,7 +339,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by rows across GPUs, see DESIGN.md", file=sys.stderr)
+              "the GEMV path shards by rows (each GPU streams rows/G of every linear, then one all-gather of y)",
+              file=sys.stderr)
         sys.exit(2)
     if p8x.device_count() < 1:
         print("bench.py: no HIP device", file=sys.stderr)
