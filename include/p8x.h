@@ -105,7 +105,10 @@ int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx
 int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, void *stream);
 /* y = W x for 1..8 columns (vr_mul_mat_vec, CPU.patch:4466-4521): activation prep + fused decode-GEMV +
- * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. */
+ * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. One launch for one column
+ * (and two columns of short K), deterministic. The K-chunk partial rows and arrival counters live in the
+ * tensor's handle: calls on one tensor from different streams must not overlap (on one stream they are
+ * ordered); the counters are put back by each call. Records kernel launches only (capture-safe). */
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
