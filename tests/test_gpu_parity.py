@@ -287,7 +287,9 @@ def test_class_zero_tiles_and_mixed_sets(cp):
 @pytest.mark.parametrize("rows,K,cp,ncols", [(1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 2), (1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 3),
                                              (1024, 14336, (0, 0, 0, 1, 0, 0, 0, 0), 8), (2048, 4096, (0, 0, 0, 1, 0, 0, 0, 0), 2),
                                              (512, 8192, (0, 0, 0, 0, 0, 0, 1, 0), 2), (256, 30720, (0, 0, 0, 1, 0, 0, 0, 0), 1),
-                                             (512, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 4), (256, 28672, (0, 0, 0, 1, 0, 0, 0, 0), 7)])
+                                             (512, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 4), (256, 28672, (0, 0, 0, 1, 0, 0, 0, 0), 7),
+                                             (32, 8192, (0, 0, 0, 1, 0, 0, 0, 0), 1), (32, 8192, (0, 0, 0, 1, 0, 0, 0, 0), 2),
+                                             (32, 256, (0, 0, 0, 1, 0, 0, 0, 0), 2), (32, 256, (0, 0, 0, 1, 0, 0, 0, 0), 1)])
 def test_single_call_columns_row_group_kernel(rows, K, cp, ncols):
     """single calls on one-class tensors: two columns with K <= 8192 and one column of any K (K-chunks past 112
     blocks) run the row-group kernel, the others the multi-column task kernel; all against fp64"""
