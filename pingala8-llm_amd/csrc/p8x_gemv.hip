@@ -327,6 +327,13 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             kcs[order[r]] = (t->nb + nks - 1) / nks;
             have += (long)t->ng * ((t->nb + kcs[order[r]] - 1) / kcs[order[r]]);
         }
+        // a small launch (one layer, say) still has fewer units than waves: every job in units of two blocks or
+        // more, so that more waves stream (the finishing launch sums up to 16 chunks per row)
+        if (have < need)
+            for (int i = 0; i < njobs; ++i) {
+                const int nks = std::min(16, std::max(1, tensors[i]->nb / 2));
+                kcs[i] = (tensors[i]->nb + nks - 1) / nks;
+            }
     }
     for (int i = 0; i < njobs; ++i) {
         const p8x_tensor *t = tensors[i];
