@@ -525,10 +525,13 @@ __device__ __forceinline__ void rg_quantize(int nbk, RgSmem<NCOL> &sm, const Blo
 }
 
 // SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
-// NCOL x (blocks of a chunk) <= kRgMaxBlocks.
-template <int CM, bool SPLIT, int NCOL>
+// NCOL x (blocks of a chunk) <= kRgMaxBlocks. gc row groups at a time: the waves form gc teams of WAVES / gc,
+// team t takes row group g0 + t * (workgroups per chunk) over the chunk, so that a workgroup with several row
+// groups streams them together instead of one after another.
+template <int CM, bool SPLIT, int NCOL, bool TEAMS>
 __global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
-void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
+void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2, int gc_) {
+    const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
     const GemvJob &J = job;
@@ -542,8 +545,10 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     const int nks = SPLIT ? J.nks : 1;
     const int ks = SPLIT ? (int)blockIdx.x % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
     c.b0 = ks * J.kchunk; c.nbl = nbk;
-    const int per = nbk / WAVES, rem = nbk % WAVES;
-    const int b0 = c.b0 + w * per + min(w, rem), b1 = b0 + per + (w < rem ? 1 : 0);   // the wave's K range
+    const int wpg = WAVES / gc, team = w / wpg, wk = w % wpg;   // waves beyond gc teams stay idle
+    const int per = nbk / wpg, rem = nbk % wpg;
+    int b0 = c.b0 + wk * per + min(wk, rem), b1 = b0 + per + (wk < rem ? 1 : 0);   // the wave's K range
+    if (team >= gc) b1 = b0;
     // the wave's activation blocks: every load first, the table meanwhile, then the quantization
     BlockLane in[RQ];
 #pragma unroll
@@ -561,15 +566,17 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
     __syncthreads();
     int set = 0;
     const int gstep = (int)gridDim.x / nks;
-    for (int g = (int)blockIdx.x / nks; g < J.ng; g += gstep, set ^= 1) {
+    for (int g0 = (int)blockIdx.x / nks; g0 < J.ng; g0 += gstep * gc, set ^= 1) {
+        const int g = g0 + min(team, gc - 1) * gstep;   // this wave's row group
+        const bool lead = wk == 0 && team < gc && g < J.ng;   // the team's first wave: epilogue of row group g
         c.g = g;
         // the output row, read before the tile loads so that the epilogue finds it in a register
         int ro = 0;
-        if (w == 0 && lane < 32) ro = as_global(J.prmd)[32 * g + lane];
+        if (lead && lane < 32) ro = as_global(J.prmd)[32 * g + lane];
         float yacc[NCOL];
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
-        for (int b = b0; b < b1;) {
+        for (int b = b0; b < (g < J.ng ? b1 : b0);) {
             const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
             switch (mt >> 29) {
                 case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
@@ -587,16 +594,16 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2) {
             yacc[n] += __shfl_xor(yacc[n], 32);
             if (lane < 32) sm.red[set][w][n][lane] = yacc[n];
         }
-        // one barrier per row group: a wave writes this set again two groups later, after wave 0 has passed the
-        // next group's barrier, so wave 0 has read it by then
+        // one barrier per round of row groups: a wave writes this set again two rounds later, after the team
+        // leads have passed the next round's barrier, so they have read it by then
         __syncthreads();
-        if (w == 0) {
+        if (lead) {
             float v[NCOL];
 #pragma unroll
             for (int n = 0; n < NCOL; ++n) {
                 v[n] = 0.f;
                 if (lane < 32)
-                    for (int i = 0; i < WAVES; ++i) v[n] += sm.red[set][i][n][lane];
+                    for (int i = 0; i < wpg; ++i) v[n] += sm.red[set][w + i][n][lane];
             }
             if constexpr (SPLIT) {   // K-chunks: the last arrival sums them in chunk order
                 const gptr<float> wpart = as_global_rw(J.wpart);
@@ -639,8 +646,11 @@ template <int CM, int NCOL>
 static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
     // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups per K-chunk, one per CU
     const int per = (ng + num_cus() - 1) / num_cus();
-    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL>), dim3((ng + per - 1) / per * job.nks), dim3(64 * rg_waves(NCOL)), 0, st, job, a2);
-    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2);
+    // a workgroup's row groups are streamed together (teams of waves), up to 4 at a time
+    const int gc = std::min(per, 4);
+    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false>), dim3((ng + per - 1) / per * job.nks), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, 1);
+    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, gc);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, 1);
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 

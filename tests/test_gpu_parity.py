@@ -301,3 +301,17 @@ def test_single_call_columns_row_group_kernel(rows, K, cp, ncols):
         Y = t.mul_mat_vec(X)
         for n in range(ncols):
             assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, (rep, n)
+
+
+@pytest.mark.parametrize("rows,K,cp", [(9728, 512, (0, 0, 0, 1, 0, 0, 0, 0)), (24576, 256, (0, 0, 0, 1, 0, 0, 0, 0)),
+                                       (32000, 512, (1, 1, 1, 1, 1, 1, 1, 1))])
+def test_single_call_many_row_groups(rows, K, cp):
+    """more row groups than CUs: a workgroup streams 2-4 row groups at once (teams of waves); one and two columns"""
+    slot = p8x.synth_random(rows + 3 * K, rows, K, class_p=cp, nd=9)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    X = np.random.default_rng(rows).standard_normal((2, K)).astype(np.float32)
+    assert rel_l2(t.mul_mat_vec(X[0])[0], orc.gemv_f64(X[0])) < 1e-5
+    Y = t.mul_mat_vec(X)
+    for n in range(2):
+        assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
