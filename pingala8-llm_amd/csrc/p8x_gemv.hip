@@ -206,8 +206,14 @@ struct FinishJob {
     int rows, nks, ncol;
 };
 
+// a row with clamp-delta entries, resolved when the batch is created: its sorted row (partials) and original
+// row, and its entries [e0, e1) of the batch's (column, value) list, so the tail thread's loads do not wait on
+// one another's results
+struct FinDelta { int job, r, ro, e0, e1; };
+struct FinEntry { int col; float val; };
+
 __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
-                                                     const int2 *__restrict__ drows, int ndrows) {
+                                                     const FinDelta *__restrict__ drows, const FinEntry *__restrict__ ent, int ndrows) {
     if ((int)blockIdx.x < nplain) {
         const uint32_t e = as_const(blk_job)[blockIdx.x];
         if (e == kFinNone) return;
@@ -233,18 +239,17 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
     } else {
         const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
         if (i >= ndrows) return;
-        const FinishJob &J = jobs[drows[i].x];
-        const int ro = drows[i].y;
-        const int r = as_global(J.pinv)[ro];
+        const FinDelta d = drows[i];
+        const FinishJob &J = jobs[d.job];
         const gptr<const float> wp = as_global(J.wpart);
         for (int n = 0; n < J.ncol; ++n) {
             float v = 0.f;
-            for (int ks = 0; ks < J.nks; ++ks) v += wp[((size_t)ks * J.ncol + n) * J.rows + r];
+            for (int ks = 0; ks < J.nks; ++ks) v += wp[((size_t)ks * J.ncol + n) * J.rows + d.r];
             if (J.x) {
                 const gptr<const float> x = as_global(J.x) + (size_t)n * J.ldx;
-                for (int e = as_global(J.cp)[ro]; e < as_global(J.cp)[ro + 1]; ++e) v += as_global(J.cv)[e] * x[as_global(J.cc)[e]];
+                for (int e = d.e0; e < d.e1; ++e) v += as_global(ent)[e].val * x[as_global(ent)[e].col];
             }
-            as_global_rw(J.y)[(size_t)n * J.ldy + ro] = v;
+            as_global_rw(J.y)[(size_t)n * J.ldy + d.ro] = v;
         }
     }
 }
@@ -257,7 +262,8 @@ struct p8x_gemv_batch {
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
     uint32_t *d_fblk = nullptr;        // its block -> job
-    int2 *d_fdrows = nullptr;          // its rows with clamp-delta entries: (job, original row)
+    p8x::FinDelta *d_fdrows = nullptr; // its rows with clamp-delta entries
+    p8x::FinEntry *d_fent = nullptr;   // and their (column, value) entries
     int fin_blocks = 0, fin_ndrows = 0;
     const uint32_t *a2 = nullptr;
     p8x::GemvJob *d_jobs = nullptr;
@@ -279,6 +285,7 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
     if (b->d_fin) (void)hipFree(b->d_fin);
     if (b->d_fblk) (void)hipFree(b->d_fblk);
     if (b->d_fdrows) (void)hipFree(b->d_fdrows);
+    if (b->d_fent) (void)hipFree(b->d_fent);
     if (b->work) (void)hipFree(b->work);
     delete b;
 }
@@ -381,7 +388,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         for (int i = 0; i < njobs; ++i)
             for (int u = 0; u < jobs[i].ntasks; ++u) uj[(size_t)jobs[i].task0 + u] = (uint32_t)i;
         std::vector<FinishJob> fin(njobs);
-        std::vector<int2> fdr;
+        std::vector<FinDelta> fdr;
+        std::vector<FinEntry> fent;
         // jobs to XCDs, largest first onto the least loaded; then block 8k + x = the k-th block of XCD x's jobs
         std::vector<std::vector<uint32_t>> xb(kXcds);
         std::vector<int> order(njobs);
@@ -402,20 +410,40 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             const GemvJob &g = jobs[i];
             const p8x_tensor *t = tensor_of[g.M];
             fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.ldx, g.ldy, g.rows, g.nks, ncols};
-            for (int r : t->dorig) fdr.push_back(make_int2(i, r));
+            if (t->dorig.empty()) continue;
+            // the tensor's delta CSR and inverse permutation, read back once (set-up time)
+            std::vector<int> cp(t->rows + 1);
+            std::vector<int16_t> pinv(t->rows);
+            std::vector<uint16_t> cc(std::max(1, t->nd));
+            std::vector<float> cv(std::max(1, t->nd));
+            if ((rc = hip_check(hipMemcpy(cp.data(), t->cp, 4 * cp.size(), hipMemcpyDeviceToHost), "p8x_gemv_batch_create: delta rows")) ||
+                (rc = hip_check(hipMemcpy(pinv.data(), t->pinv, 2 * pinv.size(), hipMemcpyDeviceToHost), "p8x_gemv_batch_create: delta rows")) ||
+                (t->nd > 0 && (rc = hip_check(hipMemcpy(cc.data(), t->cc, 2 * (size_t)t->nd, hipMemcpyDeviceToHost), "p8x_gemv_batch_create: delta rows"))) ||
+                (t->nd > 0 && (rc = hip_check(hipMemcpy(cv.data(), t->cv, 4 * (size_t)t->nd, hipMemcpyDeviceToHost), "p8x_gemv_batch_create: delta rows")))) {
+                p8x_gemv_batch_release(b);
+                return rc;
+            }
+            for (int ro : t->dorig) {
+                const int e0 = (int)fent.size();
+                for (int e = cp[ro]; e < cp[ro + 1]; ++e) fent.push_back(FinEntry{(int)cc[e], cv[e]});
+                fdr.push_back(FinDelta{i, (int)pinv[ro], ro, e0, (int)fent.size()});
+            }
         }
         b->fin_blocks = (int)fblk.size();
         b->fin_ndrows = (int)fdr.size();
         if (hipMalloc((void **)&b->d_fin, sizeof(FinishJob) * njobs) != hipSuccess ||
             hipMalloc((void **)&b->d_fblk, 4 * fblk.size()) != hipSuccess ||
-            hipMalloc((void **)&b->d_fdrows, sizeof(int2) * std::max<size_t>(1, fdr.size())) != hipSuccess) {
+            hipMalloc((void **)&b->d_fdrows, sizeof(FinDelta) * std::max<size_t>(1, fdr.size())) != hipSuccess ||
+            hipMalloc((void **)&b->d_fent, sizeof(FinEntry) * std::max<size_t>(1, fent.size())) != hipSuccess) {
             p8x_gemv_batch_release(b);
             return set_error(P8X_ERR_NOMEM, "p8x_gemv_batch_create: finishing jobs");
         }
         if ((rc = hip_check(hipMemcpy(b->d_fin, fin.data(), sizeof(FinishJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing jobs")) ||
             (rc = hip_check(hipMemcpy(b->d_fblk, fblk.data(), 4 * fblk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: finishing blocks")) ||
-            (!fdr.empty() && (rc = hip_check(hipMemcpy(b->d_fdrows, fdr.data(), sizeof(int2) * fdr.size(), hipMemcpyHostToDevice),
-                                             "p8x_gemv_batch_create: finishing delta rows")))) {
+            (!fdr.empty() && (rc = hip_check(hipMemcpy(b->d_fdrows, fdr.data(), sizeof(FinDelta) * fdr.size(), hipMemcpyHostToDevice),
+                                             "p8x_gemv_batch_create: finishing delta rows"))) ||
+            (!fent.empty() && (rc = hip_check(hipMemcpy(b->d_fent, fent.data(), sizeof(FinEntry) * fent.size(), hipMemcpyHostToDevice),
+                                              "p8x_gemv_batch_create: finishing delta entries")))) {
             p8x_gemv_batch_release(b);
             return rc;
         }
@@ -453,7 +481,7 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     if (stage == 2) {   // partial rows to original rows with the clamp delta
         const int blocks = b->fin_blocks + (b->fin_ndrows + 255) / 256;
         hipLaunchKernelGGL(k_gemv_finish, dim3(blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
-                           b->fin_blocks, (const int2 *)b->d_fdrows, b->fin_ndrows);
+                           b->fin_blocks, (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
