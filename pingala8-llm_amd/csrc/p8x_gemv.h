@@ -476,15 +476,16 @@ static int launch_gemv_t(const GemvJob &job0, int tasks, const uint32_t *a2, hip
 }
 
 // ------------------------------------------------------------------------------------------------ single GEMV, latency path
-// One column of 8-bit-per-128 activations, one linear per launch (the drop-in p8x_mul_mat_vec call). Such a
-// launch has few tiles, so latency rules: a workgroup takes whole 32-row groups over its K-chunk (the whole K,
-// or one of J.nks chunks when the tensor has too few row groups to fill the CUs), quantizes that part of the
-// activations itself into LDS once (the prep's arithmetic, one wave per block), its waves split the chunk into
-// contiguous block ranges, and the partial rows meet in LDS in a fixed order. K-chunks of a row group meet
-// through the fixed-order fix-up of the multi-column kernel (agent-coherent partial rows, an arrival counter,
-// the last arrival sums the chunks in order).
+// 8-bit-per-128 activations, one linear per launch (the drop-in p8x_mul_mat_vec call; one column, or two of a
+// one-class tensor). Such a launch has few tiles, so latency rules: a workgroup takes whole 32-row groups over
+// its K-chunk (the whole K, or one of J.nks chunks when the activations do not fit the LDS buffer at once or
+// the tensor has too few row groups to fill the CUs), quantizes that part of the activations itself into LDS
+// once (the prep's arithmetic, one wave per 256-block and column), its waves split the chunk into contiguous
+// block ranges, and the partial rows meet in LDS in a fixed order. K-chunks of a row group meet through the
+// fixed-order fix-up of the multi-column kernel (agent-coherent partial rows, an arrival counter, the last
+// arrival sums the chunks in order).
 constexpr int kRgMaxBlocks = 112;   // activation blocks in LDS (columns x blocks of the K-chunk)
-// up to two columns: 16 waves at 128 VGPRs; more: 8 waves at 256
+// up to two columns: 16 waves at 128 VGPRs; more (instantiable, measured slower than the task kernel): 8 at 256
 __host__ __device__ constexpr int rg_waves(int ncol) { return ncol <= 2 ? 16 : 8; }
 
 template <int NCOL, int WAVES = rg_waves(NCOL)>
