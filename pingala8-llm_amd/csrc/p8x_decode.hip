@@ -25,6 +25,7 @@ __host__ __device__ constexpr int dec_nw(int cm) { return cm == (1 << 3) ? 8 : 2
 
 struct DecodeArgs {
     const uint32_t *M; const uint16_t *S; const uint32_t *D; const uint32_t *a2; const int16_t *prm;
+    const uint16_t *prmd;   // prm with bit 15 set on rows that carry clamp-delta entries
     const float *ic; const int *cp; const uint16_t *cc; const float *cv;
     void *out; size_t ld;
     int rows, K, nb, ng;
@@ -135,17 +136,17 @@ __device__ __forceinline__ void walk_tiles(const DecodeArgs &a, size_t first, si
         const uint32_t mt = a.M[(size_t)g * a.nb + b];
         nx.c = (int)(mt >> 29);
         load_any<CM>(nx.raw, nx.c, a.D + (mt & 0x1FFFFFFFu) + hs * nw_of(nx.c) * 32, j, a.S + (size_t)b * a.rows + 32 * g);
-        if (want_rows) {
-            nx.ro = a.prm[32 * g + j];
-            nx.e0 = a.cp[nx.ro];
-            nx.e1 = a.cp[nx.ro + 1];
-        }
+        // the flagged row only: its delta range is read when the tile is decoded, and only for flagged rows, so
+        // no load here waits on another (a dependent load would wait for the payload issued before it)
+        if (want_rows) nx.ro = a.prmd[32 * g + j];
     };
     issue(first);
     for (size_t q = first; q < last; q += stride) {
         AnySlice<NW> ls;
         prepare_any<CM>(ls, nx.c, nx.raw, j);   // consumes this tile's words
-        const int c = nx.c, ro = nx.ro, e0 = nx.e0, e1 = nx.e1;
+        const int c = nx.c, ro = nx.ro & 0x7FFF;
+        int e0 = 0, e1 = 0;
+        if (want_rows && (nx.ro & 0x8000)) { e0 = a.cp[ro]; e1 = a.cp[ro + 1]; }
         issue(q + stride < last ? q + stride : q);   // the next tile's words load during this tile
         int g, b;
         tile_of(a, q, g, b);
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
 
 static DecodeArgs decode_args(const p8x_tensor *t, void *out, size_t ld) {
     DecodeArgs a{};
-    a.M = t->M; a.S = t->S; a.D = t->D; a.a2 = t->a2; a.prm = t->prm;
+    a.M = t->M; a.S = t->S; a.D = t->D; a.a2 = t->a2; a.prm = t->prm; a.prmd = t->prmd;
     a.ic = t->ic; a.cp = t->cp; a.cc = t->cc; a.cv = t->cv;
     a.out = out; a.ld = ld;
     a.rows = t->rows; a.K = t->K; a.nb = t->nb; a.ng = t->ng; a.nt = t->nt;
