@@ -304,6 +304,23 @@ __device__ __forceinline__ int gemv_run(const TaskCtx<NCOL, ACT> &c, const SM &s
 // prefetch depth (register buffers) per variant
 __host__ __device__ constexpr int gemv_nbuf(int ncol, int c) { return ncol == 1 && c == 3 ? GEMV_NBUF_C3 : 2; }
 
+// K-chunk fix-up publication. The chunk's partial rows go out as agent-scope atomic stores (on gfx950 these
+// carry sc1: written through the XCD's L2 to the agent's coherence point, so a workgroup on another XCD sees
+// them). A vector store counts against vmcnt until the memory system acknowledges it, and stores and atomics to
+// different addresses may complete out of order, so the wave waits for vmcnt(0) before it counts its arrival:
+// when another wave's arrival RMW returns a count that includes this one, these stores are complete. This is the
+// agent-scope release of the AMDGPU memory model without its L2 write-back, which only plain (cached) stores
+// need. The last arrival's loads are agent-scope atomic loads (sc1, served from the coherence point) issued after
+// its RMW returned. Returns the counter's value before the increment (wave-uniform).
+__device__ __forceinline__ unsigned arrive_after_stores(unsigned *ctr, int lane) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // partial-row stores complete before the arrival
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    __asm__ volatile("" ::: "memory");   // the partial loads that follow stay below the arrival
+    return old;
+}
+
 // The row group's sums after one K-chunk: the two half-slices meet through one cross-lane add; the K-chunks of
 // the row group meet in a fixed order (the last-arriving wave sums them), so results are deterministic; then the
 // clamp delta and the row permutation on the way out.
@@ -317,19 +334,16 @@ __device__ __forceinline__ void gemv_rows_out(const GemvJob &J, int g, int ks, i
     for (int n = 0; n < NCOL; ++n) yacc[n] += __shfl_xor(yacc[n], 32);
     bool final_rows = J.nks == 1;
     if (J.nks > 1) {
-        // K-chunk fix-up, no agent-scope fences (on gfx950 those write back and invalidate the XCD's whole L2):
-        // partial rows are agent-coherent stores; the wave waits for them, then bumps the row group's arrival
-        // counter; the last arrival reads the partials with agent-coherent loads and sums them in chunk order.
+        // K-chunk fix-up without agent-scope fences (on gfx950 those write back and invalidate the XCD's whole
+        // L2): agent-coherent partial rows, the arrival counted once they are complete (arrive_after_stores), the
+        // last arrival reads the partials with agent-coherent loads and sums them in chunk order.
         const gptr<float> wpart = as_global_rw(J.wpart);
-        const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
         if (lane < 32)
 #pragma unroll
             for (int n = 0; n < NCOL; ++n)
                 __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * J.rows + 32 * g + j], yacc[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(&wcnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __builtin_amdgcn_readfirstlane(old);
+        const unsigned old = arrive_after_stores(J.wcnt + g, lane);
+        const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
         final_rows = old == (unsigned)(J.nks - 1);
         if (final_rows) {
             if (lane < 32)
@@ -615,11 +629,7 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2, int gc_) {
 #pragma unroll
                     for (int n = 0; n < NCOL; ++n)
                         __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * J.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                unsigned old = 0;
-                if (lane == 0) old = __hip_atomic_fetch_add(&wcnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                old = __builtin_amdgcn_readfirstlane(old);
-                if (old != (unsigned)(nks - 1)) continue;
+                if (arrive_after_stores(J.wcnt + g, lane) != (unsigned)(nks - 1)) continue;
                 if (lane < 32)
 #pragma unroll
                     for (int n = 0; n < NCOL; ++n) {
