@@ -93,7 +93,9 @@ int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, voi
  * (d = amax/127), sum [ncols][K/128] (sum of q; may be NULL). Bit-exact to vrc_prep_block / k_vr_qx_real. */
 int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx,
                         int8_t *q, float *d, int32_t *sum, void *stream);
-/* x' quantized to ggml block_q8_1 (36 B: fp16 d, fp16 s, 32 x int8), [ncols][K/32] blocks. */
+/* x' quantized to ggml block_q8_1 (36 B: fp16 d, fp16 s, 32 x int8), [ncols][K/32] blocks, with ggml's
+ * quantize_row_q8_1_ref convention: d = amax/127, q = roundf(x' * (1/d)) (ties away from zero), s = fp16(d * sum q).
+ * The products read d and q only, so blocks from another q8_1 producer (ggml's CUDA kernel, say) are accepted. */
 int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, void *stream);
 
 /* ---- products --------------------------------------------------------------------------------------- */
@@ -135,6 +137,11 @@ int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
  * partials per K-chunk and column), 2 = partials to original rows with the clamp delta */
 int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream);
 void p8x_gemv_batch_release(p8x_gemv_batch *b);
+/* The launch plan of a batch: work units (a 32-row group over a K-chunk), jobs cut along K, waves of the launch,
+ * class_set (bit c: tile class c is decoded), small_launch = 1 when the batch had fewer whole-K units than two
+ * rounds of the launch's waves and every job was cut into units of two or more blocks. */
+typedef struct p8x_batch_info { int njobs, ncols, class_set, units, split_jobs, small_launch, waves; } p8x_batch_info;
+int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out);
 
 /* ---- host-side producers (not on the hot path) -------------------------------------------------------- */
 /* Random valid tensor slot (the reference's random-valid timing arm, CPU.patch:4391-4458). class_p[8] are

@@ -62,6 +62,7 @@ def lib():
         L.orc_partials_q8_1.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
         L.orc_gemv_q8_128_f64.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
         L.orc_gemv_q8_1_f64.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
+        L.orc_gemv_q8_128_f64_cols.argtypes = [ctypes.POINTER(OrcTensor), vp, i, sz, vp]
         L.orc_dense_f64.argtypes = [vp, i, i, vp, i, vp]
         L.orc_h2f.argtypes = [ctypes.c_uint16]; L.orc_h2f.restype = ctypes.c_float
         L.orc_f2h.argtypes = [ctypes.c_float]; L.orc_f2h.restype = ctypes.c_uint16
@@ -152,6 +153,13 @@ class Oracle:
         fn = lib().orc_gemv_q8_128_f64 if act == "q8_128" else lib().orc_gemv_q8_1_f64
         fn(ctypes.byref(self.t), _p(x), _p(y))
         return y
+
+    def gemv_f64_cols(self, X):
+        """fp64 GEMV of every row of X [ncols][K] (8-bit-per-128 activations), each tile decoded once"""
+        X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
+        Y = np.zeros((X.shape[0], self.rows), np.float64)
+        lib().orc_gemv_q8_128_f64_cols(ctypes.byref(self.t), _p(X), X.shape[0], X.shape[1], _p(Y))
+        return Y
 
     @property
     def ic(self):

@@ -358,7 +358,11 @@ void orc_prep_x16(const orc_tensor *t, const float *x, int8_t *qh, float *dh, in
     }
 }
 
-/* ggml block_q8_1 over x' (llama.cpp quantize_row_q8_1 semantics: d = amax/127, q = round-half-away(x/d), s = d * sum q) */
+/* ggml block_q8_1 over x', following ggml's quantize_row_q8_1_ref (llama.cpp @7ac59a6, not vendored in the reference):
+ * d = amax/127, id = 1/d, q = roundf(x * id) (ties away from zero), d stored as fp16, s = fp16(d * sum q).
+ * The reference calls ggml's CUDA quantize_row_q8_1_cuda at CPU.patch:1576 and restates its rounding as rintf(x/d) in
+ * its own check at CPU.patch:2283-2286; the conventions differ only at exact ties (and in s, which the VR products do
+ * not read). Pinned by crafted ties in tests/test_oracle.py. */
 void orc_quantize_q8_1(const orc_tensor *t, const float *x, uint8_t *blocks) {
     float *xr = (float *)malloc(sizeof(float) * (size_t)t->K);
     orc_rotate_act(t, x, xr);
@@ -431,6 +435,41 @@ void orc_gemv_q8_128_f64(const orc_tensor *t, const float *x, double *y) {
         y[t->prm[r]] = acc;
     }
     add_delta_f64(t, x, y);
+    free(q); free(d); free(sx); free(isum);
+}
+
+/* the same fp64 GEMV for ncols activation columns x [ncols][ldx] -> y [ncols][rows], each tile decoded once;
+ * per column the arithmetic (integer partials, then the half-slice sum in order) is orc_gemv_q8_128_f64's */
+void orc_gemv_q8_128_f64_cols(const orc_tensor *t, const float *x, int ncols, size_t ldx, double *y) {
+    int8_t *q = (int8_t *)malloc((size_t)t->K * ncols);
+    float *d = (float *)malloc(sizeof(float) * (size_t)t->nsl * ncols);
+    int32_t *sx = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->nsl);
+    int32_t *isum = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->rows * t->nsl * ncols);
+    int16_t tile[32 * 256];
+    for (int n = 0; n < ncols; ++n) orc_prep_q8_128(t, x + (size_t)n * ldx, q + (size_t)n * t->K, d + (size_t)n * t->nsl, sx);
+    for (int g = 0; g < t->ng; ++g)
+        for (int b = 0; b < t->nb; ++b) {
+            orc_decode_tile(t, g, b, tile);
+            for (int n = 0; n < ncols; ++n)
+                for (int j = 0; j < 32; ++j)
+                    for (int hs = 0; hs < 2; ++hs) {
+                        const int8_t *qn = q + (size_t)n * t->K + 256 * b + 128 * hs;
+                        int64_t s = 0;
+                        for (int i = 0; i < 128; ++i) s += (int64_t)tile[j * 256 + 128 * hs + i] * qn[i];
+                        isum[((size_t)n * t->rows + 32 * g + j) * t->nsl + 2 * b + hs] = (int32_t)s;
+                    }
+        }
+    for (int n = 0; n < ncols; ++n) {
+        double *yn = y + (size_t)n * t->rows;
+        for (int r = 0; r < t->rows; ++r) {
+            double acc = 0.0;
+            for (int s = 0; s < t->nsl; ++s)
+                acc += (double)isum[((size_t)n * t->rows + r) * t->nsl + s] * (double)d[(size_t)n * t->nsl + s] *
+                       (double)orc_h2f(t->S[(size_t)(s >> 1) * t->rows + r]);
+            yn[t->prm[r]] = acc;
+        }
+        add_delta_f64(t, x + (size_t)n * ldx, yn);
+    }
     free(q); free(d); free(sx); free(isum);
 }
 

@@ -103,6 +103,8 @@ void orc_partials_q8_1(const orc_tensor *t, const uint8_t *blocks, int32_t *isum
 /* fp64 GEMV: y[prm[r]] = sum_s S*XS*isum + delta . x (original rows) */
 void orc_gemv_q8_128_f64(const orc_tensor *t, const float *x, double *y);
 void orc_gemv_q8_1_f64(const orc_tensor *t, const float *x, double *y);
+/* orc_gemv_q8_128_f64 for ncols columns x [ncols][ldx] -> y [ncols][rows] (each tile decoded once) */
+void orc_gemv_q8_128_f64_cols(const orc_tensor *t, const float *x, int ncols, size_t ldx, double *y);
 /* fp64 dense product with the f32-dequantized weights (prompt GEMM reference): y[n][r] = W[r] . x[n] */
 void orc_dense_f64(const float *W, int rows, int K, const float *x, int N, double *y);
 

@@ -258,6 +258,7 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
 
 struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
+    int split_jobs = 0, small_launch = 0, waves = 0;   // plan facts reported by p8x_gemv_batch_info
     unsigned *ctr = nullptr;       // its unit counters (in work)
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
@@ -318,6 +319,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     const int cm = class_set(hist);
     // wave-independent units: (row group, whole K)
     std::vector<int> kcs(njobs);
+    bool small_launch = false;
     for (int i = 0; i < njobs; ++i) kcs[i] = tensors[i]->nb;
     {
         // Units are handed out longest first, so the launch drains on the units of the last jobs. Those jobs are
@@ -336,7 +338,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         }
         // a small launch (one layer, say) still has fewer units than waves: every job in units of two blocks or
         // more, so that more waves stream (the finishing launch sums up to 16 chunks per row)
-        if (have < need)
+        small_launch = have < need;
+        if (small_launch)
             for (int i = 0; i < njobs; ++i) {
                 const int nks = std::min(16, std::max(1, tensors[i]->nb / 2));
                 kcs[i] = (tensors[i]->nb + nks - 1) / nks;
@@ -382,6 +385,9 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     int task0 = 0;
     for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
     b->total_tasks = task0;
+    b->small_launch = small_launch;
+    b->waves = wave_wg_per_cu(cm, ncols) * num_cus() * wave_waves(cm, ncols);
+    for (int i = 0; i < njobs; ++i) b->split_jobs += kcs[i] < tensors[i]->nb;
     {
         // unit -> job table
         std::vector<uint32_t> uj((size_t)task0);
@@ -485,6 +491,13 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
+}
+
+int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out) {
+    if (!b || !out) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_info: null pointer");
+    out->njobs = b->njobs; out->ncols = b->ncols; out->class_set = b->cm; out->units = b->total_tasks;
+    out->split_jobs = b->split_jobs; out->small_launch = b->small_launch; out->waves = b->waves;
+    return P8X_OK;
 }
 
 int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream) {

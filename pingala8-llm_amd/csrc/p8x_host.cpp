@@ -170,15 +170,13 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         if (sg[i] != 1 && sg[i] != -1) return set_error(P8X_ERR_FORMAT, "p8x_prepare: Hadamard sign %d is %d", i, sg[i]);
 
     // derived host data
+    // coset entries A[f] + c with the CPU core's bytewise int8 add (CPU.patch:221, :255), which wraps when |A + c|
+    // exceeds 127; every kernel decodes through this table, so products equal dequantize_row's weights times x
+    // for any codebook (the shipped one never wraps: A + c lies in [-76, 62])
     std::vector<uint32_t> a2(512);
-    bool wrap_free = true;
     for (int f = 0; f < 256; ++f) {
         a2[f] = hdr[f];
         a2[256 + f] = add_bytes(hdr[f], hdr[512]);
-        for (int e = 0; e < 4; ++e) {
-            const int s = (int)(int8_t)(hdr[f] >> (8 * e)) + (int)(int8_t)(hdr[512] >> (8 * e));
-            if (s < -128 || s > 127) wrap_free = false;
-        }
     }
     std::vector<float> ic(K);
     for (int k = 0; k < K; ++k) ic[k] = (float)sg[k & 255] / half_to_float(c16[k]);
@@ -197,7 +195,6 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->n = n; t->nt = nt; t->kbytes = kbytes;
     t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
-    t->wrap_free = wrap_free;
     memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
     auto fail = [&](int code) { p8x_release(t); return code; };

@@ -47,7 +47,6 @@ struct p8x_tensor {
     size_t wx16_elems = 0;           // capacity in bytes
     float *wmm = nullptr;            // prompt GEMM: K-split partial planes (grown on demand)
     size_t wmm_bytes = 0;
-    bool wrap_free = true;           // |A + c| <= 127 bytewise
     uint32_t a2_host[512];           // host copy of a2 (batches check that tensors share the tables)
 };
 

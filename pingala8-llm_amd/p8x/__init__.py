@@ -22,7 +22,7 @@ EXPORTS = [
     "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
     "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_mul_mat_reserve", "p8x_synth_random",
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
-    "p8x_gemv_batch_release",
+    "p8x_gemv_batch_release", "p8x_gemv_batch_info",
 ]
 
 
@@ -34,6 +34,10 @@ class Info(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_int), ("K", ctypes.c_int), ("nd", ctypes.c_int), ("ng", ctypes.c_int), ("nb", ctypes.c_int),
                 ("n", ctypes.c_size_t), ("kbytes", ctypes.c_size_t), ("stream_bytes", ctypes.c_size_t),
                 ("class_tiles", ctypes.c_size_t * 8), ("dev_base", ctypes.c_void_p)]
+
+
+class BatchInfo(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int) for f in ("njobs", "ncols", "class_set", "units", "split_jobs", "small_launch", "waves")]
 
 
 _lib = None
@@ -73,6 +77,7 @@ def lib():
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
     L.p8x_gemv_batch_release.argtypes = [vp]; L.p8x_gemv_batch_release.restype = None
+    L.p8x_gemv_batch_info.argtypes = [vp, ctypes.POINTER(BatchInfo)]
     _lib = L
     return L
 
@@ -424,6 +429,11 @@ class GemvBatch:
         self.h = ctypes.c_void_p()
         check(lib().p8x_gemv_batch_create(T, X, LX, Y, LY, n, ncols, ctypes.byref(self.h)), "p8x_gemv_batch_create")
         self._keep = (tensors, xs, ys)
+
+    def info(self):
+        inf = BatchInfo()
+        check(lib().p8x_gemv_batch_info(self.h, ctypes.byref(inf)), "p8x_gemv_batch_info")
+        return {f: getattr(inf, f) for f, _ in BatchInfo._fields_}
 
     def run(self, stream=None):
         check(lib().p8x_gemv_batch_run(self.h, stream.h if stream else None), "p8x_gemv_batch_run")

@@ -49,6 +49,13 @@ def random_tables(rng):
     return A, c
 
 
+def wrapping_tables(rng):
+    """A over the whole int8 range and a large c, so that many A + c leave [-128, 127] (the bytewise add wraps)"""
+    A = rng.integers(-128, 128, size=(256, 4)).astype(np.int8).view(np.uint32).reshape(256).copy()
+    c = int(np.array([100, -90, 77, -120], np.int8).view(np.uint32)[0])
+    return A, c
+
+
 def build_slot(A, cs, cls, payload, S, c16, prm, sg, drow=None, dcol=None, dval=None, extra=0):
     """cls int[ng, nb]; payload uint32 in tile order (tile i = g*nb + b has 64*NW(cls) words);
     S uint16 [nb, rows]; c16 uint16 [K]; prm int16 [rows]; sg int8 [256]; delta arrays (original indices)."""
@@ -97,7 +104,7 @@ def random_slot(rng, rows, K, classes=(3,), class_p=None, tables="shipped", nd=0
                 c16="random", scale_range=(2e-4, 3e-4), extra=0):
     """A random-valid tensor. classes: classes drawn per tile (with probabilities class_p)."""
     ng, nb = rows // 32, K // 256
-    A, cs = shipped_tables() if tables == "shipped" else random_tables(rng)
+    A, cs = {"shipped": shipped_tables, "random": lambda: random_tables(rng), "wrapping": lambda: wrapping_tables(rng)}[tables]()
     cls = rng.choice(np.asarray(classes), size=(ng, nb), p=class_p).astype(np.int64)
     nwords = int(sum(64 * NW[c] for c in cls.reshape(-1)))
     payload = rng.integers(0, 1 << 32, size=nwords, dtype=np.uint64).astype(np.uint32)
@@ -118,3 +125,20 @@ def random_slot(rng, rows, K, classes=(3,), class_p=None, tables="shipped", nd=0
         dcol = (flat % K).astype(np.uint16)
         dval = rng.uniform(-0.05, 0.05, size=nd).astype(np.float32)
     return build_slot(A, cs, cls, payload, S, c16v, prm, sg, drow, dcol, dval, extra=extra)
+
+
+def tie_case(rng, K=512, k=2):
+    """A 32 x K class-3 tensor with c16 = 1 and an activation x whose rotated values x' land exactly on quantizer
+    ties. In 256-block b = 0, 1 only x'[0] = a, x'[1] = b are non-zero before the transform, so after FWHT256 / 16
+    every even column holds (a + b) / 16 = 127 and every odd column (a - b) / 16 = +-(k + 1/2) (block 0: +, block 1:
+    -). Every scale is then d = 127 / 127 = 1 exactly (both per 32 and per 128 columns), so x' / d is exactly
+    +-(k + 1/2): round-half-away gives +-(k + 1), round-half-even gives +-k (k even). Blocks past 1 are zero.
+    Returns (slot bytes, x, k)."""
+    buf = random_slot(rng, 32, K, classes=(3,), c16="ones", permute=False)
+    sg = buf[offsets(buf.size, 32, K, 0)["SG"]:][:256].view(np.int8).astype(np.float32)
+    a, b = (2032 + 16 * k + 8) // 2, (2032 - 16 * k - 8) // 2      # a + b = 16 * 127, a - b = 16 (k + 1/2)
+    x = np.zeros(K, np.float32)
+    # x * ic = x * sg / c must be (a, b) at columns 0, 1 of block 0 and (b, a) of block 1
+    x[0], x[1] = a * sg[0], b * sg[1]
+    x[256], x[257] = b * sg[0], a * sg[1]
+    return buf, x, k

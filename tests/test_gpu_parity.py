@@ -315,3 +315,43 @@ def test_single_call_many_row_groups(rows, K, cp):
     Y = t.mul_mat_vec(X)
     for n in range(2):
         assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
+
+
+def test_activation_ties_match_oracle():
+    """x' exactly on k + 1/2 with d = 1: block_q8_1 rounds half away from zero (+-(k+1)) and stores s = d * sum q;
+    the 8-bit-per-128 prep rounds half to even (+-k) like the reference core; GPU blocks bitwise equal to the oracle"""
+    import slotgen
+    buf, x, k = slotgen.tie_case(np.random.default_rng(12), K=512, k=2)
+    t = p8x.Tensor(buf, 32, 512)
+    orc = O.Oracle(buf, 32, 512)
+    blk = t.quantize_q8_1(x)[0]
+    assert np.array_equal(blk, orc.quantize_q8_1(x))
+    q = blk.reshape(-1, 36)[:, 4:].view(np.int8)
+    assert np.all(q[:8, 1::2] == k + 1) and np.all(q[8:16, 1::2] == -(k + 1))
+    q8, d8, s8 = t.quantize_q8_128(x)
+    oq, od, osx = orc.prep_q8_128(x)
+    assert np.array_equal(q8[0], oq) and np.array_equal(d8[0], od) and np.array_equal(s8[0], osx)
+    assert np.all(q8[0][1:256:2] == k) and np.all(q8[0][257:512:2] == -k)
+    # the products on these activations
+    assert rel_l2(t.mul_mat_vec(x)[0], orc.gemv_f64(x)) < 1e-5
+    assert rel_l2(t.mul_mat_vec(x, act=p8x.ACT_Q8_1)[0], orc.gemv_f64(x, act="q8_1")) < 1e-5
+
+
+def test_wrapping_codebook():
+    """a codebook whose A + c leaves the int8 range: every kernel decodes through the bytewise (wrapping) coset add
+    of the reference CPU core, so ints, dequantized bits, GEMV and GEMM agree with the oracle"""
+    import slotgen
+    rng = np.random.default_rng(14)
+    rows, K = 256, 2048
+    buf = slotgen.random_slot(rng, rows, K, classes=(1, 2, 3, 4, 5, 6, 7), tables="wrapping", nd=4)
+    t = p8x.Tensor(buf, rows, K)
+    orc = O.Oracle(buf, rows, K)
+    assert np.array_equal(t.decode_rotated(p8x.I16), orc.decode_all())
+    W = orc.dequant()
+    assert np.array_equal(t.dequantize(p8x.F32).view(np.uint32), W.view(np.uint32))
+    X = rng.standard_normal((3, K)).astype(np.float32)
+    Y = t.mul_mat_vec(X)
+    for n in range(3):
+        assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
+    Xm = rng.standard_normal((40, K)).astype(np.float32)
+    assert rel_l2(t.mul_mat(Xm, p8x.F32), O.dense_f64(W, Xm)) < 1e-3

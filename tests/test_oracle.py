@@ -195,6 +195,56 @@ def test_q8_1_blocks_definition(case):
     assert np.array_equal(isum.astype(np.int64), np.einsum("rsk,sk->rs", ints, q))
 
 
+def test_q8_1_tie_rule_and_sum():
+    """ggml block_q8_1 (quantize_row_q8_1_ref, llama.cpp @7ac59a6, the convention followed here): q = roundf(x' * id),
+    id = 1/d, d = amax/127, s = fp16(d * sum q). Crafted x' sits exactly on k + 1/2 with d = 1: roundf rounds half
+    away from zero (+-(k+1)), where rint / nearbyint would give +-k; s is d * sum q, which differs from sum x'."""
+    buf, x, k = slotgen.tie_case(np.random.default_rng(12), K=512, k=2)
+    orc = O.Oracle(buf, 32, 512)
+    xr = orc.rotate(x)
+    assert np.array_equal(xr[0:256:2], np.full(128, 127.0, np.float32))
+    assert np.array_equal(xr[1:256:2], np.full(128, k + 0.5, np.float32))
+    assert np.array_equal(xr[257:512:2], np.full(128, -(k + 0.5), np.float32))
+    blk = orc.quantize_q8_1(x).reshape(-1, 36)
+    d = blk[:, 0:2].copy().view(np.float16).reshape(-1)
+    s = blk[:, 2:4].copy().view(np.float16).reshape(-1)
+    q = blk[:, 4:].view(np.int8).astype(np.int64)
+    assert np.all(d[:16] == 1.0) and np.all(d[16:] == 0.0)
+    assert np.array_equal(q[:8, 1::2], np.full((8, 16), k + 1)) and np.array_equal(q[8:16, 1::2], np.full((8, 16), -(k + 1)))
+    assert np.array_equal(q[:16, 0::2], np.full((16, 16), 127)) and not q[16:].any()
+    # s = d * sum q: block 0: 16 * 127 + 16 * (k + 1); sum x' would be 16 * 127 + 16 * (k + 1/2)
+    assert np.array_equal(s[:8].astype(np.float64), np.full(8, 16 * 127 + 16 * (k + 1.0)))
+    assert np.array_equal(s[8:16].astype(np.float64), np.full(8, 16 * 127 - 16 * (k + 1.0)))
+    assert np.all(s[16:] == 0.0)
+
+
+def test_q8_128_ties_round_half_even():
+    """the reference core's own 8-bit-per-128 prep rounds x' * (1/d) with nearbyintf (round half to even, CPU.patch:566-568):
+    on the same ties +-(k + 1/2) with k even it gives +-k, not the Q8_1 +-(k + 1)"""
+    buf, x, k = slotgen.tie_case(np.random.default_rng(12), K=512, k=2)
+    orc = O.Oracle(buf, 32, 512)
+    q, d, sx = orc.prep_q8_128(x)
+    assert np.array_equal(d, np.array([1, 1, 1, 1], np.float32))
+    assert np.all(q[1:256:2] == k) and np.all(q[257:512:2] == -k)
+    assert np.array_equal(sx, np.array([64 * 127 + 64 * k] * 2 + [64 * 127 - 64 * k] * 2, np.int32))
+    if O.ref_available("scalar"):   # and so does the live reference core (build container only)
+        t = O.RefCore("scalar").open(buf, 32, 512)
+        X2, XS, SX = t.prep_q8_128(x)
+        assert np.array_equal(q, X2[:, :128].reshape(-1)) and np.array_equal(sx, SX)
+        t.close()
+
+
+def test_gemv_f64_cols_equals_single_columns():
+    """the multi-column fp64 GEMV (each tile decoded once) equals the one-column one bit for bit"""
+    rng = np.random.default_rng(21)
+    buf = slotgen.random_slot(rng, 96, 1024, classes=(0, 1, 2, 3, 4, 5, 6, 7), nd=5)
+    orc = O.Oracle(buf, 96, 1024)
+    X = rng.standard_normal((3, 1024)).astype(np.float32)
+    Y = orc.gemv_f64_cols(X)
+    for n in range(3):
+        assert np.array_equal(Y[n], orc.gemv_f64(X[n])), n
+
+
 def test_open_rejects_corruption():
     rng = np.random.default_rng(3)
     buf = slotgen.random_slot(rng, 64, 512, classes=(3, 4), nd=2)
@@ -240,6 +290,24 @@ def test_live_reference_random_shapes():
         q, d, sx = orc.prep_q8_128(x)
         assert np.array_equal(q, X2[:, :128].reshape(-1)) and np.array_equal(d, XS) and np.array_equal(sx, SX)
         t.close()
+
+
+@pytest.mark.skipif(not O.ref_available("scalar"), reason="reference core not built here")
+def test_live_reference_wrapping_codebook():
+    """A codebook whose coset entries A + c leave the int8 range: the reference core adds bytewise and wraps
+    (vrc_vadd4, CPU.patch:221, :255); the oracle's decode and dequantize_row do the same (build container only)."""
+    core = O.RefCore("scalar")
+    rng = np.random.default_rng(13)
+    buf = slotgen.random_slot(rng, 64, 512, classes=(1, 2, 3, 4, 5, 6, 7), tables="wrapping", nd=3)
+    A, c = slotgen.wrapping_tables(np.random.default_rng(0))
+    s = A.view(np.int8).reshape(256, 4).astype(int) + np.array([100, -90, 77, -120])[None, :]
+    assert (s > 127).any() and (s < -128).any()   # the table does wrap
+    t = core.open(buf, 64, 512)
+    orc = O.Oracle(buf, 64, 512)
+    for g, b in ((0, 0), (1, 1)):
+        assert np.array_equal(orc.decode_tile(g, b), t.decode_tile(g, b))
+    assert np.array_equal(orc.dequant().view(np.uint32), t.dequant().view(np.uint32))
+    t.close()
 
 
 def test_zero_block_activation():
