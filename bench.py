@@ -10,7 +10,8 @@ the timed region. value = packed weight stream bytes (M + S + D) per step x step
 
 roofline: the fused GEMV kernel, algorithmic bytes = the packed stream of each launch, durations from HIP
 events bracketing every GEMV launch on the stream it runs on. cpu_baseline: the reference's own CPU core
-(oracle/_ref, built from its patch) running its two-phase GEMV driver on a bounded sample (one layer).
+(oracle/_ref, built from its patch) running its two-phase GEMV driver on bounded samples (the stack's first 10
+layers at 16 and 8 threads, x16 and q8 activations; one tensor or layer of the other configurations).
 """
 import argparse
 import json
@@ -45,7 +46,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_stack(layers, mix, keep_host_layer0):
+def build_stack(layers, mix, keep_host_layers):
+    """the stack's tensors (device), their kinds, and the host slots of the first keep_host_layers layers (the CPU
+    baseline's sample)"""
     tensors, kinds, host0 = [], [], []
     seed = 1
     plan = [(f"blk.{l}.{k}", r, K) for l in range(layers) for (k, r, K) in LLAMA_LAYER] + \
@@ -57,39 +60,80 @@ def build_stack(layers, mix, keep_host_layer0):
         seed += 1
         tensors.append(p8x.Tensor(slot, rows, K))
         kinds.append(kind)
-        if keep_host_layer0 and name.startswith("blk.0."):
+        if name.startswith("blk.") and int(name.split(".")[1]) < keep_host_layers:
             host0.append((slot, rows, K))
     return tensors, kinds, host0
 
 
-def cpu_baseline(host0, seconds, threads):
+def stream_bytes_of(slot, rows, K):
+    """packed weight stream (payload D + scales S + tile words M) of a host slot"""
+    nt = (rows // 32) * (K // 256)
+    kb = int(np.frombuffer(slot[-32:].tobytes(), np.uint32)[2])
+    return kb - ((2064 + 68 * nt + 15) & ~15) + 68 * nt
+
+
+def host_l3():
+    """the host's last-level cache as lscpu reports it (e.g. '256 MiB (8 instances)')"""
+    import subprocess
+    try:
+        for ln in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if ln.strip().startswith("L3"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
+
+
+def cpu_baseline(host_stack, seconds):
+    """The reference's own CPU core (oracle/_ref: vr-native-cpu-core.h compiled from its patch, driven by a pthread
+    restatement of its two-phase vrc_tg GEMV) on bounded samples: the Llama-3.1-8B stack's first layers (larger than
+    the host's last-level cache), at 16 threads (this box's CPU share) and 8 (the reference paper's setting), in the
+    reference's default x16 activation mode and in q8; then one tensor or layer of the other configurations.
+    Returns the headline object (stack sample, x16, 16 threads) with every run listed under "runs"."""
     import oracle as O
     variant = O.best_ref_variant()
     if not O.ref_available(variant):
         return None
     core = O.RefCore(variant)
-    pool = O.RefPool(core, threads)
-    refs = [core.open(s, r, K) for (s, r, K) in host0]
     rng = np.random.default_rng(7)
-    xs = [rng.standard_normal(K).astype(np.float32) for (_, _, K) in host0]
-    ys = [np.zeros(r, np.float32) for (_, r, _) in host0]
-    nbytes = 0
-    for (s, r, K) in host0:
-        nt = (r // 32) * (K // 256)
-        kb = int(np.frombuffer(s[-32:].tobytes(), np.uint32)[2])
-        nbytes += kb - ((2064 + 68 * nt + 15) & ~15) + 68 * nt   # payload + S + M
-    pool.gemv_seq(refs, xs, ys, planes=1)   # warm
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        pool.gemv_seq(refs, xs, ys, planes=1)
-        n += 1
-    dt = time.perf_counter() - t0
-    pool.close()
-    for r in refs:
-        r.close()
-    return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
-            "sample": f"layer 0 of the stack (7 linears, {nbytes / 1e6:.1f} MB packed), {n} passes in {dt:.1f} s, "
-                      f"q8 activations, reference core vr-native-cpu-core.h built {core.isa}"}
+
+    def run(name, slots, planes, nth, secs):
+        pool = O.RefPool(core, nth)
+        refs = [core.open(sl, r, K) for (sl, r, K) in slots]
+        xs = [rng.standard_normal(K).astype(np.float32) for (_, _, K) in slots]
+        ys = [np.zeros(r, np.float32) for (_, r, _) in slots]
+        nbytes = sum(stream_bytes_of(sl, r, K) for (sl, r, K) in slots)
+        pool.gemv_seq(refs, xs, ys, planes=planes)   # warm
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            pool.gemv_seq(refs, xs, ys, planes=planes)
+            n += 1
+        dt = time.perf_counter() - t0
+        pool.close()
+        for r in refs:
+            r.close()
+        res = {"sample": name, "mode": "x16" if planes == 2 else "q8", "threads": nth, "MB": round(nbytes / 1e6, 1),
+               "passes": n, "ms_per_pass": round(dt / n * 1e3, 3), "GB/s": round(nbytes * n / dt / 1e9, 3)}
+        log("cpu baseline:", json.dumps(res))
+        return res
+
+    ncpu = os.cpu_count() or 1
+    threads = [t for t in (16, 8) if t <= ncpu] or [ncpu]
+    nl = len(host_stack) // 7
+    stack_name = f"llama3.1-8b layers 0-{nl - 1} ({7 * nl} linears)"
+    runs = [run(stack_name, host_stack, planes, nth, seconds / 4) for nth in threads for planes in (2, 1)]
+    cfgs = [("4096 x 4096 (one tensor)", [(4096, 4096)]),
+            ("qwen3-4b one layer", [(r, K) for (_, r, K) in QWEN3_4B_LAYER]),
+            ("qwen3-14b one layer", [(r, K) for (_, r, K) in QWEN3_14B_LAYER])]
+    for name, shapes in cfgs:
+        slots = [(p8x.synth_random(7000 + i, r, K, nd=1), r, K) for i, (r, K) in enumerate(shapes)]
+        runs.append(run(name, slots, 2, threads[0], seconds / 8))
+    head = runs[0]
+    return {"value": head["GB/s"], "unit": "GB/s", "cores": head["threads"], "kind": "reference",
+            "sample": f"{stack_name}, {head['MB']} MB packed (host L3: {host_l3()}), {head['passes']} passes, "
+                      f"x16 activations (the reference's default CPU mode), {head['threads']} threads; "
+                      f"reference core vr-native-cpu-core.h built {core.isa}",
+            "runs": runs}
 
 
 def timed_steps(run, stream, warmup, steps):
@@ -249,6 +293,59 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps, 
     return per_linear
 
 
+def measure_dependent_step(tensors, kinds, stream, steps):
+    """A batch-1 decode step that respects the data dependencies of the model: per layer, q/k/v as one grouped
+    launch on the layer input, o on q's output, gate/up as one grouped launch on o's output, down on gate's output
+    (the next layer's input); then the head shards as one grouped launch on the last down's output. Each product's
+    activations are its producer's outputs, so nothing overlaps across launches; captured once in a HIP graph and
+    replayed. (Values shrink from layer to layer without the model's norms; the products' work does not depend on
+    them.)"""
+    nl = sum(1 for k in kinds if k == "attn_q")
+    layer = [tensors[7 * l:7 * l + 7] for l in range(nl)]
+    head = tensors[7 * nl:]
+    rng = np.random.default_rng(9)
+    x0 = p8x.DeviceBuffer.from_numpy(rng.standard_normal(layer[0][0].K).astype(np.float32))
+    bufs, batches, singles = [x0], [], []
+    cur = x0
+    for q, k, v, o, gate, up, down in layer:
+        yq, yk, yv = p8x.DeviceBuffer(4 * q.rows), p8x.DeviceBuffer(4 * k.rows), p8x.DeviceBuffer(4 * v.rows)
+        yo, yg, yu, yd = p8x.DeviceBuffer(4 * o.rows), p8x.DeviceBuffer(4 * gate.rows), p8x.DeviceBuffer(4 * up.rows), p8x.DeviceBuffer(4 * down.rows)
+        bufs += [yq, yk, yv, yo, yg, yu, yd]
+        qkv = p8x.GemvBatch([q, k, v], [cur, cur, cur], [yq, yk, yv])
+        gu = p8x.GemvBatch([gate, up], [yo, yo], [yg, yu])
+        batches += [qkv, gu]
+        singles.append((qkv, (o, yq, yo), gu, (down, yg, yd)))
+        cur = yd
+    yh = [p8x.DeviceBuffer(4 * t.rows) for t in head]
+    bufs += yh
+    hb = p8x.GemvBatch(head, [cur] * len(head), yh)
+    batches.append(hb)
+
+    def enqueue(s):
+        for qkv, (o, xo, yo), gu, (down, xd, yd) in singles:
+            qkv.run(s)
+            o.mul_mat_vec_dev(xo, yo, stream=s)
+            gu.run(s)
+            down.mul_mat_vec_dev(xd, yd, stream=s)
+        hb.run(s)
+
+    eager_ms = timed_steps(lambda: enqueue(stream), stream, 3, steps)
+    graph = p8x.Graph(enqueue, stream)
+    g_ms = timed_steps(lambda: graph.launch(stream), stream, 3, steps)
+    graph.release()
+    step_bytes = sum(t.stream_bytes for t in tensors)
+    launches = nl * (3 + 1 + 3 + 1) + 3
+    log(f"dependent step: eager {eager_ms * 1e3:.0f} us, graph {g_ms * 1e3:.0f} us ({launches} launches)")
+    for b in batches:
+        b.release()
+    for b in bufs:
+        b.free()
+    return {"workload": f"{nl} layers: grouped q/k/v -> o -> grouped gate/up -> down, then the head shards grouped; "
+                        "each launch reads its producer's output", "launches": launches,
+            "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)},
+            "eager": {"ms_per_step": round(eager_ms, 4), "GB/s": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)}}
+
+
 def measure_gemm(steps, N=512):
     """prompt GEMM on the Llama-3.1-8B FFN shapes: N bf16 tokens ~ N(0, 1), whole p8x_mul_mat calls timed"""
     out = {}
@@ -322,18 +419,20 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # the first few dozen back-to-back launches run slower while the GPU settles (power management); the
-    # default warmup runs past that so the timed steps see the steady state
-    ap.add_argument("--warmup", type=int, default=150)
+    # The first few dozen back-to-back launches after the GPU has been idle run up to a third slower (clocks and
+    # power ramping). The per-linear, dependent-step, prompt-GEMM and dequantize measurements run before the headline
+    # stream, so it is timed on a busy GPU even with a short warmup.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--mix", choices=("c3", "b4"), default="c3")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
+    ap.add_argument("--cpu-layers", type=int, default=10, help="Llama layers in the CPU baseline's sample (10: 563 MB)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-per-linear", action="store_true", help="skip the per-linear launch measurement")
-    ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM measurement")
+    ap.add_argument("--no-dependent", action="store_true", help="skip the dependency-respecting decode step")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM and dequantize measurements")
     ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
-    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay of the per-linear step "
-                    "(rocprofv3 --kernel-trace ended in a host segmentation fault during graph replays)")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replays (per-linear and dependent steps)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -347,7 +446,7 @@ def main():
         sys.exit(1)
 
     t_build = time.perf_counter()
-    tensors, kinds, host0 = build_stack(args.layers, args.mix, not args.no_cpu)
+    tensors, kinds, host0 = build_stack(args.layers, args.mix, 0 if args.no_cpu else args.cpu_layers)
     log(f"built {len(tensors)} tensors in {time.perf_counter() - t_build:.1f} s")
     step_bytes = sum(t.stream_bytes for t in tensors)
     rng = np.random.default_rng(0)
@@ -355,7 +454,16 @@ def main():
     ybufs = [p8x.DeviceBuffer(4 * t.rows) for t in tensors]
     stream = p8x.Stream()
 
-    # ---- streaming: one grouped launch (activation prep + fused decode-GEMV) over every linear per step
+    # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), the dependency-respecting
+    # step, the prompt GEMM and dequantize; reported beside the headline and timed before it
+    per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3),
+                                    not args.no_graph) if not args.no_per_linear else None
+    dependent = measure_dependent_step(tensors, kinds, stream, max(5, args.steps // 4)) \
+        if not (args.no_dependent or args.no_graph) else None
+    gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
+    deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
+
+    # ---- headline: one grouped launch (activation prep + fused decode-GEMV + finishing) over every linear per step
     batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ybufs)
     for _ in range(args.warmup):
         batch.run(stream)
@@ -396,11 +504,6 @@ def main():
         src.free(); dst.free()
         log(f"copy calibration: {n} bytes device to device")
 
-    # ---- per-linear launches (the drop-in path: one p8x_mul_mat_vec per graph node), reported beside
-    per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3),
-                                    not args.no_graph) if not args.no_per_linear else None
-    gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
-    deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
     qwen14b = qwen4b = quant4096 = None
     if not args.no_qwen:
         batch.release()
@@ -409,10 +512,7 @@ def main():
         qwen14b = measure_qwen14b_columns(stream, max(10, args.steps // 4))
         qwen4b = measure_qwen4b_layer(stream, max(10, args.steps // 4))
         quant4096 = measure_quantized_4096(stream, max(10, args.steps // 10))
-    cpu = None
-    if not args.no_cpu and host0:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        cpu = cpu_baseline(host0, args.cpu_seconds, threads)
+    cpu = cpu_baseline(host0, args.cpu_seconds) if not args.no_cpu and host0 else None
     traffic, traffic_src = measured_traffic(int(step_bytes), args.layers, args.mix)
     out = {
         "metric": "bs=1 dequant-GEMV HBM GB/s (% of peak), Llama-3.1-8B linear shapes",
@@ -430,6 +530,7 @@ def main():
                      "bytes_per_launch": int(step_bytes)},
         "cpu_baseline": cpu,
         "per_linear_launches": per_linear,
+        "dependent_step": dependent,
         "prompt_gemm": gemm,
         "dequantize_f16": deq,
         "qwen3_14b_columns": qwen14b,
