@@ -122,6 +122,14 @@ int p8x_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t l
 /* No counterpart in the reference (ggml's pool allocator serves its temporaries): allocate the p8x_mul_mat
  * workspace for up to n_max tokens at set-up, so later calls with N <= n_max allocate nothing. */
 int p8x_mul_mat_reserve(const p8x_tensor *t, int n_max);
+/* No counterpart in the reference; for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): p8x_mul_mat with its workspace (fp16 x' and K-split output planes) in a
+ * fixed device array of P8X_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. Allocates nothing and never
+ * synchronizes; rejects (P8X_ERR_UNSUPPORTED) a call whose workspace exceeds the array (512 tokens of the Llama-3.1-8B
+ * FFN shapes fit). Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race; calls ordered on one stream do not. Results equal p8x_mul_mat's. */
+#define P8X_NOALLOC_SCRATCH_BYTES (64 << 20)
+int p8x_mul_mat_noalloc(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream);
 
 /* ---- grouped GEMV ------------------------------------------------------------------------------------- */
 /* No counterpart in the reference (ggml issues one mul_mat per graph node). A fixed list of independent

@@ -17,6 +17,8 @@
 // Q8_0 slab (k_r51_k1, CPU.patch:2138-2235) and calls the stock integer MMQ.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include <algorithm>
 
 #include "p8x_internal.h"
@@ -443,21 +445,27 @@ int reserve_mul_mat(const p8x_tensor *t, int n_max) {
     return P8X_OK;
 }
 
-int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st) {
-    if (((uintptr_t)x & 15) || (ldx % 8)) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x must be 16-byte aligned with ldx %% 8 == 0");
-    p8x_tensor *tw = const_cast<p8x_tensor *>(t);
+// workspace bytes of one prompt GEMM call: rotated fp16 activations [N][K], and (K split or rows to un-permute) the
+// sorted-row output planes [nsplit][N][rows] f32
+static void mm_workspace(const p8x_tensor *t, int N, size_t *x_bytes, size_t *plane_bytes) {
+    const MmPlan p = mm_plan(t, N);
+    *x_bytes = (size_t)N * t->K * sizeof(_Float16);
+    *plane_bytes = p.nsplit == 1 && t->prm_identity ? 0 : (size_t)p.nsplit * N * t->rows * 4;
+}
+
+// the launches of one prompt GEMM with its workspace given: xr >= N K fp16, wmm >= the plane bytes (unused when the
+// output is written directly)
+static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, _Float16 *xr,
+                             float *wmm, hipStream_t st) {
     const MmPlan p = mm_plan(t, N);
     const bool direct = p.nsplit == 1 && t->prm_identity;
     int rc;
-    if ((rc = grow((void **)&tw->wx16, &tw->wx16_elems, (size_t)N * t->K * sizeof(_Float16), "p8x_mul_mat: activation workspace"))) return rc;
-    if (!direct && (rc = grow((void **)&tw->wmm, &tw->wmm_bytes, (size_t)p.nsplit * N * t->rows * 4, "p8x_mul_mat: output planes"))) return rc;
-    _Float16 *xr = reinterpret_cast<_Float16 *>(tw->wx16);
     if (x_dtype == P8X_F32) hipLaunchKernelGGL(k_mm_act<float>, dim3(t->nb, N), dim3(64), 0, st, (const float *)x, ldx, t->ic, t->K, xr);
     else hipLaunchKernelGGL(k_mm_act<uint16_t>, dim3(t->nb, N), dim3(64), 0, st, (const uint16_t *)x, ldx, t->ic, t->K, xr);
     if ((rc = hip_check(hipGetLastError(), "k_mm_act launch"))) return rc;
     MmJob J;
     J.M = t->M; J.S = t->S; J.D = t->D; J.xr = xr;
-    J.y = y; J.ldy = (unsigned)ldy; J.ws = tw->wmm; J.a2 = t->a2;
+    J.y = y; J.ldy = (unsigned)ldy; J.ws = wmm; J.a2 = t->a2;
     J.N = N; J.rows = t->rows; J.K = t->K; J.nb = t->nb; J.ng = t->ng;
     J.tiles_m = p.tiles_m; J.tiles_n = p.tiles_n; J.nsplit = p.nsplit; J.kper = p.kper; J.direct = direct;
     const int grid = ((p.tiles_m * p.tiles_n * p.nsplit + kXcds - 1) / kXcds) * kXcds;
@@ -476,10 +484,10 @@ int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_
             attr_set = true;
         }
         if (x_dtype == P8X_F32)
-            hipLaunchKernelGGL(k_mm_finish<float>, dim3(N), dim3(1024), lds, st, (const float *)tw->wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
+            hipLaunchKernelGGL(k_mm_finish<float>, dim3(N), dim3(1024), lds, st, (const float *)wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
                                (const float *)x, ldx, y, ldy);
         else
-            hipLaunchKernelGGL(k_mm_finish<uint16_t>, dim3(N), dim3(1024), lds, st, (const float *)tw->wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
+            hipLaunchKernelGGL(k_mm_finish<uint16_t>, dim3(N), dim3(1024), lds, st, (const float *)wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
                                (const uint16_t *)x, ldx, y, ldy);
         return hip_check(hipGetLastError(), "k_mm_finish launch");
     }
@@ -493,4 +501,68 @@ int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_
     return P8X_OK;
 }
 
+int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st) {
+    if (((uintptr_t)x & 15) || (ldx % 8)) return set_error(P8X_ERR_ARG, "p8x_mul_mat: x must be 16-byte aligned with ldx %% 8 == 0");
+    p8x_tensor *tw = const_cast<p8x_tensor *>(t);
+    size_t xb, pb;
+    mm_workspace(t, N, &xb, &pb);
+    int rc;
+    if ((rc = grow((void **)&tw->wx16, &tw->wx16_elems, xb, "p8x_mul_mat: activation workspace"))) return rc;
+    if (pb && (rc = grow((void **)&tw->wmm, &tw->wmm_bytes, pb, "p8x_mul_mat: output planes"))) return rc;
+    return launch_mul_mat_ws(t, x, x_dtype, N, ldx, y, ldy, reinterpret_cast<_Float16 *>(tw->wx16), tw->wmm, st);
+}
+
+// ------------------------------------------------------------------------------------------------ no-allocation variant
+// Workspace of p8x_mul_mat_noalloc: one file-scope device array per GPU, held until the process ends. In host code
+// `scratch` names a host-side stand-in; the device address of each GPU's copy comes from hipGetSymbolAddress with
+// that GPU current, resolved once per device (scratch_resolve) and used everywhere host code passes the array on.
+static __device__ __align__(256) uint8_t scratch[P8X_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch[kMaxDevices];
+
+int scratch_resolve(int device) {
+    if (device < 0 || device >= kMaxDevices) return set_error(P8X_ERR_UNSUPPORTED, "scratch: device %d beyond %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[device]) return P8X_OK;
+    int cur = 0, rc;
+    if ((rc = hip_check(hipGetDevice(&cur), "scratch: hipGetDevice"))) return rc;
+    if (cur != device && (rc = hip_check(hipSetDevice(device), "scratch: hipSetDevice"))) return rc;
+    void *ptr = nullptr;
+    rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "scratch: hipGetSymbolAddress");
+    if (cur != device) (void)hipSetDevice(cur);
+    if (rc) return rc;
+    g_scratch[device] = ptr;
+    return P8X_OK;
+}
+
+static void *scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return device >= 0 && device < kMaxDevices ? g_scratch[device] : nullptr;
+}
+
 }  // namespace p8x
+
+extern "C" int p8x_mul_mat_noalloc(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream) {
+    using namespace p8x;
+    if (!t || !x || !y) return set_error(P8X_ERR_ARG, "p8x_mul_mat_noalloc: null pointer");
+    if (x_dtype != P8X_F32 && x_dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_mul_mat_noalloc: x dtype %d", x_dtype);
+    if (N < 1 || ldx < (size_t)t->K || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_noalloc: N %d ldx %zu ldy %zu", N, ldx, ldy);
+    if (((uintptr_t)x & 15) || (ldx % 8)) return set_error(P8X_ERR_ARG, "p8x_mul_mat_noalloc: x must be 16-byte aligned with ldx %% 8 == 0");
+    size_t xb, pb;
+    mm_workspace(t, N, &xb, &pb);
+    const size_t xb_al = (xb + 255) & ~(size_t)255;
+    if (xb_al + pb > (size_t)P8X_NOALLOC_SCRATCH_BYTES)
+        return set_error(P8X_ERR_UNSUPPORTED, "p8x_mul_mat_noalloc: %d tokens of a %d x %d tensor need %zu workspace bytes, above the %d-byte scratch",
+                         N, t->rows, t->K, xb_al + pb, P8X_NOALLOC_SCRATCH_BYTES);
+    uint8_t *base = static_cast<uint8_t *>(scratch_ptr(t->device));
+    if (!base) {   // the tensor was prepared on a device whose scratch is not resolved yet (first call there)
+        int rc = scratch_resolve(t->device);
+        if (rc) return rc;
+        base = static_cast<uint8_t *>(scratch_ptr(t->device));
+    }
+    // x' first, the output planes after it on a 256-byte boundary; every byte read is written earlier in the call
+    return launch_mul_mat_ws(t, x, x_dtype, N, ldx, y, ldy, reinterpret_cast<_Float16 *>(base), reinterpret_cast<float *>(base + xb_al),
+                             (hipStream_t)stream);
+}

@@ -197,6 +197,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
     memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
+    if ((rc = scratch_resolve(t->device))) { delete t; return rc; }   // set-up of the no-allocation entry point
     auto fail = [&](int code) { p8x_release(t); return code; };
     auto alloc = [&](void **p, size_t bytes, const char *what) -> int {
         if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return set_error(P8X_ERR_NOMEM, "p8x_prepare: hipMalloc %s (%zu B)", what, bytes);

@@ -71,6 +71,8 @@ int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, 
 int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
 int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st);
 int reserve_mul_mat(const p8x_tensor *t, int n_max);
+// device address of the no-allocation scratch array on `device` (hipGetSymbolAddress, once per device)
+int scratch_resolve(int device);
 
 int num_cus();
 

@@ -22,7 +22,7 @@ EXPORTS = [
     "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
     "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_mul_mat_reserve", "p8x_synth_random",
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
-    "p8x_gemv_batch_release", "p8x_gemv_batch_info",
+    "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
 ]
 
 
@@ -70,6 +70,7 @@ def lib():
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
     L.p8x_mul_mat_reserve.argtypes = [vp, i]
+    L.p8x_mul_mat_noalloc.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
     L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
     L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
     L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
@@ -343,6 +344,10 @@ class Tensor:
     def mul_mat_dev(self, x, x_dtype, N, y, ldx=None, ldy=None, stream=None):
         check(lib().p8x_mul_mat(self.h, _vp(x), x_dtype, N, ldx or self.K, _vp(y), ldy or self.rows,
                                 stream.h if stream else None), "p8x_mul_mat")
+
+    def mul_mat_noalloc_dev(self, x, x_dtype, N, y, ldx=None, ldy=None, stream=None):
+        check(lib().p8x_mul_mat_noalloc(self.h, _vp(x), x_dtype, N, ldx or self.K, _vp(y), ldy or self.rows,
+                                        stream.h if stream else None), "p8x_mul_mat_noalloc")
 
     # ---- numpy conveniences (copy in / out, synchronous)
     def dequantize(self, dtype=F32):
