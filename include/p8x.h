@@ -57,7 +57,8 @@ typedef struct p8x_info {
     size_t kbytes;          /* kernel bytes (header + M + S + D) */
     size_t stream_bytes;    /* packed weight stream read by a GEMV: M words + S + D payload */
     size_t class_tiles[8];  /* tiles per class 0..7 */
-    const void *dev_base;   /* device address of the slot bytes */
+    const void *dev_base;   /* device address of the slot bytes (on_device = 0: the library's copy, whose payload
+                               region is re-laid for 16-byte loads; on_device = 1: the caller's bytes, unchanged) */
 } p8x_info;
 
 const char *p8x_version(void);
@@ -72,7 +73,8 @@ int p8x_probe(const void *slot, size_t n, int rows, int K);
 
 /* Validate a slot and build its device-side metadata: vrc_init + vr_prepare_native (CPU.patch:240-275,
  * :4335-4390). on_device = 0: `slot` is host memory and is copied to a device allocation the handle owns;
- * on_device = 1: `slot` is device memory that must outlive the handle. Allocates everything the GEMV,
+ * on_device = 1: `slot` is device memory that must outlive the handle; it is only read, and the handle keeps a
+ * copy of the payload re-laid for 16-byte loads (the device then holds the payload twice). Allocates everything the GEMV,
  * decode and activation entry points use; only p8x_mul_mat (see p8x_mul_mat_reserve) and
  * p8x_gemv_batch_create allocate later. */
 int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_tensor **out);

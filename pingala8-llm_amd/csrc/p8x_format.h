@@ -32,6 +32,17 @@ P8X_HD constexpr int nw_of(int c) { return w1_of(c) + w2_of(c) + w3_of(c); }
 P8X_HD constexpr int nstage_of(int c) { return c == 0 ? 0 : c <= 3 ? 1 : c <= 6 ? 2 : 3; }
 
 P8X_HD constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// Payload word i of lane j inside a half-slice of a class with NW words per lane.
+// In the file (and the reference's memory), word pairs of the 32 lanes interleave: [i >> 1][j][i & 1]
+// (CPU.patch:292-297). p8x_prepare re-lays each tile's payload on the device so that a lane's words come in 16-byte
+// groups: the first NW & ~3 words as [i >> 2][j][i & 3] (512 contiguous bytes per group of the 32 lanes), the last two
+// of NW = 6 and 10 as in the file after them ([j][i & 1]). Every kernel reads this device layout; one buffer load of
+// 16 bytes per lane then fetches a lane's four consecutive words.
+P8X_HD constexpr int file_word(int i, int j) { return ((i >> 1) << 6) + 2 * j + (i & 1); }
+P8X_HD constexpr int dev_word(int i, int j, int nw) {
+    return i < (nw & ~3) ? ((i >> 2) << 7) + 4 * j + (i & 3) : ((nw & ~3) << 5) + 2 * j + (i & 1);
+}
 P8X_HD constexpr size_t offset_S(size_t nt) { return kHeaderBytes + 4 * nt; }
 P8X_HD constexpr size_t offset_D(size_t nt) { return align16(kHeaderBytes + 68 * nt); }
 

@@ -235,6 +235,7 @@ struct GemvRun {
     uint32_t wn;   // tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
     // lane part of the payload offsets: one base (step order) or the NW rotated word offsets
     std::conditional_t<STEP, uint32_t, uint32_t[NW]> vo;
+    uint32_t vp;   // step order: the lane's trailing-pair offset (classes with NW % 4 == 2)
     uint32_t vs;
 
     __device__ __forceinline__ kptr<const uint32_t> mrow(const TaskCtx<NCOL, ACT> &c) const {
@@ -248,7 +249,8 @@ struct GemvRun {
         const uint32_t soff = ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
         const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
         __builtin_amdgcn_s_setprio(2);   // loads issued at raised priority (see wave_run)
-        r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        if constexpr (STEP) r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        else r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         __builtin_amdgcn_s_setprio(0);
         wn = mrow(c)[min(ta + 1, e - 1)];
     }
@@ -259,8 +261,12 @@ struct GemvRun {
             e = b + 1;
             while (e < bend && (mrow(c)[e] >> 29) == (uint32_t)C) ++e;
         }
-        if constexpr (STEP) vo = (uint32_t)(c.hs * NW * 128 + 8 * c.j);
-        else RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
+        if constexpr (STEP) {
+            vo = StepSlice<C>::quad_offset(c.hs, c.j);
+            vp = StepSlice<C>::pair_offset(c.hs, c.j);
+        } else {
+            RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
+        }
         vs = 2u * (uint32_t)c.j;
         wn = mrow(c)[b];
 #pragma unroll
@@ -746,7 +752,8 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
     constexpr int NW = nw_of(C);
     // activations [NCOL][K] int8 and scales [NCOL][K / 128]
     const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.K), dbytes = (uint32_t)(NCOL * J.nsl) * 4u;
-    const uint32_t vo = (uint32_t)(hs * NW * 128 + 8 * j), vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)lane, vd = 4u * (uint32_t)hs;
+    const uint32_t vo = StepSlice<C>::quad_offset(hs, j), vp = StepSlice<C>::pair_offset(hs, j);
+    const uint32_t vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)lane, vd = 4u * (uint32_t)hs;
     uint32_t wn = mrow[b];
     auto issue = [&](WaveSlice<C, NCOL> &r, int ta) {
         const bool ok = ta < e;
@@ -757,7 +764,7 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
         // The wave issues its loads at raised priority, so the arbiter lets it put the next tile in flight
         // ahead of other waves' decode work (about 1% on the class-3 stream).
         __builtin_amdgcn_s_setprio(2);
-        r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u), rd = buffer_rsrc(J.d, ok ? dbytes : 0u);
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) {

@@ -52,6 +52,16 @@ __global__ void k_regroup_scales(const uint16_t *__restrict__ S, uint16_t *__res
     Sg[i] = S[(size_t)b * rows + 32 * g + j];
 }
 
+// tile payloads from the file layout (file_word) to the device layout (dev_word); one 64-thread block per tile,
+// thread (hs, j) moves the NW words of lane j of half-slice hs; every tile lies inside the payload (checked at prepare)
+__global__ void k_relayout_payload(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, const uint32_t *__restrict__ M) {
+    const uint32_t m = M[blockIdx.x];
+    const int nw = nw_of((int)(m >> 29));
+    const int hs = threadIdx.x >> 5, j = threadIdx.x & 31;
+    const size_t base = (size_t)(m & 0x1FFFFFFFu) + (size_t)hs * nw * 32;
+    for (int i = 0; i < nw; ++i) dst[base + dev_word(i, j, nw)] = src[base + file_word(i, j)];
+}
+
 }  // namespace p8x
 
 using namespace p8x;
@@ -96,7 +106,7 @@ static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -216,6 +226,30 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->S = (const uint16_t *)(t->base + offset_S(nt));
     t->D = (const uint32_t *)(t->base + offset_D(nt));
     t->prm = (const int16_t *)(t->base + off[2]);
+    if (words) {
+        // payload to the device layout (16-byte groups per lane): in place in the library's copy (through a temporary
+        // copy of the file payload), or into a payload copy of its own when the caller owns the slot
+        uint32_t *dst = nullptr, *tmp = nullptr;
+        const uint32_t *srcD = t->D;
+        if (on_device) {
+            if ((rc = alloc((void **)&t->Dl, 4 * words, "payload"))) return fail(rc);
+            dst = t->Dl;
+        } else {
+            if ((rc = alloc((void **)&tmp, 4 * words, "payload staging"))) return fail(rc);
+            if ((rc = hip_check(hipMemcpy(tmp, t->D, 4 * words, hipMemcpyDeviceToDevice), "p8x_prepare: payload staging"))) {
+                (void)hipFree(tmp);
+                return fail(rc);
+            }
+            srcD = tmp;
+            dst = const_cast<uint32_t *>(t->D);
+        }
+        hipLaunchKernelGGL(k_relayout_payload, dim3((unsigned)nt), dim3(64), 0, 0, srcD, dst, t->M);
+        rc = hip_check(hipGetLastError(), "p8x_prepare: payload layout");
+        if (!rc) rc = hip_check(hipDeviceSynchronize(), "p8x_prepare: payload layout");
+        if (tmp) (void)hipFree(tmp);
+        if (rc) return fail(rc);
+        t->D = dst;
+    }
     for (int nc = 1; nc <= P8X_MAX_COLS; ++nc) {   // partial rows of the largest single-GEMV plan
         for (int act : {P8X_ACT_Q8_128, P8X_ACT_Q8_1}) {
             const GemvPlan plan = gemv_plan(t, nc, act, false);

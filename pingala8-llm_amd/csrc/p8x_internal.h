@@ -20,7 +20,8 @@ struct p8x_tensor {
     // views into the slot (device)
     const uint32_t *M = nullptr;
     const uint16_t *S = nullptr;
-    const uint32_t *D = nullptr;
+    const uint32_t *D = nullptr;     // payload in the device layout (dev_word): in the slot copy, or Dl
+    uint32_t *Dl = nullptr;          // the library's re-laid payload copy when the caller owns the device slot
     const int16_t *prm = nullptr;
     uint16_t *Sg = nullptr;          // row scales regrouped [ng][nb][32]: a row group's scales in one run
     int16_t *pinv = nullptr;         // original row -> sorted row (built at prepare)

@@ -2,10 +2,11 @@
 //
 // One wave64 owns one tile (g, b): lane L decodes half-slice hs = L >> 5 of sorted row 32g + (L & 31).
 // A lane-slice is NW(c) payload words holding 32 fields per stage; step k of lane j encodes chunk
-// t = (j + k) & 31 (CPU.patch:155-158). Here every lane loads its words already rotated by j fields
-// (per-lane load addresses plus one v_alignbit per word), so field t of the rotated registers IS chunk t
-// for every lane: all later indexing is compile-time and the activation chunk is the same for all 32
-// lanes of a half-wave (an LDS broadcast).
+// t = (j + k) & 31 (CPU.patch:155-158). Payload words are read in the device layout of p8x_format.h (dev_word:
+// a lane's words in 16-byte groups). The chunk-order loaders (RawSlice, AnyRaw) load every lane's words already
+// rotated by j fields (per-lane load addresses plus one v_alignbit per word), so field t of the rotated registers
+// IS chunk t for every lane: all later indexing is compile-time and the activation chunk is the same for all 32
+// lanes of a half-wave (an LDS broadcast). The step-order loader (StepSlice) loads words as stored.
 //
 // Coset table in LDS: entry (f, h) = A[f] + h * c (bytewise, CPU.patch:221/:255), replicated across the
 // 32 LDS banks: byte address (f << 8) | (h << 7) | (bank << 2) with bank = lane & 31, so the 32 lanes of a
@@ -91,25 +92,6 @@ __device__ __forceinline__ uint32_t trellis_coset_bits(uint32_t z) {
     return u << 2;
 }
 
-// address of word i of lane j inside a half-slice: [i >> 1][j][i & 1] (CPU.patch:292-297)
-__device__ __forceinline__ int lane_word_offset(int i, int j) { return ((i >> 1) << 6) + 2 * j + (i & 1); }
-
-// Load a region of W words (32 fields of W bits) starting at lane word WB, rotated so field t = chunk t.
-// R = original rotated right by r = W * (32 - j) bits (mod 32 W).
-template <int W, int WB>
-__device__ __forceinline__ void load_region(const uint32_t *__restrict__ p, int j, uint32_t (&R)[W]) {
-    const int r = ((32 - j) & 31) * W;
-    const int wr = r >> 5, br = r & 31;
-    uint32_t L[W];
-#pragma unroll
-    for (int m = 0; m < W; ++m) {
-        const int i = WB + (m + wr) % W;
-        L[m] = __builtin_nontemporal_load(p + lane_word_offset(i, j));
-    }
-#pragma unroll
-    for (int i = 0; i < W; ++i) R[i] = __builtin_amdgcn_alignbit(L[(i + 1) % W], L[i], br);
-}
-
 template <int W, int N>
 __device__ __forceinline__ uint32_t field_of(const uint32_t (&R)[N], int t) {
     const int pos = W * t, wi = pos >> 5, bb = pos & 31;
@@ -148,7 +130,7 @@ struct RawSlice {
     static __device__ __forceinline__ void region_offsets(uint32_t hsoff, int j, uint32_t (&vo)[NW]) {
         const int wr = ((((32 - j) & 31) * W) >> 5);
 #pragma unroll
-        for (int m = 0; m < W; ++m) vo[O + m] = 4u * (hsoff + (uint32_t)lane_word_offset(WB + (m + wr) % W, j));
+        for (int m = 0; m < W; ++m) vo[O + m] = 4u * (hsoff + (uint32_t)dev_word(WB + (m + wr) % W, j, NW));
     }
 
     // Byte offsets, within a tile's payload, of the lane's NW words in load order. They depend only on the
@@ -157,7 +139,7 @@ struct RawSlice {
         if constexpr (W1 == 8) {
             region_offsets<8, 0, 0>(hsoff, j, vo);
         } else {
-            vo[0] = 4u * (hsoff + (uint32_t)lane_word_offset(0, j));
+            vo[0] = 4u * (hsoff + (uint32_t)dev_word(0, j, NW));
             region_offsets<W1 - 1, 1, 1>(hsoff, j, vo);
         }
         if constexpr (W2 > 0) region_offsets<W2, W1, W1>(hsoff, j, vo);
@@ -194,19 +176,6 @@ struct LaneSlice {
     uint32_t r3[NR3];
     uint32_t H;            // coset bits, chunk order
     uint32_t bankbytes;
-
-    // p = half-slice base (tile payload + hs * NW * 32), j = lane row
-    __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j) {
-        if constexpr (W1 == 8) {
-            load_region<8, 0>(p, j, r1);
-        } else {
-            const uint32_t w0 = __builtin_nontemporal_load(p + lane_word_offset(0, j));
-            r0 = __builtin_amdgcn_alignbit(w0, w0, (32 - j) & 31);
-            load_region<W1 - 1, 1>(p, j, r1);
-        }
-        if constexpr (W2 > 0) load_region<W2, W1>(p, j, r2);
-        if constexpr (W3 > 0) load_region<W3, W1 + W2>(p, j, r3);
-    }
 
     // same state from words already in registers
     __device__ __forceinline__ void from_raw(const RawSlice<C> &raw, int j) {
@@ -265,19 +234,31 @@ __device__ __forceinline__ uint32_t field_at(const uint32_t (&w)[NW], int k) {
 
 template <int C>
 struct StepSlice {
-    static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C), NP = NW / 2;
+    static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
+    static constexpr int NQ = NW / 4, NP = (NW % 4) / 2;   // 16-byte groups and a trailing word pair per lane
     static constexpr int O1 = W1 == 8 ? 0 : 1, O2 = W1, O3 = W1 + W2;   // first word of each stage's fields
     uint32_t w[NW];
     uint32_t s;   // fp16 row scale, zero-extended by its load
 
-    // vo = hs * NW * 128 + 8 j: the lane's byte offset of word pair 0; pair p sits 256 p bytes further
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rd, uint32_t toff, uint32_t vo,
+    // lane byte offsets in the device layout (dev_word): of its first 16-byte group, and of its trailing pair
+    static __device__ __forceinline__ uint32_t quad_offset(int hs, int j) { return (uint32_t)(hs * NW * 128 + 16 * j); }
+    static __device__ __forceinline__ uint32_t pair_offset(int hs, int j) { return (uint32_t)(hs * NW * 128 + 512 * NQ + 8 * j); }
+
+    // vo = quad_offset: group q sits 512 q bytes further; vp = pair_offset (classes with NW % 4 == 2)
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rd, uint32_t toff, uint32_t vo, uint32_t vp,
                                          __amdgpu_buffer_rsrc_t rs, uint32_t soff, uint32_t vs) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, vo + 256u * p, toff, kBufNT);
-            w[2 * p] = v[0];
-            w[2 * p + 1] = v[1];
+        for (int q = 0; q < NQ; ++q) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rd, vo + 512u * q, toff, kBufNT);
+            w[4 * q] = v[0];
+            w[4 * q + 1] = v[1];
+            w[4 * q + 2] = v[2];
+            w[4 * q + 3] = v[3];
+        }
+        if constexpr (NP) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, vp, toff, kBufNT);
+            w[4 * NQ] = v[0];
+            w[4 * NQ + 1] = v[1];
         }
         s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, soff, kBufNT);
     }
@@ -325,22 +306,23 @@ struct AnyRaw {
     uint32_t w[NWMAX];
     uint32_t s;   // fp16 row scale, zero-extended by its load
 
-    template <int W, int WB>
+    template <int W, int WB, int NW>
     __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
         const int wr = (((32 - j) & 31) * W) >> 5;
 #pragma unroll
-        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + lane_word_offset(WB + (m + wr) % W, j));
+        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + dev_word(WB + (m + wr) % W, j, NW));
     }
+    // p = the tile's half-slice base (tile payload + hs * NW * 32 words)
     template <int C>
     __device__ __forceinline__ void load(const uint32_t *__restrict__ p, int j, const uint16_t *__restrict__ srow) {
-        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
-        if constexpr (W1 == 8) region<8, 0>(p, j);
+        constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
+        if constexpr (W1 == 8) region<8, 0, NW>(p, j);
         else {
-            w[0] = __builtin_nontemporal_load(p + lane_word_offset(0, j));
-            region<W1 - 1, 1>(p, j);
+            w[0] = __builtin_nontemporal_load(p + dev_word(0, j, NW));
+            region<W1 - 1, 1, NW>(p, j);
         }
-        if constexpr (W2 > 0) region<W2, W1>(p, j);
-        if constexpr (W3 > 0) region<W3, W1 + W2>(p, j);
+        if constexpr (W2 > 0) region<W2, W1, NW>(p, j);
+        if constexpr (W3 > 0) region<W3, W1 + W2, NW>(p, j);
         s = srow[j];
     }
 };
