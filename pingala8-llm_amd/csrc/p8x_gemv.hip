@@ -187,14 +187,15 @@ __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restri
     if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
 }
 
-// Finishing launch of a grouped GEMV. The first blocks take 1024 sorted rows of one job each (4 per thread, loads
-// issued together): per column, sorted row r sums its K-chunk partials in chunk order (coalesced reads) and is
-// written to its original row prmd[r] (a scatter inside the job's output). Rows that carry clamp-delta entries
-// (bit 15 of prmd) are left to the last blocks, one thread per such row, which add the delta entries after the
-// partials (the order and arithmetic of the single-launch fix-up).
-// Every block of a job runs on one XCD (workgroups go to XCDs round robin by index: block 8k + x runs on XCD x),
-// so the job's output lines fill in one L2. Block table entries: job | 1024-row block of the job << 24, or
-// kFinNone for padding.
+// Finishing launch of a grouped GEMV. Rows that carry clamp-delta entries (bit 15 of prmd) go to the first blocks,
+// one thread per such row: it sums the row's K-chunk partials in chunk order and adds its delta entries (resolved at
+// batch creation, so its loads do not wait on one another beyond the activation gather); these blocks come first so
+// that their chain of dependent loads overlaps the plain blocks instead of ending the launch. The plain blocks take
+// 1024 sorted rows of one job each (4 per thread): per column, sorted row r sums its K-chunk partials in chunk order
+// (coalesced reads, four chunks' loads issued together) and is written to its original row prmd[r] (a scatter
+// inside the job's output). Plain block 8k + x runs on XCD x (workgroups go to the XCDs round robin by index, and
+// the delta blocks are padded to a multiple of 8), and every plain block of a job is on one XCD, so the job's
+// output lines fill in one L2. Block table entries: job | 1024-row block of the job << 24, or kFinNone (padding).
 constexpr int kFinRows = 1024;
 constexpr uint32_t kFinNone = 0xFFFFFFFFu;
 
@@ -207,37 +208,14 @@ struct FinishJob {
 };
 
 // a row with clamp-delta entries, resolved when the batch is created: its sorted row (partials) and original
-// row, and its entries [e0, e1) of the batch's (column, value) list, so the tail thread's loads do not wait on
-// one another's results
+// row, and its entries [e0, e1) of the batch's (column, value) list
 struct FinDelta { int job, r, ro, e0, e1; };
 struct FinEntry { int col; float val; };
 
-__global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int nplain,
+__global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int ndblk,
                                                      const FinDelta *__restrict__ drows, const FinEntry *__restrict__ ent, int ndrows) {
-    if ((int)blockIdx.x < nplain) {
-        const uint32_t e = as_const(blk_job)[blockIdx.x];
-        if (e == kFinNone) return;
-        const FinishJob &J = jobs[e & 0xFFFFFFu];
-        const int r0 = (int)(e >> 24) * kFinRows + threadIdx.x;
-        const gptr<const float> wp = as_global(J.wpart);
-        int r[4];
-        uint32_t pd[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r[i] = min(r0 + 256 * i, J.rows - 1);
-            pd[i] = as_global(J.prmd)[r[i]];
-        }
-        for (int n = 0; n < J.ncol; ++n) {
-            float v[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int ks = 0; ks < J.nks; ++ks)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] += wp[((size_t)ks * J.ncol + n) * J.rows + r[i]];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[(size_t)n * J.ldy + pd[i]] = v[i];
-        }
-    } else {
-        const int i = ((int)blockIdx.x - nplain) * 256 + threadIdx.x;
+    if ((int)blockIdx.x < ndblk) {
+        const int i = (int)blockIdx.x * 256 + threadIdx.x;
         if (i >= ndrows) return;
         const FinDelta d = drows[i];
         const FinishJob &J = jobs[d.job];
@@ -251,6 +229,37 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
             }
             as_global_rw(J.y)[(size_t)n * J.ldy + d.ro] = v;
         }
+        return;
+    }
+    const uint32_t e = as_const(blk_job)[blockIdx.x - ndblk];
+    if (e == kFinNone) return;
+    const FinishJob &J = jobs[e & 0xFFFFFFu];
+    const int r0 = (int)(e >> 24) * kFinRows + threadIdx.x;
+    const gptr<const float> wp = as_global(J.wpart);
+    int r[4];
+    uint32_t pd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = min(r0 + 256 * i, J.rows - 1);
+        pd[i] = as_global(J.prmd)[r[i]];
+    }
+    for (int n = 0; n < J.ncol; ++n) {
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < J.nks; k0 += 4) {
+            float p[4][4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[k][i] = k0 + k < J.nks ? wp[((size_t)(k0 + k) * J.ncol + n) * J.rows + r[i]] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (k0 + k < J.nks) v[i] += p[k][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[(size_t)n * J.ldy + pd[i]] = v[i];
     }
 }
 
@@ -485,9 +494,10 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
         return launch_gemv_wave(b->ncols, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st);
     }
     if (stage == 2) {   // partial rows to original rows with the clamp delta
-        const int blocks = b->fin_blocks + (b->fin_ndrows + 255) / 256;
-        hipLaunchKernelGGL(k_gemv_finish, dim3(blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
-                           b->fin_blocks, (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
+        // the delta blocks first, padded to a multiple of the XCD count so plain block 8k + x still lands on XCD x
+        const int ndblk = (b->fin_ndrows + 255) / 256, ndpad = (ndblk + kXcds - 1) / kXcds * kXcds;
+        hipLaunchKernelGGL(k_gemv_finish, dim3(ndpad + b->fin_blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
+                           ndpad, (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
