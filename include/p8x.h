@@ -153,6 +153,41 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b);
 typedef struct p8x_batch_info { int njobs, ncols, class_set, units, split_jobs, small_launch, waves; } p8x_batch_info;
 int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out);
 
+/* ---- native model files (GGUF): slot bytes for p8x_prepare ----------------------------------------------- */
+/* The host side of the reference's model loader for VR tensors (llama_model_loader::vr_native_init and
+ * vr_native_load, CPU.patch:4700-4869): p8x_vr_open parses one GGUF file (or the shards of one model, metadata from
+ * the first) and checks its VR metadata (vr.format, vr.ns = 108, vr.trl = 2, vr.n_linear = 7 x block_count,
+ * vr.layout 2 or 3), finds every linear by its ".vr_c" side tensor and checks the side tensors (vr_c F16 [K], vr_prm
+ * I16 [rows] in layout 2 and none in layout 3, optional vr_didx I16 [nd, 2] + vr_dval F32 [nd], vr.had_signs I8
+ * [256]). p8x_vr_load assembles linear i's in-memory slot exactly as the reference's loader does (kernel bytes, VR3
+ * expanded; c16, prm or identity, pinv, delta, signs, trailer at the top-down offsets of a slot of slot_bytes, the
+ * size of the smallest of the reference's six quant slot types that holds it), with its checks (header NS / TRL,
+ * tables equal across tensors, kbytes against the M words, prm a permutation, delta indices, signs +-1). Failures
+ * return P8X_ERR_FORMAT with the reason in p8x_last_error(). Loads of one file may run on several threads. */
+typedef struct p8x_vr_file p8x_vr_file;
+typedef struct p8x_vr_desc {
+    const char *name;       /* "<base>.weight" (valid while the file is open) */
+    int rows, K, nd;
+    int layout;             /* 2: sorted rows + vr_prm; 3: VR3 file bytes, natural rows */
+    size_t fbytes;          /* bytes of the weight tensor in the file */
+    size_t kbytes;          /* kernel bytes in memory (header, M, S, D) */
+    size_t slot_bytes;      /* bytes p8x_vr_load writes (pass them to p8x_prepare as n) */
+    int slot_type;          /* the ggml quant type of that slot (IQ2_XXS = 16, Q2_K = 10 .. Q6_K = 14) */
+} p8x_vr_desc;
+int p8x_vr_open(const char *const *paths, int npaths, p8x_vr_file **out);
+int p8x_vr_count(const p8x_vr_file *f);
+int p8x_vr_find(const p8x_vr_file *f, const char *name);   /* index of "<base>.weight", or -1 */
+int p8x_vr_describe(const p8x_vr_file *f, int i, p8x_vr_desc *out);
+int p8x_vr_load(p8x_vr_file *f, int i, void *slot, size_t cap);
+void p8x_vr_close(p8x_vr_file *f);
+/* The VR3 file layout (llama-vr3.h vrn3_rows / vrn3_expand, CPU.patch:4916-4950): one class per tensor, natural
+ * rows, no M words; word 515 = P8X_VR3_TAG | class. p8x_vr3_rows: rows from the file size, K and word 515 (0 when
+ * inconsistent), *kbytes = the expanded kernel bytes. p8x_vr3_expand writes those kbytes (arithmetic M words, word
+ * 515 = 0, zero pad before the payload). */
+#define P8X_VR3_TAG 0x56523300u
+size_t p8x_vr3_rows(size_t fbytes, size_t K, uint32_t w515, size_t *kbytes);
+int p8x_vr3_expand(const void *file_bytes, size_t fbytes, size_t rows, size_t K, void *dst, size_t cap);
+
 /* ---- host-side producers (not on the hot path) -------------------------------------------------------- */
 /* Random valid tensor slot (the reference's random-valid timing arm, CPU.patch:4391-4458). class_p[8] are
  * tile-class probabilities; codebook 0 = the shipped table (research/work/r48k3/tables_vrc.pt), 1 = random

@@ -749,7 +749,6 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
         e = b + 1;
         while (e < bend && (mrow[e] >> 29) == (uint32_t)C) ++e;
     }
-    constexpr int NW = nw_of(C);
     // activations [NCOL][K] int8 and scales [NCOL][K / 128]
     const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.K), dbytes = (uint32_t)(NCOL * J.nsl) * 4u;
     const uint32_t vo = StepSlice<C>::quad_offset(hs, j), vp = StepSlice<C>::pair_offset(hs, j);

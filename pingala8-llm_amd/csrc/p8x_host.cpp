@@ -43,6 +43,15 @@ int num_cus() {
 
 static int nw_tile(uint32_t m) { return nw_of((int)(m >> 29)); }
 
+void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]) {
+    const size_t t = n - 32, sg = t - 256;
+    const size_t q = (sg - 2 * rows) & ~(size_t)15;
+    const size_t p = (q - 2 * rows) & ~(size_t)15;
+    const size_t c = (p - 2 * K) & ~(size_t)15;
+    const size_t e = (c - 8 * nd) & ~(size_t)15;
+    off[0] = e; off[1] = c; off[2] = p; off[3] = q; off[4] = sg; off[5] = t;
+}
+
 // row scales [nb][rows] -> [ng][nb][32], one element per thread
 __global__ void k_regroup_scales(const uint16_t *__restrict__ S, uint16_t *__restrict__ Sg, int nb, int rows, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -95,14 +104,6 @@ int p8x_probe(const void *slot, size_t n, int rows, int K) {
     return tr[0] == kMagic0 && tr[1] == kMagic1 && tr[4] == (uint32_t)rows && tr[5] == (uint32_t)K && tr[6] == kNS;
 }
 
-static void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]) {
-    const size_t t = n - 32, sg = t - 256;
-    const size_t q = (sg - 2 * rows) & ~(size_t)15;
-    const size_t p = (q - 2 * rows) & ~(size_t)15;
-    const size_t c = (p - 2 * K) & ~(size_t)15;
-    const size_t e = (c - 8 * nd) & ~(size_t)15;
-    off[0] = e; off[1] = c; off[2] = p; off[3] = q; off[4] = sg; off[5] = t;
-}
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;

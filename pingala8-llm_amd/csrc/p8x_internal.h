@@ -76,5 +76,8 @@ int reserve_mul_mat(const p8x_tensor *t, int n_max);
 int scratch_resolve(int device);
 
 int num_cus();
+// offsets of the side regions of an n-byte slot, top-down from its end (vrn_offsets, CPU.patch:33-40):
+// delta, c16, prm, pinv, signs, trailer
+void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]);
 
 }  // namespace p8x

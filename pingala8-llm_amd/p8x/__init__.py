@@ -16,6 +16,7 @@ P8X_OK, P8X_ERR_ARG, P8X_ERR_FORMAT, P8X_ERR_HIP, P8X_ERR_UNSUPPORTED, P8X_ERR_N
 F32, F16, BF16, I16 = 0, 1, 2, 3
 ACT_Q8_128, ACT_Q8_1 = 0, 1
 MAX_COLS = 8
+VR3_TAG = 0x56523300
 
 EXPORTS = [
     "p8x_version", "p8x_error_string", "p8x_last_error", "p8x_need", "p8x_probe", "p8x_prepare", "p8x_release",
@@ -23,6 +24,8 @@ EXPORTS = [
     "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_mul_mat_reserve", "p8x_synth_random",
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
+    "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
+    "p8x_vr3_expand",
 ]
 
 
@@ -34,6 +37,12 @@ class Info(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_int), ("K", ctypes.c_int), ("nd", ctypes.c_int), ("ng", ctypes.c_int), ("nb", ctypes.c_int),
                 ("n", ctypes.c_size_t), ("kbytes", ctypes.c_size_t), ("stream_bytes", ctypes.c_size_t),
                 ("class_tiles", ctypes.c_size_t * 8), ("dev_base", ctypes.c_void_p)]
+
+
+class VrDesc(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("rows", ctypes.c_int), ("K", ctypes.c_int), ("nd", ctypes.c_int),
+                ("layout", ctypes.c_int), ("fbytes", ctypes.c_size_t), ("kbytes", ctypes.c_size_t),
+                ("slot_bytes", ctypes.c_size_t), ("slot_type", ctypes.c_int)]
 
 
 class BatchInfo(ctypes.Structure):
@@ -71,6 +80,14 @@ def lib():
     L.p8x_mul_mat.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
     L.p8x_mul_mat_reserve.argtypes = [vp, i]
     L.p8x_mul_mat_noalloc.argtypes = [vp, vp, i, i, sz, vp, sz, vp]
+    L.p8x_vr_open.argtypes = [ctypes.POINTER(ctypes.c_char_p), i, ctypes.POINTER(vp)]
+    L.p8x_vr_count.argtypes = [vp]
+    L.p8x_vr_find.argtypes = [vp, ctypes.c_char_p]
+    L.p8x_vr_describe.argtypes = [vp, i, ctypes.POINTER(VrDesc)]
+    L.p8x_vr_load.argtypes = [vp, i, vp, sz]
+    L.p8x_vr_close.argtypes = [vp]; L.p8x_vr_close.restype = None
+    L.p8x_vr3_rows.argtypes = [sz, sz, ctypes.c_uint32, ctypes.POINTER(sz)]; L.p8x_vr3_rows.restype = sz
+    L.p8x_vr3_expand.argtypes = [vp, sz, sz, sz, vp, sz]
     L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
     L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
     L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
@@ -273,6 +290,58 @@ def quantize_tensor(W, c16=None, sign_seed=0):
     buf = np.empty(n.value + 64, np.uint8)
     check(L.p8x_quantize_tensor(W.ctypes.data, rows, K, cptr, sign_seed, buf.ctypes.data, buf.size, ctypes.byref(n)), "quantize_tensor")
     return buf[:n.value].copy()
+
+
+# --------------------------------------------------------------------------------------------------- model files
+class VrFile:
+    """A native Pingala-8 model file (GGUF; one path, or the shards of one model)."""
+
+    def __init__(self, paths):
+        if isinstance(paths, (str, bytes, os.PathLike)):
+            paths = [paths]
+        arr = (ctypes.c_char_p * len(paths))(*[os.fsencode(p) for p in paths])
+        self.h = ctypes.c_void_p()
+        check(lib().p8x_vr_open(arr, len(paths), ctypes.byref(self.h)), "p8x_vr_open")
+
+    def __len__(self):
+        return lib().p8x_vr_count(self.h)
+
+    def find(self, name):
+        return lib().p8x_vr_find(self.h, name.encode())
+
+    def describe(self, i):
+        d = VrDesc()
+        check(lib().p8x_vr_describe(self.h, i, ctypes.byref(d)), "p8x_vr_describe")
+        return {f: (getattr(d, f).decode() if f == "name" else getattr(d, f)) for f, _ in VrDesc._fields_}
+
+    def load(self, i):
+        """slot bytes of linear i (numpy uint8), ready for Tensor(slot, rows, K)"""
+        n = self.describe(i)["slot_bytes"]
+        buf = np.empty(n, np.uint8)
+        check(lib().p8x_vr_load(self.h, i, buf.ctypes.data, n), "p8x_vr_load")
+        return buf
+
+    def close(self):
+        if self.h:
+            lib().p8x_vr_close(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def vr3_rows(fbytes, K, w515):
+    kb = ctypes.c_size_t(0)
+    rows = lib().p8x_vr3_rows(fbytes, K, w515, ctypes.byref(kb))
+    return rows, kb.value
+
+
+def vr3_expand(file_bytes, rows, K, out):
+    f = np.ascontiguousarray(file_bytes, np.uint8)
+    check(lib().p8x_vr3_expand(f.ctypes.data, f.size, rows, K, out.ctypes.data, out.size), "p8x_vr3_expand")
 
 
 # --------------------------------------------------------------------------------------------------- tensors
