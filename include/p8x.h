@@ -45,7 +45,7 @@ enum {
 
 enum { P8X_F32 = 0, P8X_F16 = 1, P8X_BF16 = 2, P8X_I16 = 3 };
 enum { P8X_DOMAIN_ORIGINAL = 0, P8X_DOMAIN_ROTATED = 1 };
-enum { P8X_ACT_Q8_128 = 0, P8X_ACT_Q8_1 = 1 };
+enum { P8X_ACT_Q8_128 = 0, P8X_ACT_Q8_1 = 1, P8X_ACT_X16 = 2 };
 
 #define P8X_MAX_COLS 8
 
@@ -95,6 +95,12 @@ int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, voi
  * (d = amax/127), sum [ncols][K/128] (sum of q; may be NULL). Bit-exact to vrc_prep_block / k_vr_qx_real. */
 int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx,
                         int8_t *q, float *d, int32_t *sum, void *stream);
+/* x16 precision mode (the reference CPU path's default, vrc_prep_block16, CPU.patch:575-616): per 128-column half,
+ * d = max|x'| / 8191 and q = round-half-even(x' / d) (14 bits), split into two 8-bit planes q = 128 hi + lo:
+ * qh/ql [ncols][K] int8, dh = 128 d and dl = d [ncols][K/128], sh/sl sums (may be NULL). Bit-exact to the reference.
+ * The planes are two virtual 8-bit-per-128 columns: p8x_vec_dot(P8X_ACT_Q8_128) takes them as such. */
+int p8x_quantize_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh,
+                     int8_t *ql, float *dl, int32_t *sl, void *stream);
 /* x' quantized to ggml block_q8_1 (36 B: fp16 d, fp16 s, 32 x int8), [ncols][K/32] blocks, with ggml's
  * quantize_row_q8_1_ref convention: d = amax/127, q = roundf(x' * (1/d)) (ties away from zero), s = fp16(d * sum q).
  * The products read d and q only, so blocks from another q8_1 producer (ggml's CUDA kernel, say) are accepted. */
@@ -114,6 +120,8 @@ int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int
  * tensor's handle: calls on one tensor from different streams must not overlap (on one stream they are
  * ordered); the counters are put back by each call. Records kernel launches only (capture-safe). */
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
+/* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1, or P8X_ACT_X16 (1..4
+ * columns: both planes of each column through one GEMV, summed, then the clamp delta; the reference's CPU default) */
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
  * X in P8X_F32 or P8X_BF16 (16-byte aligned, ldx % 8 == 0). The Hadamard rotation is applied to X (fp16 x'),

@@ -62,6 +62,7 @@ def lib():
         L.orc_partials_q8_1.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
         L.orc_gemv_q8_128_f64.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
         L.orc_gemv_q8_1_f64.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
+        L.orc_gemv_x16_f64.argtypes = [ctypes.POINTER(OrcTensor), vp, vp]
         L.orc_gemv_q8_128_f64_cols.argtypes = [ctypes.POINTER(OrcTensor), vp, i, sz, vp]
         L.orc_dense_f64.argtypes = [vp, i, i, vp, i, vp]
         L.orc_h2f.argtypes = [ctypes.c_uint16]; L.orc_h2f.restype = ctypes.c_float
@@ -150,7 +151,7 @@ class Oracle:
     def gemv_f64(self, x, act="q8_128"):
         x = np.ascontiguousarray(x, np.float32)
         y = np.zeros(self.rows, np.float64)
-        fn = lib().orc_gemv_q8_128_f64 if act == "q8_128" else lib().orc_gemv_q8_1_f64
+        fn = {"q8_128": lib().orc_gemv_q8_128_f64, "q8_1": lib().orc_gemv_q8_1_f64, "x16": lib().orc_gemv_x16_f64}[act]
         fn(ctypes.byref(self.t), _p(x), _p(y))
         return y
 

@@ -438,6 +438,29 @@ void orc_gemv_q8_128_f64(const orc_tensor *t, const float *x, double *y) {
     free(q); free(d); free(sx); free(isum);
 }
 
+/* fp64 GEMV on x16 activations (vrc_prep_block16 planes, CPU.patch:575-616; the planes are two virtual columns that the
+ * reference sums before the clamp delta, CPU.patch:1232-1244, :1193): y[prm[r]] = sum_s S (hi_s 128 d_s + lo_s d_s)
+ * + delta . x, with hi_s / lo_s the integer partials of each plane */
+void orc_gemv_x16_f64(const orc_tensor *t, const float *x, double *y) {
+    int8_t *qh = (int8_t *)malloc((size_t)t->K), *ql = (int8_t *)malloc((size_t)t->K);
+    float *dh = (float *)malloc(sizeof(float) * (size_t)t->nsl), *dl = (float *)malloc(sizeof(float) * (size_t)t->nsl);
+    int32_t *sh = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->nsl), *sl = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->nsl);
+    int32_t *ih = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->rows * t->nsl), *il = (int32_t *)malloc(sizeof(int32_t) * (size_t)t->rows * t->nsl);
+    orc_prep_x16(t, x, qh, dh, sh, ql, dl, sl);
+    orc_partials_q8_128(t, qh, ih);
+    orc_partials_q8_128(t, ql, il);
+    for (int r = 0; r < t->rows; ++r) {
+        double acc = 0.0;
+        for (int s = 0; s < t->nsl; ++s) {
+            const double sc = (double)orc_h2f(t->S[(size_t)(s >> 1) * t->rows + r]);
+            acc += ((double)ih[(size_t)r * t->nsl + s] * (double)dh[s] + (double)il[(size_t)r * t->nsl + s] * (double)dl[s]) * sc;
+        }
+        y[t->prm[r]] = acc;
+    }
+    add_delta_f64(t, x, y);
+    free(qh); free(ql); free(dh); free(dl); free(sh); free(sl); free(ih); free(il);
+}
+
 /* the same fp64 GEMV for ncols activation columns x [ncols][ldx] -> y [ncols][rows], each tile decoded once;
  * per column the arithmetic (integer partials, then the half-slice sum in order) is orc_gemv_q8_128_f64's */
 void orc_gemv_q8_128_f64_cols(const orc_tensor *t, const float *x, int ncols, size_t ldx, double *y) {

@@ -103,6 +103,8 @@ void orc_partials_q8_1(const orc_tensor *t, const uint8_t *blocks, int32_t *isum
 /* fp64 GEMV: y[prm[r]] = sum_s S*XS*isum + delta . x (original rows) */
 void orc_gemv_q8_128_f64(const orc_tensor *t, const float *x, double *y);
 void orc_gemv_q8_1_f64(const orc_tensor *t, const float *x, double *y);
+/* fp64 GEMV on the x16 planes (hi scaled 128 d, lo scaled d), planes summed before the clamp delta */
+void orc_gemv_x16_f64(const orc_tensor *t, const float *x, double *y);
 /* orc_gemv_q8_128_f64 for ncols columns x [ncols][ldx] -> y [ncols][rows] (each tile decoded once) */
 void orc_gemv_q8_128_f64_cols(const orc_tensor *t, const float *x, int ncols, size_t ldx, double *y);
 /* fp64 dense product with the f32-dequantized weights (prompt GEMM reference): y[n][r] = W[r] . x[n] */

@@ -42,6 +42,62 @@ __global__ __launch_bounds__(64) void k_act_q8_128(const float *__restrict__ x, 
     }
 }
 
+// x16 precision mode (vrc_prep_block16, CPU.patch:575-616): per 128-column half, d = max|x'| / 8191, q = round-half-even
+// (x' * (1/d)) (14 bits), split q = 128 hi + lo with hi = (q + 64) >> 7: two int8 planes scaled 128 d and d. grid (nb,
+// ncols), block 64 (lane l: x' elements 4l .. 4l+3); outputs like k_act_q8_128 per plane.
+__global__ __launch_bounds__(64) void k_act_x16(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
+                                                int8_t *__restrict__ qh, float *__restrict__ dh, int32_t *__restrict__ sh,
+                                                int8_t *__restrict__ ql, float *__restrict__ dl, int32_t *__restrict__ sl, int qstride) {
+    const int b = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    BlockLane in;
+    in.load(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane);
+    float v[4];
+    rotate_block_lane(in, lane, v);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = half_wave_max(am, lane);
+    const float dd = div_rn(am, 8191.f);
+    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
+    int hi[4], lo[4], s_hi = 0, s_lo = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int q = __float2int_rn(v[e] * id);
+        hi[e] = (q + 64) >> 7;
+        lo[e] = q - 128 * hi[e];
+        s_hi += hi[e];
+        s_lo += lo[e];
+    }
+    auto pack = [](const int (&a)[4]) {
+        return (uint32_t)(uint8_t)a[0] | ((uint32_t)(uint8_t)a[1] << 8) | ((uint32_t)(uint8_t)a[2] << 16) | ((uint32_t)(uint8_t)a[3] << 24);
+    };
+    const size_t qo = (size_t)n * qstride + 256 * b;
+    reinterpret_cast<uint32_t *>(qh + qo)[lane] = pack(hi);
+    reinterpret_cast<uint32_t *>(ql + qo)[lane] = pack(lo);
+    s_hi = half_wave_sum(s_hi, lane);
+    s_lo = half_wave_sum(s_lo, lane);
+    const int nsl = K / 128;
+    if ((lane & 31) == 0) {
+        const size_t so = (size_t)n * (qstride / 128) + 2 * b + (lane >> 5);
+        dh[so] = 128.f * dd;
+        dl[so] = dd;
+        if (sh) sh[so] = s_hi;
+        if (sl) sl[so] = s_lo;
+    }
+    (void)nsl;
+}
+
+// x16 products: y[n][ro] = (plane sums: hi column 2n + lo column 2n + 1, already in original rows) + the clamp delta
+// of row ro on the original activations, as the reference sums its two planes then adds the delta (CPU.patch:1193)
+__global__ __launch_bounds__(256) void k_x16_combine(const float *__restrict__ yv, int rows, const float *__restrict__ x, size_t ldx,
+                                                     const int *__restrict__ cp, const uint16_t *__restrict__ cc, const float *__restrict__ cv,
+                                                     float *__restrict__ y, size_t ldy) {
+    const int ro = blockIdx.x * 256 + threadIdx.x, n = blockIdx.y;
+    if (ro >= rows) return;
+    float v = yv[(size_t)(2 * n) * rows + ro] + yv[(size_t)(2 * n + 1) * rows + ro];
+    const float *xr = x + (size_t)n * ldx;
+    for (int e = cp[ro]; e < cp[ro + 1]; ++e) v += cv[e] * xr[cc[e]];
+    y[(size_t)n * ldy + ro] = v;
+}
+
 // block_q8_1 over x' (ggml layout: fp16 d, fp16 s = d * sum q, 32 int8). 8 lanes per 32-column block.
 __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
                                                  uint8_t *__restrict__ blocks) {
@@ -523,6 +579,24 @@ namespace p8x {
 int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st) {
     hipLaunchKernelGGL(k_act_q8_128, dim3(t->nb, ncols), dim3(64), 0, st, x, ldx, (const float *)t->ic, t->K, q, d, sum);
     return hip_check(hipGetLastError(), "k_act_q8_128 launch");
+}
+
+int launch_act_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh, int8_t *ql, float *dl,
+                   int32_t *sl, int qstride, hipStream_t st) {
+    hipLaunchKernelGGL(k_act_x16, dim3(t->nb, ncols), dim3(64), 0, st, x, ldx, (const float *)t->ic, t->K, qh, dh, sh, ql, dl, sl, qstride);
+    return hip_check(hipGetLastError(), "k_act_x16 launch");
+}
+
+// x16 products of ncols <= 4 columns: both planes of every column quantized into the handle's workspace as 2 ncols
+// virtual columns (hi of column n at 2n, lo at 2n + 1), one 8-bit-per-128 GEMV over them into the plane rows, then
+// the combine pass
+int launch_gemv_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, hipStream_t st) {
+    int rc;
+    if ((rc = launch_act_x16(t, x, ncols, ldx, t->wq, t->wd, nullptr, t->wq + t->K, t->wd + t->nsl, nullptr, 2 * t->K, st))) return rc;
+    if ((rc = launch_gemv(t, P8X_ACT_Q8_128, t->wq, t->wd, 2 * ncols, nullptr, 0, t->wy, t->rows, nullptr, st))) return rc;
+    hipLaunchKernelGGL(k_x16_combine, dim3((t->rows + 255) / 256, ncols), dim3(256), 0, st, (const float *)t->wy, t->rows, x, ldx,
+                       (const int *)t->cp, (const uint16_t *)t->cc, (const float *)t->cv, y, ldy);
+    return hip_check(hipGetLastError(), "k_x16_combine launch");
 }
 
 int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, hipStream_t st) {

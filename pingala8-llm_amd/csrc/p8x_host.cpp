@@ -107,7 +107,7 @@ int p8x_probe(const void *slot, size_t n, int rows, int K) {
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->wy, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -277,6 +277,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wsum, 4 * (size_t)P8X_MAX_COLS * nsl, "sum"))) return fail(rc);
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
     if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wy, 4 * (size_t)P8X_MAX_COLS * rows, "x16 plane rows"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
     {
         std::vector<int16_t> pinv(rows);
@@ -343,6 +344,14 @@ int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t l
     return launch_act_q8_128(t, x, ncols, ldx, q, d, sum, (hipStream_t)stream);
 }
 
+int p8x_quantize_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh, int8_t *ql,
+                     float *dl, int32_t *sl, void *stream) {
+    if (!t || !x || !qh || !dh || !ql || !dl) return set_error(P8X_ERR_ARG, "p8x_quantize_x16: null pointer");
+    if (ncols < 1 || ldx < (size_t)t->K || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "p8x_quantize_x16: ncols %d ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", ncols, ldx);
+    return launch_act_x16(t, x, ncols, ldx, qh, dh, sh, ql, dl, sl, t->K, (hipStream_t)stream);
+}
+
 int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, void *stream) {
     if (!t || !x || !blocks) return set_error(P8X_ERR_ARG, "p8x_quantize_q8_1: null pointer");
     if (ncols < 1 || ldx < (size_t)t->K || ldx % 4 || ((uintptr_t)x & 15))
@@ -372,6 +381,10 @@ int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols,
     if (act == P8X_ACT_Q8_1) {
         if ((rc = launch_act_q8_1(t, x, ncols, ldx, t->wq81, st))) return rc;
         return launch_gemv(t, act, t->wq81, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
+    }
+    if (act == P8X_ACT_X16) {
+        if (2 * ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: x16 takes at most %d columns", P8X_MAX_COLS / 2);
+        return launch_gemv_x16(t, x, ncols, ldx, y, ldy, st);
     }
     return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: act %d", act);
 }

@@ -38,6 +38,7 @@ struct p8x_tensor {
     float *wd = nullptr;             // [P8X_MAX_COLS][nsl]
     int32_t *wsum = nullptr;         // [P8X_MAX_COLS][nsl]
     uint8_t *wq81 = nullptr;         // block_q8_1 [P8X_MAX_COLS][K / 32]
+    float *wy = nullptr;             // x16 products: plane rows [2 x 4][rows]
     float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan
     size_t wpart_floats = 0;
     unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
@@ -66,6 +67,10 @@ int rg_plan(const p8x_tensor *t, int ncols, int *kc);
 // launchers (p8x_gemv.hip, p8x_decode.hip, p8x_gemm.hip)
 int launch_act_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, hipStream_t st);
 int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, hipStream_t st);
+// x16 planes: column n's hi plane at qh + n qstride, lo plane at ql + n qstride (scales and sums at n qstride / 128)
+int launch_act_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh, int8_t *ql, float *dl,
+                   int32_t *sl, int qstride, hipStream_t st);
+int launch_gemv_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, hipStream_t st);
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st);
 int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libp8x.so")
 
 P8X_OK, P8X_ERR_ARG, P8X_ERR_FORMAT, P8X_ERR_HIP, P8X_ERR_UNSUPPORTED, P8X_ERR_NOMEM = range(6)
 F32, F16, BF16, I16 = 0, 1, 2, 3
-ACT_Q8_128, ACT_Q8_1 = 0, 1
+ACT_Q8_128, ACT_Q8_1, ACT_X16 = 0, 1, 2
 MAX_COLS = 8
 VR3_TAG = 0x56523300
 
@@ -25,7 +25,7 @@ EXPORTS = [
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
-    "p8x_vr3_expand",
+    "p8x_vr3_expand", "p8x_quantize_x16",
 ]
 
 
@@ -74,6 +74,7 @@ def lib():
     L.p8x_decode_rotated.argtypes = [vp, i, vp, sz, vp]
     L.p8x_quantize_q8_128.argtypes = [vp, vp, i, sz, vp, vp, vp, vp]
     L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
+    L.p8x_quantize_x16.argtypes = [vp, vp, i, sz, vp, vp, vp, vp, vp, vp, vp]
     L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
@@ -442,6 +443,18 @@ class Tensor:
         synchronize()
         return (q.to_numpy(np.int8, (ncols, self.K)), d.to_numpy(np.float32, (ncols, self.nsl)),
                 s.to_numpy(np.int32, (ncols, self.nsl)))
+
+    def quantize_x16(self, x):
+        """(qh, dh, sh, ql, dl, sl) per column: the x16 planes"""
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        ncols = x.shape[0]
+        xd = DeviceBuffer.from_numpy(x)
+        bufs = [DeviceBuffer(ncols * self.K), DeviceBuffer(4 * ncols * self.nsl), DeviceBuffer(4 * ncols * self.nsl),
+                DeviceBuffer(ncols * self.K), DeviceBuffer(4 * ncols * self.nsl), DeviceBuffer(4 * ncols * self.nsl)]
+        check(lib().p8x_quantize_x16(self.h, xd.ptr, ncols, self.K, *[b.ptr for b in bufs], None), "p8x_quantize_x16")
+        synchronize()
+        kinds = [(np.int8, self.K), (np.float32, self.nsl), (np.int32, self.nsl)] * 2
+        return tuple(b.to_numpy(dt, (ncols, n)) for b, (dt, n) in zip(bufs, kinds))
 
     def quantize_q8_1(self, x):
         x = np.ascontiguousarray(np.atleast_2d(x), np.float32)

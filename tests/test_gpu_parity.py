@@ -355,3 +355,34 @@ def test_wrapping_codebook():
         assert rel_l2(Y[n], orc.gemv_f64(X[n])) < 1e-5, n
     Xm = rng.standard_normal((40, K)).astype(np.float32)
     assert rel_l2(t.mul_mat(Xm, p8x.F32), O.dense_f64(W, Xm)) < 1e-3
+
+
+def test_act_x16_exact(case):
+    """x16 planes bit-exact to the reference core's vrc_prep_block16 (fixtures)"""
+    qh, dh, sh, ql, dl, sl = case["t"].quantize_x16(case["x"])
+    assert np.array_equal(qh[0], case["x16_hi"]) and np.array_equal(ql[0], case["x16_lo"])
+    assert np.array_equal(dh[0].view(np.uint32), case["x16_hi_d"].view(np.uint32))
+    assert np.array_equal(dl[0].view(np.uint32), case["x16_lo_d"].view(np.uint32))
+    assert np.array_equal(sh[0], case["x16_hi_sum"]) and np.array_equal(sl[0], case["x16_lo_sum"])
+
+
+def test_gemv_x16(case):
+    """x16 products against the fp64 oracle on the same planes and the reference core's own x16 GEMV"""
+    orc = O.Oracle(case["slot"], case["rows"], case["K"])
+    y = case["t"].mul_mat_vec(case["x"], act=p8x.ACT_X16)[0]
+    assert rel_l2(y, orc.gemv_f64(case["x"], act="x16")) < 1e-5
+    assert rel_l2(y, case["y_x16"]) < 1e-5
+
+
+@pytest.mark.parametrize("rows,K,ncols", [(256, 2560, 1), (256, 2560, 2), (256, 2560, 3), (256, 2560, 4), (4096, 14336, 1),
+                                          (14336, 4096, 2)])
+def test_gemv_x16_columns_and_shapes(rows, K, ncols):
+    slot = p8x.synth_random(rows + ncols, rows, K, class_p=(1, 1, 1, 4, 1, 1, 1, 1) if rows == 256 else (0, 0, 0, 1, 0, 0, 0, 0), nd=6)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    X = np.random.default_rng(ncols).standard_normal((ncols, K)).astype(np.float32)
+    Y = t.mul_mat_vec(X, act=p8x.ACT_X16)
+    for n in range(ncols):
+        assert rel_l2(Y[n], orc.gemv_f64(X[n], act="x16")) < 1e-5, n
+    with pytest.raises(p8x.P8xError, match="x16 takes at most 4"):
+        t.mul_mat_vec(np.zeros((5, K), np.float32), act=p8x.ACT_X16)

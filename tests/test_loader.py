@@ -35,7 +35,7 @@ class Linear:
     def __init__(self, rng, rows, K, A, cs, sg, natural, cls=None, nd=0):
         ng, nb = rows // 32, K // 256
         self.rows, self.K, self.nd = rows, K, nd
-        self.cls = np.full((ng, nb), cls, np.int64) if cls else rng.choice([1, 2, 3, 4, 5, 6, 7], size=(ng, nb))
+        self.cls = np.full((ng, nb), cls, np.int64) if cls else rng.choice([1, 2, 3, 4, 5], size=(ng, nb))
         nwords = int(sum(64 * slotgen.NW[c] for c in self.cls.reshape(-1)))
         self.payload = rng.integers(0, 1 << 32, size=nwords, dtype=np.uint64).astype(np.uint32)
         self.S = rng.uniform(2e-4, 3e-4, size=(nb, rows)).astype(np.float16).view(np.uint16)

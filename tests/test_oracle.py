@@ -109,6 +109,17 @@ def test_prep_x16_bit_exact(case):
     assert np.array_equal(sh, case["x16_hi_sum"]) and np.array_equal(sl, case["x16_lo_sum"])
 
 
+def test_gemv_x16_f64_matches_reference_gemv(case):
+    """fp64 GEMV on the x16 planes vs the reference core's own fp32 two-phase GEMV in its x16 mode (y_x16), and a
+    negative control: the q8 GEMV differs from y_x16 by far more (the modes quantize the activations differently)"""
+    y = case["orc"].gemv_f64(case["x"], act="x16")
+    ref = case["y_x16"].astype(np.float64)
+    rel = np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert rel < 1e-5, rel
+    y8 = case["orc"].gemv_f64(case["x"])
+    assert np.linalg.norm(y8 - ref) / np.linalg.norm(ref) > 10 * rel
+
+
 def test_partials_are_integer_matmul(case):
     orc = case["orc"]
     q, d, sx = orc.prep_q8_128(case["x"])
