@@ -123,6 +123,18 @@ int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, 
 /* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1, or P8X_ACT_X16 (1..4
  * columns: both planes of each column through one GEMV, summed, then the clamp delta; the reference's CPU default) */
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
+/* Several linears on the same activation vector in one launch, batch 1 (the q/k/v or gate/up of a layer; ggml issues
+ * one mul_mat per linear): y_i = W_i x for n = 1..4 tensors with the same K, codebook and input rotation (column
+ * scales c and signs; a file encodes the linears that share an input with one c). Same arithmetic and results as n
+ * p8x_mul_mat_vec calls; no counterpart in the reference. */
+int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy,
+                          void *stream);
+/* The gated FFN input in one launch, batch 1: out[r] = silu(gate x)[r] * (up x)[r], silu(g) = g / (1 + e^-g) (ggml's
+ * swiglu, the fusion ggml applies to mul_mat_vec + glu and the reference switches off for its tensors, CPU.patch:2608-
+ * 2610). gate and up: same rows, K, codebook and input rotation; the two products are p8x_mul_mat_vec's (with their
+ * clamp deltas), each row's pair meets through the gate tensor's workspace (calls with one gate tensor are ordered
+ * on one stream). */
+int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream);
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
  * X in P8X_F32 or P8X_BF16 (16-byte aligned, ldx % 8 == 0). The Hadamard rotation is applied to X (fp16 x'),
  * weight tiles are decoded from the LDS coset table straight into fp16 MFMA operands (v S), fp32 accumulation,

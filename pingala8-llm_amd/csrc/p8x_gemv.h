@@ -547,26 +547,84 @@ __device__ __forceinline__ void rg_quantize(int nbk, RgSmem<NCOL> &sm, const Blo
     }
 }
 
+// Linears of one launch of the row-group kernel: 1..kRgMaxJobs GEMVs on the same activations (same x, K and rotation
+// sg / c: q/k/v, or gate/up), row groups numbered across the jobs (job i owns gbase[i] .. gbase[i + 1] - 1). With glu,
+// jobs 0 (gate) and 1 (up) do not write their rows: each row's two values meet through a per-row arrival counter and
+// the second arrival writes out[row] = silu(gate) * up (ggml's swiglu).
+// Job 0 travels by value (a single call reads only it); with several jobs each workgroup serves one job: workgroups
+// wgbase[i] .. wgbase[i + 1] - 1 take job i, whose tensor metadata comes from its tensor's device copy jt[i] and
+// its output from y[i] / ldy[i] (selected once, by comparisons: indexing the arguments at run time would copy them
+// to scratch). Unused wgbase entries are INT_MAX.
+constexpr int kRgMaxJobs = 4;
+struct RgJobs {
+    GemvJob j0;                        // job 0: activations, K plan and rotation of every job
+    kptr<const GemvJob> jt[kRgMaxJobs];   // tensor metadata of each job (device memory, read-only: scalar loads)
+    float *y[kRgMaxJobs];
+    unsigned ldy[kRgMaxJobs];
+    int wgbase[kRgMaxJobs + 1];
+    int njobs;
+    int glu;
+    float *glu_out;        // [rows] original rows
+    float *glu_pair;       // [2][rows]: gate, up values by original row (agent-coherent)
+    unsigned *glu_cnt;     // [rows] arrival counters, 0 between calls
+};
+
+template <typename T>
+__device__ __forceinline__ T pick(int jb, T a0, T a1, T a2, T a3) { return jb == 0 ? a0 : jb == 1 ? a1 : jb == 2 ? a2 : a3; }
+
+// The second of a row's two arrivals computes silu(gate) * up: each lane stores its row's value (agent-coherent),
+// waits for the stores (as in arrive_after_stores), counts its arrival on the row's counter, and the lane that saw
+// the partner's arrival reads the partner's value and writes the output (the counter goes back to 0).
+__device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v, bool active) {
+    const gptr<float> pair = as_global_rw(R.glu_pair);
+    const int rows = R.j0.rows;
+    if (active) __hip_atomic_store(&pair[(size_t)jb * rows + r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned old = 0;
+    if (active) old = __hip_atomic_fetch_add(&R.glu_cnt[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("" ::: "memory");
+    if (active && old == 1u) {
+        const float other = __hip_atomic_load(&pair[(size_t)(1 - jb) * rows + r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float gate = jb == 0 ? v : other, up = jb == 0 ? other : v;
+        as_global_rw(R.glu_out)[r] = gate / (1.0f + expf(-gate)) * up;
+        __hip_atomic_store(&R.glu_cnt[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
 // NCOL x (blocks of a chunk) <= kRgMaxBlocks. gc row groups at a time: the waves form gc teams of WAVES / gc,
 // team t takes row group g0 + t * (workgroups per chunk) over the chunk, so that a workgroup with several row
-// groups streams them together instead of one after another.
-template <int CM, bool SPLIT, int NCOL, bool TEAMS>
+// groups streams them together instead of one after another. The activations, K plan and rotation come from job 0.
+template <int CM, bool SPLIT, int NCOL, bool TEAMS, bool MULTI>
 __global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
-void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2, int gc_) {
+void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
-    const GemvJob &J = job;
+    // this workgroup's job, its index among the job's workgroups and their count
+    int jb = 0, wgl = (int)blockIdx.x, nwg = (int)gridDim.x;
+    GemvJob JL = jobs.j0;
+    if constexpr (MULTI) {
+        const int bi = (int)blockIdx.x;
+        jb = (bi >= jobs.wgbase[1]) + (bi >= jobs.wgbase[2]) + (bi >= jobs.wgbase[3]);
+        const int wb = pick(jb, jobs.wgbase[0], jobs.wgbase[1], jobs.wgbase[2], jobs.wgbase[3]);
+        wgl = bi - wb;
+        nwg = pick(jb, jobs.wgbase[1], jobs.wgbase[2], jobs.wgbase[3], jobs.wgbase[4]) - wb;
+        JL = *(const GemvJob *)pick(jb, jobs.jt[0], jobs.jt[1], jobs.jt[2], jobs.jt[3]);
+        JL.x = jobs.j0.x; JL.ldx = jobs.j0.ldx; JL.nks = jobs.j0.nks; JL.kchunk = jobs.j0.kchunk;
+        JL.y = pick(jb, jobs.y[0], jobs.y[1], jobs.y[2], jobs.y[3]);
+        JL.ldy = pick(jb, jobs.ldy[0], jobs.ldy[1], jobs.ldy[2], jobs.ldy[3]);
+    }
+    const GemvJob &J = JL;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     TaskCtx<NCOL, P8X_ACT_Q8_128> c;
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64 + c.j;
-    // workgroup b: K-chunk ks = b % nks of row groups b / nks, b / nks + gridDim.x / nks, ...
+    // workgroup b (of the job's nwg): K-chunk ks = b % nks of row groups b / nks, b / nks + nwg / nks, ...
     const int nks = SPLIT ? J.nks : 1;
-    const int ks = SPLIT ? (int)blockIdx.x % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
+    const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
     c.b0 = ks * J.kchunk; c.nbl = nbk;
     const int wpg = WAVES / gc, team = w / wpg, wk = w % wpg;   // waves beyond gc teams stay idle
     const int per = nbk / wpg, rem = nbk % wpg;
@@ -588,19 +646,20 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2, int gc_) {
     else rg_quantize<4, NCOL>(nbk, sm, in, w, lane);
     __syncthreads();
     int set = 0;
-    const int gstep = (int)gridDim.x / nks;
-    for (int g0 = (int)blockIdx.x / nks; g0 < J.ng; g0 += gstep * gc, set ^= 1) {
+    const int gstep = nwg / nks;
+    const GemvJob &JB = J;
+    for (int g0 = wgl / nks; g0 < J.ng; g0 += gstep * gc, set ^= 1) {
         const int g = g0 + min(team, gc - 1) * gstep;   // this wave's row group
         const bool lead = wk == 0 && team < gc && g < J.ng;   // the team's first wave: epilogue of row group g
         c.g = g;
         // the output row, read before the tile loads so that the epilogue finds it in a register
         int ro = 0;
-        if (lead && lane < 32) ro = as_global(J.prmd)[32 * g + lane];
+        if (lead && lane < 32) ro = as_global(JB.prmd)[32 * g + lane];
         float yacc[NCOL];
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
         for (int b = b0; b < (g < J.ng ? b1 : b0);) {
-            const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
+            const uint32_t mt = as_const(JB.M)[(size_t)g * JB.nb + b];
             switch (mt >> 29) {
                 case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
                 case 2: if constexpr ((CM >> 2) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 2, gemv_nbuf(NCOL, 2), CM == (1 << 2)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
@@ -629,47 +688,55 @@ void k_gemv_rg(GemvJob job, const uint32_t *__restrict__ a2, int gc_) {
                     for (int i = 0; i < wpg; ++i) v[n] += sm.red[set][w + i][n][lane];
             }
             if constexpr (SPLIT) {   // K-chunks: the last arrival sums them in chunk order
-                const gptr<float> wpart = as_global_rw(J.wpart);
-                const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
+                const gptr<float> wpart = as_global_rw(JB.wpart);
+                const gptr<unsigned> wcnt = as_global_rw(JB.wcnt);
                 if (lane < 32)
 #pragma unroll
                     for (int n = 0; n < NCOL; ++n)
-                        __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * J.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (arrive_after_stores(J.wcnt + g, lane) != (unsigned)(nks - 1)) continue;
+                        __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * JB.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (arrive_after_stores(JB.wcnt + g, lane) != (unsigned)(nks - 1)) continue;
                 if (lane < 32)
 #pragma unroll
                     for (int n = 0; n < NCOL; ++n) {
                         v[n] = 0.f;
                         for (int k = 0; k < nks; ++k)
-                            v[n] += __hip_atomic_load(&wpart[((size_t)k * NCOL + n) * J.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            v[n] += __hip_atomic_load(&wpart[((size_t)k * NCOL + n) * JB.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane < 32) {
-                const int r = ro & 0x7FFF;
+            const int r = ro & 0x7FFF;
+            float vo[NCOL];
 #pragma unroll
-                for (int n = 0; n < NCOL; ++n) {
-                    float vn = v[n];
-                    if (ro & 0x8000) {
-                        const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;
-                        for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e) vn += as_global(J.cv)[e] * xr[as_global(J.cc)[e]];
-                    }
-                    as_global_rw(J.y)[(size_t)n * J.ldy + r] = vn;
+            for (int n = 0; n < NCOL; ++n) {
+                vo[n] = v[n];
+                if (lane < 32 && (ro & 0x8000)) {
+                    const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;   // the shared activations
+                    for (int e = as_global(JB.cp)[r]; e < as_global(JB.cp)[r + 1]; ++e) vo[n] += as_global(JB.cv)[e] * xr[as_global(JB.cc)[e]];
                 }
+            }
+            if (MULTI && jobs.glu) {
+                glu_meet(jobs, jb, r, vo[0], lane < 32);
+            } else if (lane < 32) {
+#pragma unroll
+                for (int n = 0; n < NCOL; ++n) as_global_rw(J.y)[(size_t)n * J.ldy + r] = vo[n];
             }
         }
     }
 }
 
-template <int CM, int NCOL>
-static int launch_gemv_rg_t(const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
+// ng = the row groups of all jobs; the K plan (nks) is job 0's
+template <int CM, int NCOL, bool MULTI>
+static int launch_gemv_rg_t(const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st) {
     // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups per K-chunk, one per CU
     const int per = (ng + num_cus() - 1) / num_cus();
     // a workgroup's row groups are streamed together (teams of waves), up to 4 at a time
     const int gc = std::min(per, 4);
-    if (job.nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false>), dim3((ng + per - 1) / per * job.nks), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, 1);
-    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, gc);
-    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false>), dim3((ng + per - 1) / per), dim3(64 * rg_waves(NCOL)), 0, st, job, a2, 1);
+    const int nks = jobs.j0.nks;
+    // several jobs: each takes ceil(its row groups / per) workgroups per K-chunk (wgbase, set by the caller)
+    const int grid = MULTI ? jobs.wgbase[4] : (ng + per - 1) / per * nks;
+    if (nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
+    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, gc);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 
@@ -880,7 +947,8 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int uni
 int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
-int launch_gemv_rg(int ncols, int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
+int launch_gemv_rg(int ncols, int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);
+int launch_gemv_rg_multi(int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
 
 }  // namespace p8x

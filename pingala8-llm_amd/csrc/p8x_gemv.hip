@@ -168,6 +168,18 @@ GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
 
 
 static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
+                     float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int gpt, int task0);
+
+// the tensor's metadata as a GemvJob in device memory (activations, outputs and K plan unset), for launches that
+// pick their job at run time
+int upload_job(p8x_tensor *t) {
+    GemvJob g;
+    fill_job(g, t, nullptr, nullptr, nullptr, 0, nullptr, 0, nullptr, 1, t->nb, 1, 0);
+    if (hipMalloc((void **)&t->djob, sizeof(GemvJob)) != hipSuccess) return set_error(P8X_ERR_NOMEM, "p8x_prepare: hipMalloc job");
+    return hip_check(hipMemcpy(t->djob, &g, sizeof g, hipMemcpyHostToDevice), "p8x_prepare: job");
+}
+
+static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float *d, const float *x, size_t ldx,
                      float *y, size_t ldy, int32_t *partials, int nks, int kchunk, int gpt, int task0) {
     g = GemvJob{};
     g.M = t->M; g.S = t->Sg; g.D = t->D; g.prm = t->prm; g.prmd = t->prmd;
@@ -208,9 +220,10 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
         int kc;
         const int nks = rg_plan(t, ncols, &kc);
         if (nks == 1 || (size_t)nks * ncols * t->rows <= t->wpart_floats) {
-            GemvJob job0;
-            fill_job(job0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, nks, kc, 1, 0);
-            return launch_gemv_rg(ncols, cm, job0, t->ng, t->a2, st);
+            RgJobs R{};
+            fill_job(R.j0, t, nullptr, nullptr, x, ldx, y, ldy, nullptr, nks, kc, 1, 0);
+            R.njobs = 1;
+            return launch_gemv_rg(ncols, cm, R, t->ng, t->a2, st);
         }
     }
     const GemvPlan p = gemv_plan(t, ncols, act, false);
@@ -219,6 +232,49 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
     fill_job(job0, t, q, d, x, ldx, y, ldy, nullptr, p.nks, p.bpk, p.gpt, 0);
     if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, job0, job0.ntasks, t->a2, st);
     return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
+}
+
+// Several linears on the same activations in one row-group launch (out == nullptr), or a gate / up pair with the
+// swiglu epilogue (out != nullptr: n == 2, tensors[0] = gate). Shapes, codebook and rotation are checked by the caller.
+int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
+                      hipStream_t st) {
+    size_t hist[8] = {0};
+    int ng = 0;
+    for (int i = 0; i < n; ++i) {
+        for (int c = 0; c < 8; ++c) hist[c] += ts[i]->class_tiles[c];
+        ng += ts[i]->ng;
+    }
+    const int cm = class_set(hist);
+    // the K plan of the combined row groups: K-chunks that fit the LDS buffer, split in two when they fill at most
+    // half the CUs and K is long (the single-call rule)
+    const p8x_tensor *t0 = ts[0];
+    int nks = (t0->nb + kRgMaxBlocks - 1) / kRgMaxBlocks;
+    if (nks == 1 && 2 * ng <= num_cus() && t0->nb >= 32) nks = 2;
+    const int kc = (t0->nb + nks - 1) / nks;
+    nks = (t0->nb + kc - 1) / kc;
+    RgJobs R{};
+    R.njobs = n;
+    fill_job(R.j0, t0, nullptr, nullptr, x, ldx, out ? nullptr : y[0], out ? 0 : ldy[0], nullptr, nks, kc, 1, 0);
+    // workgroups per job: ceil(its row groups / per) per K-chunk, with per = ceil(all row groups / CUs)
+    const int per = (ng + num_cus() - 1) / num_cus();
+    for (int i = 0; i <= kRgMaxJobs; ++i) R.wgbase[i] = 0x7FFFFFFF;
+    R.wgbase[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        if (nks > 1 && (size_t)nks * ts[i]->rows > ts[i]->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "multi GEMV: partial workspace too small");
+        R.jt[i] = (kptr<const GemvJob>)ts[i]->djob;
+        R.y[i] = out ? nullptr : y[i];
+        R.ldy[i] = out ? 0u : (unsigned)ldy[i];
+        R.wgbase[i + 1] = R.wgbase[i] + (ts[i]->ng + per - 1) / per * nks;
+    }
+    for (int i = n; i < kRgMaxJobs; ++i) R.jt[i] = (kptr<const GemvJob>)ts[0]->djob;   // never selected
+    R.wgbase[kRgMaxJobs] = R.wgbase[n];   // the total
+    if (out) {
+        R.glu = 1;
+        R.glu_out = out;
+        R.glu_pair = t0->wglu;
+        R.glu_cnt = t0->wglu_cnt;
+    }
+    return launch_gemv_rg_multi(cm, R, ng, t0->a2, st);
 }
 
 // ------------------------------------------------------------------------------------------------ grouped launches
@@ -557,6 +613,38 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
+}
+
+static int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what) {
+    for (int i = 0; i < n; ++i) {
+        if (!ts[i]) return set_error(P8X_ERR_ARG, "%s: tensor %d is null", what, i);
+        if (ts[i]->K != ts[0]->K) return set_error(P8X_ERR_ARG, "%s: tensor %d has K %d, tensor 0 has %d", what, i, ts[i]->K, ts[0]->K);
+        if (memcmp(ts[i]->a2_host, ts[0]->a2_host, sizeof ts[0]->a2_host))
+            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d has a different codebook", what, i);
+        if (ts[i]->ic_hash != ts[0]->ic_hash)
+            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d rotates its input differently (column scales c or signs); call it alone", what, i);
+    }
+    if (!x || ldx < (size_t)ts[0]->K || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "%s: x null or ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", what, ldx);
+    return P8X_OK;
+}
+
+int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, void *stream) {
+    if (!tensors || !y || !ldy || n < 1 || n > kRgMaxJobs) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi: bad arguments (1..%d tensors)", kRgMaxJobs);
+    int rc;
+    if ((rc = check_shared_input(tensors, n, x, ldx, "p8x_mul_mat_vec_multi"))) return rc;
+    for (int i = 0; i < n; ++i)
+        if (!y[i] || ldy[i] < (size_t)tensors[i]->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi: y %d null or short", i);
+    return launch_gemv_multi(tensors, n, x, ldx, y, ldy, nullptr, (hipStream_t)stream);
+}
+
+int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream) {
+    const p8x_tensor *ts[2] = {gate, up};
+    if (!gate || !up || !out) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_glu: null pointer");
+    int rc;
+    if ((rc = check_shared_input(ts, 2, x, ldx, "p8x_mul_mat_vec_glu"))) return rc;
+    if (gate->rows != up->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_glu: gate has %d rows, up %d", gate->rows, up->rows);
+    return launch_gemv_multi(ts, 2, x, ldx, nullptr, nullptr, out, (hipStream_t)stream);
 }
 
 int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out) {

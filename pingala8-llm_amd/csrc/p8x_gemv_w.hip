@@ -15,15 +15,15 @@ int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujo
     return launch_gemv_wave_t<kCmAll, 1>(jobs, ujob, units, ctr, a2, st);
 }
 
-int launch_gemv_rg_mc(int ncols, int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st);
+int launch_gemv_rg_mc(int ncols, int cm, const RgJobs &job, int ng, const uint32_t *a2, hipStream_t st);
 
-int launch_gemv_rg(int ncols, int cm, const GemvJob &job, int ng, const uint32_t *a2, hipStream_t st) {
+int launch_gemv_rg(int ncols, int cm, const RgJobs &job, int ng, const uint32_t *a2, hipStream_t st) {
     if (ncols != 1) return launch_gemv_rg_mc(ncols, cm, job, ng, a2, st);
-    if (cm == kCmC3) return launch_gemv_rg_t<kCmC3, 1>(job, ng, a2, st);
-    if (cm == kCmC6) return launch_gemv_rg_t<kCmC6, 1>(job, ng, a2, st);
-    if (cm == kCmC234) return launch_gemv_rg_t<kCmC234, 1>(job, ng, a2, st);
-    if (cm == kCmC2346) return launch_gemv_rg_t<kCmC2346, 1>(job, ng, a2, st);
-    return launch_gemv_rg_t<kCmAll, 1>(job, ng, a2, st);
+    if (cm == kCmC3) return launch_gemv_rg_t<kCmC3, 1, false>(job, ng, a2, st);
+    if (cm == kCmC6) return launch_gemv_rg_t<kCmC6, 1, false>(job, ng, a2, st);
+    if (cm == kCmC234) return launch_gemv_rg_t<kCmC234, 1, false>(job, ng, a2, st);
+    if (cm == kCmC2346) return launch_gemv_rg_t<kCmC2346, 1, false>(job, ng, a2, st);
+    return launch_gemv_rg_t<kCmAll, 1, false>(job, ng, a2, st);
 }
 
 }  // namespace p8x

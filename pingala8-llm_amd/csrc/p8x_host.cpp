@@ -107,7 +107,7 @@ int p8x_probe(const void *slot, size_t n, int rows, int K) {
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->wy, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->wy, (void *)t->wglu, (void *)t->wglu_cnt, (void *)t->djob, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -191,6 +191,12 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     }
     std::vector<float> ic(K);
     for (int k = 0; k < K; ++k) ic[k] = (float)sg[k & 255] / half_to_float(c16[k]);
+    uint64_t ic_hash = 1469598103934665603ull;   // FNV-1a over the rotation's bytes (K included)
+    for (int k = 0; k < K; ++k) {
+        uint32_t b;
+        memcpy(&b, &ic[k], 4);
+        for (int i = 0; i < 4; ++i) ic_hash = (ic_hash ^ ((b >> (8 * i)) & 0xFFu)) * 1099511628211ull;
+    }
     std::vector<int> cp(rows + 1, 0);
     std::vector<uint16_t> cc(nd);
     std::vector<float> cv(nd);
@@ -205,6 +211,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->rows = rows; t->K = K; t->nb = nb; t->ng = ng; t->nsl = nsl; t->nd = nd;
     t->n = n; t->nt = nt; t->kbytes = kbytes;
     t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
+    t->ic_hash = ic_hash;
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
     memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
@@ -278,6 +285,9 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
     if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
     if ((rc = alloc((void **)&t->wy, 4 * (size_t)P8X_MAX_COLS * rows, "x16 plane rows"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wglu, 8 * (size_t)rows, "gate / up values"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wglu_cnt, 4 * (size_t)rows, "gate / up counters"))) return fail(rc);
+    if ((rc = hip_check(hipMemset(t->wglu_cnt, 0, 4 * (size_t)rows), "p8x_prepare: gate / up counters"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
     {
         std::vector<int16_t> pinv(rows);
@@ -308,6 +318,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         if ((rc = hip_check(hipMemcpy(t->cv, cv.data(), 4 * (size_t)nd, hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);
     }
     if ((rc = hip_check(hipMemset(t->wcnt, 0, 4 * (size_t)ng), "p8x_prepare: counters"))) return fail(rc);
+    if ((rc = upload_job(t))) return fail(rc);
     if ((rc = hip_check(hipDeviceSynchronize(), "p8x_prepare: sync"))) return fail(rc);
     *out = t;
     return P8X_OK;

@@ -9,6 +9,10 @@
 #include "../../include/p8x.h"
 #include "p8x_format.h"
 
+namespace p8x {
+struct GemvJob;
+}
+
 struct p8x_tensor {
     int rows = 0, K = 0, nb = 0, ng = 0, nsl = 0, nd = 0;
     size_t n = 0, nt = 0, kbytes = 0, stream_bytes = 0;
@@ -39,6 +43,10 @@ struct p8x_tensor {
     int32_t *wsum = nullptr;         // [P8X_MAX_COLS][nsl]
     uint8_t *wq81 = nullptr;         // block_q8_1 [P8X_MAX_COLS][K / 32]
     float *wy = nullptr;             // x16 products: plane rows [2 x 4][rows]
+    float *wglu = nullptr;           // gate / up meeting (this tensor as the gate): values [2][rows]
+    unsigned *wglu_cnt = nullptr;    // and arrival counters [rows], 0 between calls
+    uint64_t ic_hash = 0;            // hash of the rotation sg / c (tensors with equal hashes share quantized inputs)
+    p8x::GemvJob *djob = nullptr;    // the tensor's metadata as a device-side GEMV job (launches over several tensors)
     float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan
     size_t wpart_floats = 0;
     unsigned *wcnt = nullptr;        // split-K arrival counters [ng]
@@ -71,12 +79,16 @@ int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, 
 int launch_act_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh, int8_t *ql, float *dl,
                    int32_t *sl, int qstride, hipStream_t st);
 int launch_gemv_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, hipStream_t st);
+int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
+                      hipStream_t st);
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st);
 int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
 int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
 int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st);
 int reserve_mul_mat(const p8x_tensor *t, int n_max);
+// the tensor's GemvJob in device memory (t->djob), at prepare
+int upload_job(p8x_tensor *t);
 // device address of the no-allocation scratch array on `device` (hipGetSymbolAddress, once per device)
 int scratch_resolve(int device);
 

@@ -25,7 +25,7 @@ EXPORTS = [
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
-    "p8x_vr3_expand", "p8x_quantize_x16",
+    "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu",
 ]
 
 
@@ -75,6 +75,8 @@ def lib():
     L.p8x_quantize_q8_128.argtypes = [vp, vp, i, sz, vp, vp, vp, vp]
     L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
     L.p8x_quantize_x16.argtypes = [vp, vp, i, sz, vp, vp, vp, vp, vp, vp, vp]
+    L.p8x_mul_mat_vec_multi.argtypes = [vp, i, vp, sz, vp, vp, vp]
+    L.p8x_mul_mat_vec_glu.argtypes = [vp, vp, vp, sz, vp, vp]
     L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
@@ -499,6 +501,36 @@ class Tensor:
         self.mul_mat_dev(xd, dtype, N, y)
         synchronize()
         return y.to_numpy(np.float32, (N, self.rows))
+
+
+def mul_mat_vec_multi_dev(tensors, x, ys, stream=None):
+    """y_i = W_i x for tensors sharing K and input rotation, one launch (device buffers)"""
+    n = len(tensors)
+    T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
+    Y = (ctypes.c_void_p * n)(*[y.addr for y in ys])
+    LY = (ctypes.c_size_t * n)(*[t.rows for t in tensors])
+    check(lib().p8x_mul_mat_vec_multi(T, n, _vp(x), tensors[0].K, Y, LY, stream.h if stream else None), "p8x_mul_mat_vec_multi")
+
+
+def mul_mat_vec_multi(tensors, x):
+    xd = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
+    ys = [DeviceBuffer(4 * t.rows) for t in tensors]
+    mul_mat_vec_multi_dev(tensors, xd, ys)
+    synchronize()
+    return [y.to_numpy(np.float32, (t.rows,)) for y, t in zip(ys, tensors)]
+
+
+def mul_mat_vec_glu_dev(gate, up, x, out, stream=None):
+    check(lib().p8x_mul_mat_vec_glu(gate.h, up.h, _vp(x), gate.K, _vp(out), stream.h if stream else None), "p8x_mul_mat_vec_glu")
+
+
+def mul_mat_vec_glu(gate, up, x):
+    """silu(gate x) * (up x), one launch"""
+    xd = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
+    out = DeviceBuffer(4 * gate.rows)
+    mul_mat_vec_glu_dev(gate, up, xd, out)
+    synchronize()
+    return out.to_numpy(np.float32, (gate.rows,))
 
 
 class GemvBatch:

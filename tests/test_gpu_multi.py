@@ -1,0 +1,87 @@
+"""Several linears on one activation vector in one launch (p8x_mul_mat_vec_multi: q/k/v, gate/up) and the gated
+FFN input silu(gate x) * (up x) (p8x_mul_mat_vec_glu), against the fp64 oracle of each tensor on the same 8-bit
+activations (bar 1e-3 relative L2, asserted at 1e-5), and the rejections of tensors that cannot share an input."""
+import numpy as np
+import pytest
+
+import oracle as O
+import p8x
+import slotgen
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def shared_input(specs, seed):
+    """slots for [(rows, K, class_p, nd)] with tensor 0's column scales c and Hadamard signs copied into the others
+    (one input rotation, as a file encodes the linears that share an input)"""
+    slots = [p8x.synth_random(seed + i, r, K, class_p=cp, nd=nd) for i, (r, K, cp, nd) in enumerate(specs)]
+    r0, K0, _, nd0 = specs[0]
+    o0 = slotgen.offsets(slots[0].size, r0, K0, nd0)
+    c16, sg = slots[0][o0["C"]:o0["C"] + 2 * K0].copy(), slots[0][o0["SG"]:o0["SG"] + 256].copy()
+    for s, (r, K, _, nd) in zip(slots[1:], specs[1:]):
+        o = slotgen.offsets(s.size, r, K, nd)
+        s[o["C"]:o["C"] + 2 * K] = c16
+        s[o["SG"]:o["SG"] + 256] = sg
+    return slots
+
+
+C3 = (0, 0, 0, 1, 0, 0, 0, 0)
+MIX = (0, 0, 1, 6, 1, 0, 1, 0)
+
+
+@pytest.mark.parametrize("specs", [
+    [(4096, 4096, C3, 3), (1024, 4096, C3, 1), (1024, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 2)],   # Llama q / k / v
+    [(4096, 2560, C3, 2), (1024, 2560, C3, 0), (1024, 2560, C3, 4)],                         # Qwen3-4B q / k / v
+    [(512, 14336, MIX, 5), (256, 14336, MIX, 3)],                                           # long K: the K-split path
+    [(96, 1024, (1, 1, 1, 1, 1, 1, 1, 1), 2), (64, 1024, C3, 1), (32, 1024, C3, 0), (128, 1024, MIX, 3)],
+], ids=["llama_qkv", "qwen4b_qkv", "ksplit", "four_mixed"])
+def test_multi_matches_oracle(specs):
+    slots = shared_input(specs, 60)
+    ts = [p8x.Tensor(s, r, K) for s, (r, K, _, _) in zip(slots, specs)]
+    x = np.random.default_rng(61).standard_normal(specs[0][1]).astype(np.float32)
+    for rep in range(2):
+        ys = p8x.mul_mat_vec_multi(ts, x)
+        for i, (s, (r, K, _, _)) in enumerate(zip(slots, specs)):
+            assert rel_l2(ys[i], O.Oracle(s, r, K).gemv_f64(x)) < 1e-5, (rep, i)
+
+
+def silu_up(g, u):
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("rows,K,cp,nd", [(14336, 4096, C3, 6), (9728, 2560, C3, 3), (1024, 14336, MIX, 4), (96, 512, (1, 1, 1, 1, 1, 1, 1, 1), 2)],
+                         ids=["llama_ffn", "qwen4b_ffn", "ksplit", "small_mixed"])
+def test_glu_matches_oracle(rows, K, cp, nd):
+    slots = shared_input([(rows, K, cp, nd), (rows, K, cp, nd + 1)], 70)
+    gate, up = p8x.Tensor(slots[0], rows, K), p8x.Tensor(slots[1], rows, K)
+    x = np.random.default_rng(71).standard_normal(K).astype(np.float32)
+    ref = silu_up(O.Oracle(slots[0], rows, K).gemv_f64(x), O.Oracle(slots[1], rows, K).gemv_f64(x))
+    first = None
+    for rep in range(3):   # the per-row counters go back to 0: repeated calls agree bit for bit
+        out = p8x.mul_mat_vec_glu(gate, up, x)
+        assert rel_l2(out, ref) < 1e-5, rep
+        if first is None:
+            first = out
+        else:
+            assert np.array_equal(out.view(np.uint32), first.view(np.uint32)), rep
+
+
+def test_multi_and_glu_reject_unshared_inputs():
+    a, b = p8x.synth_random(80, 256, 1024), p8x.synth_random(81, 256, 1024)   # own c16 and signs each
+    ta, tb = p8x.Tensor(a, 256, 1024), p8x.Tensor(b, 256, 1024)
+    x = np.zeros(1024, np.float32)
+    with pytest.raises(p8x.P8xError, match="rotates its input differently"):
+        p8x.mul_mat_vec_multi([ta, tb], x)
+    with pytest.raises(p8x.P8xError, match="rotates its input differently"):
+        p8x.mul_mat_vec_glu(ta, tb, x)
+    tc = p8x.Tensor(p8x.synth_random(82, 256, 2048), 256, 2048)
+    with pytest.raises(p8x.P8xError, match="has K 2048"):
+        p8x.mul_mat_vec_multi([ta, tc], x)
+    s = shared_input([(256, 1024, C3, 0), (128, 1024, C3, 0)], 83)
+    with pytest.raises(p8x.P8xError, match="rows"):
+        p8x.mul_mat_vec_glu(p8x.Tensor(s[0], 256, 1024), p8x.Tensor(s[1], 128, 1024), x)
