@@ -46,22 +46,34 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# linears that read the same input share its rotation (one column scale c per input, one sign vector per model)
+SHARED_INPUT = [("attn_q", "attn_k", "attn_v"), ("attn_output",), ("ffn_gate", "ffn_up"), ("ffn_down",)]
+
+
 def build_stack(layers, mix, keep_host_layers):
     """the stack's tensors (device), their kinds, and the host slots of the first keep_host_layers layers (the CPU
     baseline's sample)"""
     tensors, kinds, host0 = [], [], []
     seed = 1
-    plan = [(f"blk.{l}.{k}", r, K) for l in range(layers) for (k, r, K) in LLAMA_LAYER] + \
-           [(f"output.{i}", r, K) for i, (_, r, K) in enumerate(HEAD_SHARDS)]
-    for name, rows, K in plan:
-        kind = name.split(".")[-1] if name.startswith("blk") else "lm_head"
-        cp = CLASS_B4.get(kind, CLASS_C3) if mix == "b4" else CLASS_C3
-        slot = p8x.synth_random(seed, rows, K, class_p=cp, nd=1)
-        seed += 1
-        tensors.append(p8x.Tensor(slot, rows, K))
-        kinds.append(kind)
-        if name.startswith("blk.") and int(name.split(".")[1]) < keep_host_layers:
-            host0.append((slot, rows, K))
+    signs = None
+    groups = [[(f"blk.{l}.{k}", r, K) for (k, r, K) in LLAMA_LAYER if k in grp] for l in range(layers) for grp in SHARED_INPUT]
+    groups.append([(f"output.{i}", r, K) for i, (_, r, K) in enumerate(HEAD_SHARDS)])
+    for grp in groups:
+        slots = []
+        for name, rows, K in grp:
+            kind = name.split(".")[-1] if name.startswith("blk") else "lm_head"
+            cp = CLASS_B4.get(kind, CLASS_C3) if mix == "b4" else CLASS_C3
+            slots.append(p8x.synth_random(seed, rows, K, class_p=cp, nd=1))
+            seed += 1
+        if signs is None:
+            o = p8x.side_offsets(slots[0].size, grp[0][1], grp[0][2], 1)
+            signs = slots[0][o["SG"]:o["SG"] + 256].copy()
+        p8x.share_input(slots, [(r, K) for _, r, K in grp], signs_from=signs)
+        for slot, (name, rows, K) in zip(slots, grp):
+            tensors.append(p8x.Tensor(slot, rows, K))
+            kinds.append(name.split(".")[-1] if name.startswith("blk") else "lm_head")
+            if name.startswith("blk.") and int(name.split(".")[1]) < keep_host_layers:
+                host0.append((slot, rows, K))
     return tensors, kinds, host0
 
 
@@ -294,54 +306,47 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps, 
 
 
 def measure_dependent_step(tensors, kinds, stream, steps):
-    """A batch-1 decode step that respects the data dependencies of the model: per layer, q/k/v as one grouped
-    launch on the layer input, o on q's output, gate/up as one grouped launch on o's output, down on gate's output
-    (the next layer's input); then the head shards as one grouped launch on the last down's output. Each product's
-    activations are its producer's outputs, so nothing overlaps across launches; captured once in a HIP graph and
-    replayed. (Values shrink from layer to layer without the model's norms; the products' work does not depend on
-    them.)"""
+    """A batch-1 decode step that respects the data dependencies of the model: per layer, q/k/v as one launch on the
+    layer input (p8x_mul_mat_vec_multi), o on q's output, the gated FFN input silu(gate x) * (up x) as one launch on
+    o's output (p8x_mul_mat_vec_glu), down on that (the next layer's input); then the head shards as one launch on
+    the last down's output. Each product's activations are its producer's outputs, so nothing overlaps across
+    launches; captured once in a HIP graph and replayed. (Values shrink from layer to layer without the model's
+    norms; the products' work does not depend on them.)"""
     nl = sum(1 for k in kinds if k == "attn_q")
     layer = [tensors[7 * l:7 * l + 7] for l in range(nl)]
     head = tensors[7 * nl:]
     rng = np.random.default_rng(9)
     x0 = p8x.DeviceBuffer.from_numpy(rng.standard_normal(layer[0][0].K).astype(np.float32))
-    bufs, batches, singles = [x0], [], []
+    bufs, plan = [x0], []
     cur = x0
     for q, k, v, o, gate, up, down in layer:
         yq, yk, yv = p8x.DeviceBuffer(4 * q.rows), p8x.DeviceBuffer(4 * k.rows), p8x.DeviceBuffer(4 * v.rows)
-        yo, yg, yu, yd = p8x.DeviceBuffer(4 * o.rows), p8x.DeviceBuffer(4 * gate.rows), p8x.DeviceBuffer(4 * up.rows), p8x.DeviceBuffer(4 * down.rows)
-        bufs += [yq, yk, yv, yo, yg, yu, yd]
-        qkv = p8x.GemvBatch([q, k, v], [cur, cur, cur], [yq, yk, yv])
-        gu = p8x.GemvBatch([gate, up], [yo, yo], [yg, yu])
-        batches += [qkv, gu]
-        singles.append((qkv, (o, yq, yo), gu, (down, yg, yd)))
+        yo, yg, yd = p8x.DeviceBuffer(4 * o.rows), p8x.DeviceBuffer(4 * gate.rows), p8x.DeviceBuffer(4 * down.rows)
+        bufs += [yq, yk, yv, yo, yg, yd]
+        plan.append(((q, k, v), cur, (yq, yk, yv), (o, yq, yo), (gate, up, yo, yg), (down, yg, yd)))
         cur = yd
     yh = [p8x.DeviceBuffer(4 * t.rows) for t in head]
     bufs += yh
-    hb = p8x.GemvBatch(head, [cur] * len(head), yh)
-    batches.append(hb)
 
     def enqueue(s):
-        for qkv, (o, xo, yo), gu, (down, xd, yd) in singles:
-            qkv.run(s)
+        for qkv, xin, yqkv, (o, xo, yo), (gate, up, xg, yg), (down, xd, yd) in plan:
+            p8x.mul_mat_vec_multi_dev(list(qkv), xin, list(yqkv), stream=s)
             o.mul_mat_vec_dev(xo, yo, stream=s)
-            gu.run(s)
+            p8x.mul_mat_vec_glu_dev(gate, up, xg, yg, stream=s)
             down.mul_mat_vec_dev(xd, yd, stream=s)
-        hb.run(s)
+        p8x.mul_mat_vec_multi_dev(head, cur, yh, stream=s)
 
     eager_ms = timed_steps(lambda: enqueue(stream), stream, 3, steps)
     graph = p8x.Graph(enqueue, stream)
     g_ms = timed_steps(lambda: graph.launch(stream), stream, 3, steps)
     graph.release()
     step_bytes = sum(t.stream_bytes for t in tensors)
-    launches = nl * (3 + 1 + 3 + 1) + 3
+    launches = 4 * nl + 1
     log(f"dependent step: eager {eager_ms * 1e3:.0f} us, graph {g_ms * 1e3:.0f} us ({launches} launches)")
-    for b in batches:
-        b.release()
     for b in bufs:
         b.free()
-    return {"workload": f"{nl} layers: grouped q/k/v -> o -> grouped gate/up -> down, then the head shards grouped; "
-                        "each launch reads its producer's output", "launches": launches,
+    return {"workload": f"{nl} layers: q/k/v in one launch -> o -> silu(gate) * up in one launch -> down, then the head "
+                        "shards in one launch; each launch reads its producer's output", "launches": launches,
             "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)},
             "eager": {"ms_per_step": round(eager_ms, 4), "GB/s": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)}}
 

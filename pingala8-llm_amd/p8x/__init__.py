@@ -295,6 +295,38 @@ def quantize_tensor(W, c16=None, sign_seed=0):
     return buf[:n.value].copy()
 
 
+def side_offsets(n, rows, K, nd):
+    """byte offsets of the side regions of an n-byte slot, top-down from its end (delta, c16, prm, pinv, signs,
+    trailer), as the tensor contract lays them out"""
+    t = n - 32
+    sg = t - 256
+    q = (sg - 2 * rows) & ~15
+    p = (q - 2 * rows) & ~15
+    c = (p - 2 * K) & ~15
+    e = (c - 8 * nd) & ~15
+    return {"E": e, "C": c, "P": p, "Q": q, "SG": sg, "T": t}
+
+
+def slot_nd(slot):
+    """clamp-delta entry count from a slot's trailer"""
+    return int(np.frombuffer(np.ascontiguousarray(slot[-32:]).tobytes(), np.uint32)[3])
+
+
+def share_input(slots, shapes, signs_from=None):
+    """Give host slots [(rows, K)] one input rotation in place: the column scales c and Hadamard signs of slots[0]
+    (or the signs of signs_from) copied into the others, as a file encodes linears that share an input (one c per
+    input, one sign vector for the model). The slots must have equal K."""
+    r0, K0 = shapes[0]
+    o0 = side_offsets(slots[0].size, r0, K0, slot_nd(slots[0]))
+    c16 = slots[0][o0["C"]:o0["C"] + 2 * K0].copy()
+    sg = (signs_from if signs_from is not None else slots[0][o0["SG"]:o0["SG"] + 256]).copy()
+    for s, (r, K) in zip(slots, shapes):
+        assert K == K0
+        o = side_offsets(s.size, r, K, slot_nd(s))
+        s[o["C"]:o["C"] + 2 * K] = c16
+        s[o["SG"]:o["SG"] + 256] = sg
+
+
 # --------------------------------------------------------------------------------------------------- model files
 class VrFile:
     """A native Pingala-8 model file (GGUF; one path, or the shards of one model)."""
