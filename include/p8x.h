@@ -90,6 +90,13 @@ int p8x_dequantize(const p8x_tensor *t, int dtype, void *out, size_t ld, void *s
  * P8X_F32 = int * S (vr_wint * vr_wscale, CPU.patch:4030-4071). out is [rows][ld]. */
 int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream);
 
+/* The same on part of a tensor (the reference's per-tile and per-row-group core functions): p8x_decode_tiles = the
+ * tiles of row groups g0 .. g0 + ng - 1 and blocks b0 .. b0 + nb - 1 (vrc_decode_tile_int for one tile,
+ * CPU.patch:992-1010), out [32 ng][ld >= 256 nb] relative to the window; p8x_dequantize_rows = ORIGINAL rows
+ * row0 .. row0 + nrows - 1 of dequantize_row, out [nrows][ld >= K], the same bits as the whole-tensor call. */
+int p8x_decode_tiles(const p8x_tensor *t, int dtype, int g0, int ng, int b0, int nb, void *out, size_t ld, void *stream);
+int p8x_dequantize_rows(const p8x_tensor *t, int dtype, int row0, int nrows, void *out, size_t ld, void *stream);
+
 /* ---- activations ------------------------------------------------------------------------------------ */
 /* x' = FWHT256(x * sg / c) / 16, 8-bit per 128-column half-slice: q [ncols][K] int8, d [ncols][K/128]
  * (d = amax/127), sum [ncols][K/128] (sum of q; may be NULL). Bit-exact to vrc_prep_block / k_vr_qx_real. */
@@ -114,6 +121,11 @@ int p8x_quantize_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx
  * Q8_128 or [ncols][rows][K/32] for Q8_1, the exact integer dot of each row with each quantization block. */
 int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, void *stream);
+/* p8x_vec_dot on the sorted row groups g0 .. g0 + ng - 1 (vrc_tile's per-tile products summed over K, CPU.patch:617-
+ * 668; the reference's CPU GEMV hands such row groups to its threads): y is written at those groups' ORIGINAL rows
+ * only (same values as the whole-tensor call), partials are [ncols][32 ng][blocks] for those sorted rows. */
+int p8x_vec_dot_rows(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, int g0, int ng, const float *x, size_t ldx,
+                     float *y, size_t ldy, int32_t *partials, void *stream);
 /* y = W x for 1..8 columns (vr_mul_mat_vec, CPU.patch:4466-4521): activation prep + fused decode-GEMV +
  * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. One launch for one column
  * (and two columns of short K), deterministic. The K-chunk partial rows and arrival counters live in the

@@ -23,12 +23,16 @@ constexpr int kStgRowWords = 132;   // dequant staging row: 512 bytes + 16 bytes
 // raw words held per lane: the largest class of the instantiation's class set
 __host__ __device__ constexpr int dec_nw(int cm) { return cm == (1 << 3) ? 8 : 24; }
 
+// The tiles walked are the window of row groups g0 .. g0 + gn - 1 and blocks b0 .. b0 + bn - 1 (nt = gn bn). Rotated
+// outputs are relative to the window (row 32 (g - g0) + j, column 256 (b - b0) + ...); original-domain outputs keep
+// the rows row0 .. row0 + nrows - 1 (original indices) at out row ro - row0 and skip the others.
 struct DecodeArgs {
     const uint32_t *M; const uint16_t *S; const uint32_t *D; const uint32_t *a2; const int16_t *prm;
     const uint16_t *prmd;   // prm with bit 15 set on rows that carry clamp-delta entries
     const float *ic; const int *cp; const uint16_t *cc; const float *cv;
     void *out; size_t ld;
     int rows, K, nb, ng;
+    int g0, gn, b0, bn, row0, nrows;
     size_t nt;
 };
 
@@ -121,8 +125,8 @@ struct TileNext {
 };
 
 __device__ __forceinline__ void tile_of(const DecodeArgs &a, size_t q, int &g, int &b) {
-    b = (int)(q / a.ng);
-    g = (int)(q % a.ng);
+    b = a.b0 + (int)(q / a.gn);
+    g = a.g0 + (int)(q % a.gn);
 }
 
 template <int CM, typename Body>
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
     walk_tiles<CM>(a, first + w, last, kDecWaves, hs, j, false, [&](int g, int b, int c, const AnySlice<NW> &ls, int, int, int) {
         float v[128];
         lane_values_any<DT == P8X_F32, CM>(c, ls, tab, bankbytes, half_to_float(ls.s), v);
-        const size_t o = (size_t)(32 * g + j) * a.ld + 256 * b + 128 * hs;
+        const size_t o = (size_t)(32 * (g - a.g0) + j) * a.ld + 256 * (b - a.b0) + 128 * hs;
         if constexpr (DT == P8X_I16) {
             uint2 *dst = reinterpret_cast<uint2 *>((int16_t *)a.out + o);
 #pragma unroll
@@ -250,9 +254,11 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
             for (int i = 0; i < 16; ++i) {
                 const int row = 2 * i + (lane >> 5), ch = lane & 31;
                 const uint4 val = *reinterpret_cast<const uint4 *>(sw + row * kStgRowWords + 4 * ch);
-                const int rro = __shfl(ro, row);
-                if constexpr (DT == P8X_F32) *reinterpret_cast<uint4 *>((float *)a.out + (size_t)rro * a.ld + col0 + 4 * ch) = val;
-                else *reinterpret_cast<uint4 *>((uint16_t *)a.out + (size_t)rro * a.ld + col0 + 8 * ch) = val;
+                const int orow = __shfl(ro, row) - a.row0;   // output row; rows outside the range are skipped
+                if ((unsigned)orow < (unsigned)a.nrows) {
+                    if constexpr (DT == P8X_F32) *reinterpret_cast<uint4 *>((float *)a.out + (size_t)orow * a.ld + col0 + 4 * ch) = val;
+                    else *reinterpret_cast<uint4 *>((uint16_t *)a.out + (size_t)orow * a.ld + col0 + 8 * ch) = val;
+                }
                 if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // 4 stores at a time: bounds the live registers
             }
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the buffer is written again
@@ -296,12 +302,13 @@ static DecodeArgs decode_args(const p8x_tensor *t, void *out, size_t ld) {
     a.ic = t->ic; a.cp = t->cp; a.cc = t->cc; a.cv = t->cv;
     a.out = out; a.ld = ld;
     a.rows = t->rows; a.K = t->K; a.nb = t->nb; a.ng = t->ng; a.nt = t->nt;
+    a.g0 = 0; a.gn = t->ng; a.b0 = 0; a.bn = t->nb; a.row0 = 0; a.nrows = t->rows;
     return a;
 }
 
 // two 4-wave workgroups per CU (the 64 KB table each), persistent
-static int decode_grid(const p8x_tensor *t) {
-    const size_t wgs = (t->nt + kDecWaves - 1) / kDecWaves;
+static int decode_grid(const DecodeArgs &a) {
+    const size_t wgs = (a.nt + kDecWaves - 1) / kDecWaves;
     return (int)std::min<size_t>(wgs, (size_t)num_cus() * 2);
 }
 
@@ -312,28 +319,39 @@ static bool only_class3(const p8x_tensor *t) {
 
 template <int CM>
 static void launch_rot(const p8x_tensor *t, int dtype, const DecodeArgs &a, hipStream_t st) {
-    if (dtype == P8X_I16) hipLaunchKernelGGL((k_decode_rotated<P8X_I16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else hipLaunchKernelGGL((k_decode_rotated<P8X_F32, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    if (dtype == P8X_I16) hipLaunchKernelGGL((k_decode_rotated<P8X_I16, CM>), dim3(decode_grid(a)), dim3(kDecThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_decode_rotated<P8X_F32, CM>), dim3(decode_grid(a)), dim3(kDecThreads), 0, st, a);
 }
 
 template <int CM>
 static void launch_deq(const p8x_tensor *t, int dtype, const DecodeArgs &a, hipStream_t st) {
-    if (dtype == P8X_F32) hipLaunchKernelGGL((k_dequant<P8X_F32, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else if (dtype == P8X_F16) hipLaunchKernelGGL((k_dequant<P8X_F16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
-    else hipLaunchKernelGGL((k_dequant<P8X_BF16, CM>), dim3(decode_grid(t)), dim3(kDecThreads), 0, st, a);
+    if (dtype == P8X_F32) hipLaunchKernelGGL((k_dequant<P8X_F32, CM>), dim3(decode_grid(a)), dim3(kDecThreads), 0, st, a);
+    else if (dtype == P8X_F16) hipLaunchKernelGGL((k_dequant<P8X_F16, CM>), dim3(decode_grid(a)), dim3(kDecThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_dequant<P8X_BF16, CM>), dim3(decode_grid(a)), dim3(kDecThreads), 0, st, a);
 }
 
-int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st) {
+int launch_decode_rotated(const p8x_tensor *t, int dtype, int g0, int gn, int b0, int bn, void *out, size_t ld, hipStream_t st) {
     if (ld % 4) return set_error(P8X_ERR_ARG, "decode: ld %zu must be a multiple of 4", ld);
-    const DecodeArgs a = decode_args(t, out, ld);
+    DecodeArgs a = decode_args(t, out, ld);
+    a.g0 = g0; a.gn = gn; a.b0 = b0; a.bn = bn; a.nt = (size_t)gn * bn;
     if (only_class3(t)) launch_rot<(1 << 3)>(t, dtype, a, st);
     else launch_rot<0xFE>(t, dtype, a, st);
     return hip_check(hipGetLastError(), "k_decode_rotated launch");
 }
 
-int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st) {
+int launch_dequant(const p8x_tensor *t, int dtype, int row0, int nrows, void *out, size_t ld, hipStream_t st) {
     if (ld % 4) return set_error(P8X_ERR_ARG, "dequantize: ld %zu must be a multiple of 4", ld);
-    const DecodeArgs a = decode_args(t, out, ld);
+    DecodeArgs a = decode_args(t, out, ld);
+    a.row0 = row0; a.nrows = nrows;
+    if (row0 != 0 || nrows != t->rows) {   // the row groups holding those original rows (their sorted rows' groups)
+        int lo = t->ng, hi = -1;
+        for (int ro = row0; ro < row0 + nrows; ++ro) {
+            const int g = t->pinv_host[ro] / 32;
+            lo = std::min(lo, g);
+            hi = std::max(hi, g);
+        }
+        a.g0 = lo; a.gn = hi - lo + 1; a.nt = (size_t)a.gn * a.bn;
+    }
     if (only_class3(t)) launch_deq<(1 << 3)>(t, dtype, a, st);
     else launch_deq<0xFE>(t, dtype, a, st);
     return hip_check(hipGetLastError(), "k_dequant launch");

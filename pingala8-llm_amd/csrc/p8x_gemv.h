@@ -45,6 +45,7 @@ struct GemvJob {
     int rows, K, nb, ng, nsl;
     int kchunk, nks, task0, ntasks;
     unsigned dbytes;                 // payload region bytes (D .. end of the slot's payload)
+    int g0, gend, prows;             // task kernel: row groups g0 .. gend - 1; partials rows (32 g0 ..) with row stride prows
 };
 
 // LDS activation bytes per task: ncol x kchunk x 512. The step-order kernels keep each 128-column half of a
@@ -144,9 +145,9 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const SM 
             if constexpr (NST > 1) isum += acc[1][n][u] * (1 << SH2);
             if constexpr (NST > 2) isum += acc[2][n][u];
             if constexpr (PARTIALS) {
-                const int r = 32 * c.g + c.j;
-                if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(c.J->partials)[((size_t)n * c.J->rows + r) * c.J->nsl + 2 * b + c.hs] = isum;
-                else as_global_rw(c.J->partials)[((size_t)n * c.J->rows + r) * (c.J->K / 32) + 8 * b + 4 * c.hs + u] = isum;
+                const int r = 32 * (c.g - c.J->g0) + c.j;
+                if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(c.J->partials)[((size_t)n * c.J->prows + r) * c.J->nsl + 2 * b + c.hs] = isum;
+                else as_global_rw(c.J->partials)[((size_t)n * c.J->prows + r) * (c.J->K / 32) + 8 * b + 4 * c.hs + u] = isum;
             }
             const float dsc = ACT == P8X_ACT_Q8_128 ? sm.xd[n * NSC + 2 * bl + c.hs] : sm.xd[n * NSC + 8 * bl + 4 * c.hs + u];
             yacc[n] += ((float)isum * dsc) * sc;
@@ -409,7 +410,7 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
         const int local = task - J.task0, oct = local / J.nks, ks = local % J.nks;
         c.b0 = ks * J.kchunk;
         c.nbl = min(J.kchunk, J.nb - c.b0);
-        c.g = WAVES * oct + w;
+        c.g = J.g0 + WAVES * oct + w;
         // stage this task's activations and scales
         __syncthreads();
         bool scales_staged = false;
@@ -455,7 +456,7 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
             }
         }
         __syncthreads();
-        if (c.g >= J.ng) continue;
+        if (c.g >= J.gend) continue;
         float yacc[NCOL];
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
@@ -473,10 +474,10 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
                 case 7: if constexpr ((CM >> 7) & 1) { b = gemv_run<NCOL, ACT, PARTIALS, 7, gemv_nbuf(NCOL, 7), CM == (1 << 7)>(c, sm, b, bend, yacc); break; } [[fallthrough]];
                 default:
                     if constexpr (PARTIALS) {   // class 0: zero weights
-                        const int r = 32 * c.g + c.j;
+                        const int r = 32 * (c.g - J.g0) + c.j;
                         for (int n = 0; n < NCOL; ++n) {
-                            if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(J.partials)[((size_t)n * J.rows + r) * J.nsl + 2 * b + c.hs] = 0;
-                            else for (int u = 0; u < 4; ++u) as_global_rw(J.partials)[((size_t)n * J.rows + r) * (J.K / 32) + 8 * b + 4 * c.hs + u] = 0;
+                            if constexpr (ACT == P8X_ACT_Q8_128) as_global_rw(J.partials)[((size_t)n * J.prows + r) * J.nsl + 2 * b + c.hs] = 0;
+                            else for (int u = 0; u < 4; ++u) as_global_rw(J.partials)[((size_t)n * J.prows + r) * (J.K / 32) + 8 * b + 4 * c.hs + u] = 0;
                         }
                     }
                     ++b;

@@ -190,16 +190,21 @@ static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float
     g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + gpt - 1) / gpt) * nks;
     g.dbytes = (unsigned)(t->kbytes - offset_D(t->nt));
     g.ic = t->ic;
+    g.g0 = 0; g.gend = t->ng; g.prows = t->rows;
 }
 
-int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
-                float *y, size_t ldy, int32_t *partials, hipStream_t st) {
+// vec_dot over the row groups g0 .. g0 + ng - 1 with the whole tensor's plan (so the rows' results equal the whole
+// call's): y at those groups' original rows, partials [ncols][32 ng][blocks]
+int launch_gemv_range(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
+                      float *y, size_t ldy, int32_t *partials, int g0, int ng, hipStream_t st) {
     const int cm = class_set(t->class_tiles);
     if (partials) {   // integer partials: one column per launch
         const GemvPlan p1 = gemv_plan(t, 1, act, true);
         if (p1.nks > 1 && (size_t)p1.nks * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
         GemvJob job0;
         fill_job(job0, t, q, d, x, ldx, y, ldy, partials, p1.nks, p1.bpk, p1.gpt, 0);
+        job0.g0 = g0; job0.gend = g0 + ng; job0.prows = 32 * ng;
+        job0.ntasks = ((ng + p1.gpt - 1) / p1.gpt) * p1.nks;
         for (int n = 0; n < ncols; ++n) {
             GemvJob jn = job0;
             const size_t qcol = act == P8X_ACT_Q8_128 ? (size_t)t->K : (size_t)36 * (t->K / 32);
@@ -207,12 +212,26 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
             if (d) jn.d = d + (size_t)n * t->nsl;
             if (x) jn.x = x + (size_t)n * ldx;
             jn.y = y + (size_t)n * ldy;
-            jn.partials = partials + (size_t)n * t->rows * (act == P8X_ACT_Q8_128 ? t->nsl : t->K / 32);
+            jn.partials = partials + (size_t)n * 32 * ng * (act == P8X_ACT_Q8_128 ? t->nsl : t->K / 32);
             const int rc = launch_gemv_partials(act, jn, t->a2, st);
             if (rc) return rc;
         }
         return P8X_OK;
     }
+    const GemvPlan p = gemv_plan(t, ncols, act, false);
+    if (p.nks > 1 && (size_t)p.nks * ncols * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
+    GemvJob job0;
+    fill_job(job0, t, q, d, x, ldx, y, ldy, nullptr, p.nks, p.bpk, p.gpt, 0);
+    job0.g0 = g0; job0.gend = g0 + ng;
+    job0.ntasks = ((ng + p.gpt - 1) / p.gpt) * p.nks;
+    if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, job0, job0.ntasks, t->a2, st);
+    return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
+}
+
+int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
+                float *y, size_t ldy, int32_t *partials, hipStream_t st) {
+    const int cm = class_set(t->class_tiles);
+    if (partials) return launch_gemv_range(t, act, q, d, ncols, x, ldx, y, ldy, partials, 0, t->ng, st);
     // the row-group kernel: one column, or two columns of a one-class tensor with K <= 8192 (measured faster
     // than the multi-column task kernel there, slower for longer K and more columns)
     if (act == P8X_ACT_Q8_128 && !q && (ncols == 1 || (ncols == 2 && t->nb <= 32 && (cm == kCmC3 || cm == kCmC6)))) {

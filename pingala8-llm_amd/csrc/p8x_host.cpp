@@ -294,6 +294,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         bool ident = true;
         for (int r = 0; r < rows; ++r) { pinv[prm[r]] = (int16_t)r; ident = ident && prm[r] == r; }
         t->prm_identity = ident;
+        t->pinv_host = pinv;
         if ((rc = alloc((void **)&t->pinv, 2 * (size_t)rows, "pinv"))) return fail(rc);
         if ((rc = hip_check(hipMemcpy(t->pinv, pinv.data(), 2 * (size_t)rows, hipMemcpyHostToDevice), "p8x_prepare: pinv"))) return fail(rc);
     }
@@ -338,14 +339,31 @@ int p8x_dequantize(const p8x_tensor *t, int dtype, void *out, size_t ld, void *s
     if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_dequantize: null pointer");
     if (dtype != P8X_F32 && dtype != P8X_F16 && dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_dequantize: dtype %d", dtype);
     if (ld < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_dequantize: ld %zu < K %d", ld, t->K);
-    return launch_dequant(t, dtype, out, ld, (hipStream_t)stream);
+    return launch_dequant(t, dtype, 0, t->rows, out, ld, (hipStream_t)stream);
+}
+
+int p8x_dequantize_rows(const p8x_tensor *t, int dtype, int row0, int nrows, void *out, size_t ld, void *stream) {
+    if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_dequantize_rows: null pointer");
+    if (dtype != P8X_F32 && dtype != P8X_F16 && dtype != P8X_BF16) return set_error(P8X_ERR_ARG, "p8x_dequantize_rows: dtype %d", dtype);
+    if (row0 < 0 || nrows < 1 || row0 + nrows > t->rows) return set_error(P8X_ERR_ARG, "p8x_dequantize_rows: rows %d + %d of %d", row0, nrows, t->rows);
+    if (ld < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_dequantize_rows: ld %zu < K %d", ld, t->K);
+    return launch_dequant(t, dtype, row0, nrows, out, ld, (hipStream_t)stream);
 }
 
 int p8x_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, void *stream) {
     if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: null pointer");
     if (dtype != P8X_I16 && dtype != P8X_F32) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: dtype %d", dtype);
     if (ld < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_decode_rotated: ld %zu < K %d", ld, t->K);
-    return launch_decode_rotated(t, dtype, out, ld, (hipStream_t)stream);
+    return launch_decode_rotated(t, dtype, 0, t->ng, 0, t->nb, out, ld, (hipStream_t)stream);
+}
+
+int p8x_decode_tiles(const p8x_tensor *t, int dtype, int g0, int ng, int b0, int nb, void *out, size_t ld, void *stream) {
+    if (!t || !out) return set_error(P8X_ERR_ARG, "p8x_decode_tiles: null pointer");
+    if (dtype != P8X_I16 && dtype != P8X_F32) return set_error(P8X_ERR_ARG, "p8x_decode_tiles: dtype %d", dtype);
+    if (g0 < 0 || ng < 1 || g0 + ng > t->ng || b0 < 0 || nb < 1 || b0 + nb > t->nb)
+        return set_error(P8X_ERR_ARG, "p8x_decode_tiles: tiles [%d, +%d) x [%d, +%d) of %d x %d", g0, ng, b0, nb, t->ng, t->nb);
+    if (ld < (size_t)256 * nb) return set_error(P8X_ERR_ARG, "p8x_decode_tiles: ld %zu < %d", ld, 256 * nb);
+    return launch_decode_rotated(t, dtype, g0, ng, b0, nb, out, ld, (hipStream_t)stream);
 }
 
 int p8x_quantize_q8_128(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *q, float *d, int32_t *sum, void *stream) {
@@ -378,6 +396,17 @@ int p8x_vec_dot(const p8x_tensor *t, int act, const void *q, const float *d, int
     if (ncols < 1 || ncols > P8X_MAX_COLS || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_vec_dot: ncols %d ldy %zu", ncols, ldy);
     if (x && ldx < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_vec_dot: ldx %zu < K %d", ldx, t->K);
     return launch_gemv(t, act, q, d, ncols, x, ldx, y, ldy, partials, (hipStream_t)stream);
+}
+
+int p8x_vec_dot_rows(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, int g0, int ng, const float *x, size_t ldx,
+                     float *y, size_t ldy, int32_t *partials, void *stream) {
+    if (!t || !q || !y) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: null pointer");
+    if (act != P8X_ACT_Q8_128 && act != P8X_ACT_Q8_1) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: act %d", act);
+    if (act == P8X_ACT_Q8_128 && !d) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: Q8_128 needs d");
+    if (ncols < 1 || ncols > P8X_MAX_COLS || ldy < (size_t)t->rows) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: ncols %d ldy %zu", ncols, ldy);
+    if (g0 < 0 || ng < 1 || g0 + ng > t->ng) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: row groups [%d, +%d) of %d", g0, ng, t->ng);
+    if (x && ldx < (size_t)t->K) return set_error(P8X_ERR_ARG, "p8x_vec_dot_rows: ldx %zu < K %d", ldx, t->K);
+    return launch_gemv_range(t, act, q, d, ncols, x, ldx, y, ldy, partials, g0, ng, (hipStream_t)stream);
 }
 
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream) {

@@ -29,6 +29,7 @@ struct p8x_tensor {
     const int16_t *prm = nullptr;
     uint16_t *Sg = nullptr;          // row scales regrouped [ng][nb][32]: a row group's scales in one run
     int16_t *pinv = nullptr;         // original row -> sorted row (built at prepare)
+    std::vector<int16_t> pinv_host;  // the same on the host (row-range requests find their row groups)
     uint16_t *prmd = nullptr;        // sorted row -> original row, bit 15 set when that row carries clamp-delta entries
     bool prm_identity = false;
     // device metadata built at prepare
@@ -83,8 +84,12 @@ int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t
                       hipStream_t st);
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st);
-int launch_decode_rotated(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
-int launch_dequant(const p8x_tensor *t, int dtype, void *out, size_t ld, hipStream_t st);
+int launch_gemv_range(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
+                      float *y, size_t ldy, int32_t *partials, int g0, int ng, hipStream_t st);
+// window of row groups g0 .. g0 + gn - 1 and blocks b0 .. b0 + bn - 1; out relative to it
+int launch_decode_rotated(const p8x_tensor *t, int dtype, int g0, int gn, int b0, int bn, void *out, size_t ld, hipStream_t st);
+// original rows row0 .. row0 + nrows - 1 to out rows 0 .. nrows - 1
+int launch_dequant(const p8x_tensor *t, int dtype, int row0, int nrows, void *out, size_t ld, hipStream_t st);
 int launch_mul_mat(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, hipStream_t st);
 int reserve_mul_mat(const p8x_tensor *t, int n_max);
 // the tensor's GemvJob in device memory (t->djob), at prepare

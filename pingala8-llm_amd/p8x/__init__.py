@@ -25,7 +25,8 @@ EXPORTS = [
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
-    "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu",
+    "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_decode_tiles",
+    "p8x_dequantize_rows", "p8x_vec_dot_rows",
 ]
 
 
@@ -76,6 +77,9 @@ def lib():
     L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
     L.p8x_quantize_x16.argtypes = [vp, vp, i, sz, vp, vp, vp, vp, vp, vp, vp]
     L.p8x_mul_mat_vec_multi.argtypes = [vp, i, vp, sz, vp, vp, vp]
+    L.p8x_decode_tiles.argtypes = [vp, i, i, i, i, i, vp, sz, vp]
+    L.p8x_dequantize_rows.argtypes = [vp, i, i, i, vp, sz, vp]
+    L.p8x_vec_dot_rows.argtypes = [vp, i, vp, vp, i, i, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec_glu.argtypes = [vp, vp, vp, sz, vp, vp]
     L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
@@ -477,6 +481,39 @@ class Tensor:
         synchronize()
         return (q.to_numpy(np.int8, (ncols, self.K)), d.to_numpy(np.float32, (ncols, self.nsl)),
                 s.to_numpy(np.int32, (ncols, self.nsl)))
+
+    def decode_tiles(self, g0, ng, b0, nb, dtype=I16):
+        """rotated-domain tiles of row groups g0 .. and blocks b0 ..: [32 ng][256 nb]"""
+        npdt = {I16: np.int16, F32: np.float32}[dtype]
+        out = DeviceBuffer(32 * ng * 256 * nb * np.dtype(npdt).itemsize)
+        check(lib().p8x_decode_tiles(self.h, dtype, g0, ng, b0, nb, out.ptr, 256 * nb, None), "p8x_decode_tiles")
+        synchronize()
+        return out.to_numpy(npdt, (32 * ng, 256 * nb))
+
+    def dequantize_rows(self, row0, nrows, dtype=F32, ld=None):
+        """original rows row0 .. row0 + nrows - 1, [nrows][ld] (ld >= K; the columns past K are left as allocated)"""
+        ld = ld or self.K
+        npdt = {F32: np.float32, F16: np.uint16, BF16: np.uint16}[dtype]
+        out = DeviceBuffer(nrows * ld * np.dtype(npdt).itemsize)
+        out.fill(0)
+        check(lib().p8x_dequantize_rows(self.h, dtype, row0, nrows, out.ptr, ld, None), "p8x_dequantize_rows")
+        synchronize()
+        return out.to_numpy(npdt, (nrows, ld))
+
+    def vec_dot_rows(self, act, q, d, g0, ng, x=None):
+        """(y [ncols][rows] with only row groups g0 .. written (NaN elsewhere), partials [ncols][32 ng][blocks])"""
+        q = np.ascontiguousarray(q)
+        ncols = q.shape[0]
+        qd = DeviceBuffer.from_numpy(q)
+        dd = DeviceBuffer.from_numpy(np.ascontiguousarray(d, np.float32)) if d is not None else None
+        xd = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32)) if x is not None else None
+        y = DeviceBuffer.from_numpy(np.full((ncols, self.rows), np.nan, np.float32))
+        nblk = self.nsl if act == ACT_Q8_128 else self.K // 32
+        p = DeviceBuffer(4 * ncols * 32 * ng * nblk)
+        check(lib().p8x_vec_dot_rows(self.h, act, qd.ptr, dd.ptr if dd else None, ncols, g0, ng, xd.ptr if xd else None, self.K,
+                                     y.ptr, self.rows, p.ptr, None), "p8x_vec_dot_rows")
+        synchronize()
+        return y.to_numpy(np.float32, (ncols, self.rows)), p.to_numpy(np.int32, (ncols, 32 * ng, nblk))
 
     def quantize_x16(self, x):
         """(qh, dh, sh, ql, dl, sl) per column: the x16 planes"""

@@ -386,3 +386,47 @@ def test_gemv_x16_columns_and_shapes(rows, K, ncols):
         assert rel_l2(Y[n], orc.gemv_f64(X[n], act="x16")) < 1e-5, n
     with pytest.raises(p8x.P8xError, match="x16 takes at most 4"):
         t.mul_mat_vec(np.zeros((5, K), np.float32), act=p8x.ACT_X16)
+
+
+@pytest.mark.parametrize("permute", [True, False])
+def test_tile_and_row_ranges(permute):
+    """the per-tile / per-row forms: decode_tiles windows and single tiles bit-exact to the oracle's tile decode,
+    dequantize_rows bit-exact to the oracle's rows (identity and permuted rows), vec_dot_rows equal to the whole
+    call on those rows with exact partials"""
+    rows, K = 512, 2048
+    slot = p8x.synth_random(900 + permute, rows, K, class_p=(1, 1, 1, 4, 1, 1, 1, 1), nd=9, permute=permute)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    ints = orc.decode_all()
+    for g0, ng, b0, nb in ((0, 1, 0, 1), (3, 1, 5, 1), (2, 5, 1, 3), (0, 16, 0, 8), (15, 1, 7, 1)):
+        got = t.decode_tiles(g0, ng, b0, nb)
+        assert np.array_equal(got, ints[32 * g0:32 * (g0 + ng), 256 * b0:256 * (b0 + nb)]), (g0, ng, b0, nb)
+    assert np.array_equal(t.decode_tiles(4, 1, 2, 1), orc.decode_tile(4, 2))
+    W = orc.dequant()
+    for row0, nrows in ((0, rows), (0, 1), (37, 1), (100, 57), (480, 32), (511, 1)):
+        got = t.dequantize_rows(row0, nrows, ld=K + 64)
+        assert np.array_equal(got[:, :K].view(np.uint32), W[row0:row0 + nrows].view(np.uint32)), (row0, nrows)
+        assert not got[:, K:].any()   # only the K columns are written
+    h = t.dequantize_rows(200, 40, dtype=p8x.F16)
+    assert np.array_equal(h, W[200:240].astype(np.float16).view(np.uint16))
+    x = np.random.default_rng(5).standard_normal((2, K)).astype(np.float32)
+    q = np.stack([orc.prep_q8_128(x[n])[0] for n in range(2)])
+    d = np.stack([orc.prep_q8_128(x[n])[1] for n in range(2)])
+    yall, pall = t.vec_dot(p8x.ACT_Q8_128, q, d, partials=True)
+    prm = np.frombuffer(slot[slotgen_offsets(slot, rows, K)["P"]:][:2 * rows].tobytes(), np.int16)
+    for g0, ng in ((0, 16), (3, 2), (15, 1)):
+        y, part = t.vec_dot_rows(p8x.ACT_Q8_128, q, d, g0, ng)
+        orig = prm[32 * g0:32 * (g0 + ng)]
+        assert np.array_equal(y[:, orig].view(np.uint32), yall[:, orig].view(np.uint32)), (g0, ng)
+        others = np.setdiff1d(np.arange(rows), orig)
+        assert np.isnan(y[:, others]).all()
+        assert np.array_equal(part, pall[:, 32 * g0:32 * (g0 + ng)]), (g0, ng)
+    blk = orc.quantize_q8_1(x[0])
+    y1, p1 = t.vec_dot_rows(p8x.ACT_Q8_1, blk[None, :], None, 6, 3)
+    assert np.array_equal(p1[0], orc.partials_q8_1(blk)[192:288])
+
+
+def slotgen_offsets(slot, rows, K):
+    import slotgen
+    nd = int(np.frombuffer(slot[-32:].tobytes(), np.uint32)[3])
+    return slotgen.offsets(slot.size, rows, K, nd)
