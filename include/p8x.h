@@ -232,6 +232,47 @@ int p8x_synth_random(uint64_t seed, int rows, int K, const double *class_p, int 
  * |W| > fp16(1.001 max|W|). c16 may be NULL (all ones). */
 int p8x_quantize_tensor(const float *W, int rows, int K, const uint16_t *c16, uint64_t sign_seed,
                         void *out, size_t cap, size_t *n_out);
+
+/* ---- encoder of real weights: every class, LDLQ error feedback, class allocation ----
+ * Restates the reference's offline tensor encoder (research/detail/r48k.py:213-239 k_tensor, :104-118 encode,
+ * :57-95 vit_k, :33-55 best_cw, :97-102 zero_ldlq, :121-141 alloc), which is Python (torch) there; this is its
+ * native host form, behind the same inputs: weights W [rows][K], column scales c, the layer input's second moment H,
+ * a bit budget. Every choice is a deterministic function of the inputs (fixed operation order, ties to the lower
+ * index). */
+typedef struct p8x_encode_params {
+    const uint16_t *c16;     /* K fp16 column scales c (the decoder divides column k by c[k]); NULL: all 1 */
+    const int8_t *signs;     /* 256 Hadamard signs (+1/-1); NULL: drawn from sign_seed */
+    uint64_t sign_seed;
+    const float *H;          /* K x K row-major symmetric second moment of the layer input (original columns); NULL:
+                              * identity (plain MSE, no feedback) */
+    const double *U;         /* K x K row-major upper factor in the rotated domain (p8x_encode_factor); overrides H */
+    double damp;             /* diagonal damping of the rotated H, relative to its mean diagonal (0.1) */
+    const uint8_t *classes;  /* (rows/32) x (K/256) class per tile, sorted-row order; NULL: allocated */
+    double bits_per_weight;  /* index-stream budget of the allocation (2.0) */
+    int n_salient;           /* the tiles that hold the n largest |W| are allocated class >= 6 (4) */
+    const int16_t *prm;      /* sorted row -> original row; NULL: ascending mean log block energy */
+    double alpha;            /* S = fp16(alpha * rms / gain[class]) per row and 256 columns (1.05) */
+    const double *gain;      /* 8 class gains; NULL: those of the shipped codebook */
+    const double *dist;      /* 8 class distortion factors of the allocation; NULL: those of the shipped codebook */
+    const uint32_t *A;       /* 256-entry int8x4 codebook; NULL: the shipped one (then cs is ignored) */
+    uint32_t cs;             /* coset int8x4 of a caller codebook; A[f] + cs must stay in int8 */
+    int threads;             /* host worker threads; 0: hardware concurrency, at most 16 */
+} p8x_encode_params;
+void p8x_encode_defaults(p8x_encode_params *p);
+/* Encodes W into a new slot (malloc'd; release with p8x_encode_free). P8X_ERR_ARG for bad shapes or inputs
+ * (non-finite W, zero/non-finite c, H not positive definite, prm not a permutation, class > 7),
+ * P8X_ERR_UNSUPPORTED when the payload or the delta list exceed the format or A + cs wraps. */
+int p8x_encode_tensor(const float *W, int rows, int K, const p8x_encode_params *p, void **out, size_t *n_out);
+void p8x_encode_free(void *slot);
+/* U (K x K, upper, U^T U = Hq^-1) with Hq = R diag(1/c) H diag(1/c) R^T + damp * mean(diag) * I and R the per-256
+ * block rotation FWHT(sg * .)/16 (research/detail/r48k.py:215-218). */
+int p8x_encode_factor(const float *H, const uint16_t *c16, const int8_t *signs, uint64_t sign_seed, int K,
+                      double damp, int threads, double *U);
+/* Class per tile from per-tile distortion weights E (sum over the tile's 32 rows of block energy times the block's
+ * mean U_ii^-2 share) within budget_bits for the whole tensor; floor_ (or NULL) marks tiles held at class >= 6
+ * (research/detail/r48k.py:121-141). */
+int p8x_encode_alloc(const double *E, int n_tiles, double budget_bits, const double *dist, const uint8_t *floor_,
+                     uint8_t *classes);
 /* bytes the two producers need */
 size_t p8x_slot_bytes(int rows, int K, const size_t class_tiles[8], int nd);
 

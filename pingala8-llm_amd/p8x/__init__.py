@@ -26,7 +26,8 @@ EXPORTS = [
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_decode_tiles",
-    "p8x_dequantize_rows", "p8x_vec_dot_rows",
+    "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
+    "p8x_encode_factor", "p8x_encode_alloc",
 ]
 
 
@@ -48,6 +49,14 @@ class VrDesc(ctypes.Structure):
 
 class BatchInfo(ctypes.Structure):
     _fields_ = [(f, ctypes.c_int) for f in ("njobs", "ncols", "class_set", "units", "split_jobs", "small_launch", "waves")]
+
+
+class EncodeParams(ctypes.Structure):
+    _fields_ = [("c16", ctypes.c_void_p), ("signs", ctypes.c_void_p), ("sign_seed", ctypes.c_uint64),
+                ("H", ctypes.c_void_p), ("U", ctypes.c_void_p), ("damp", ctypes.c_double), ("classes", ctypes.c_void_p),
+                ("bits_per_weight", ctypes.c_double), ("n_salient", ctypes.c_int), ("prm", ctypes.c_void_p),
+                ("alpha", ctypes.c_double), ("gain", ctypes.c_void_p), ("dist", ctypes.c_void_p), ("A", ctypes.c_void_p),
+                ("cs", ctypes.c_uint32), ("threads", ctypes.c_int)]
 
 
 _lib = None
@@ -98,6 +107,11 @@ def lib():
     L.p8x_synth_random.argtypes = [u64, i, i, vp, i, i, i, vp, sz, ctypes.POINTER(sz)]
     L.p8x_quantize_tensor.argtypes = [vp, i, i, vp, u64, vp, sz, ctypes.POINTER(sz)]
     L.p8x_slot_bytes.argtypes = [i, i, vp, i]; L.p8x_slot_bytes.restype = sz
+    L.p8x_encode_defaults.argtypes = [ctypes.POINTER(EncodeParams)]; L.p8x_encode_defaults.restype = None
+    L.p8x_encode_tensor.argtypes = [vp, i, i, ctypes.POINTER(EncodeParams), ctypes.POINTER(vp), ctypes.POINTER(sz)]
+    L.p8x_encode_free.argtypes = [vp]; L.p8x_encode_free.restype = None
+    L.p8x_encode_factor.argtypes = [vp, vp, vp, u64, i, ctypes.c_double, i, vp]
+    L.p8x_encode_alloc.argtypes = [vp, i, ctypes.c_double, vp, vp, vp]
     L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
@@ -283,6 +297,77 @@ def synth_random(seed, rows, K, class_p=CLASS_P_C3, codebook=0, nd=0, permute=Tr
     buf = np.empty(n.value, np.uint8)
     check(L.p8x_synth_random(seed, rows, K, cp, codebook, nd, int(permute), buf.ctypes.data, buf.size, ctypes.byref(n)), "synth_random")
     return buf
+
+
+def encode_tensor(W, c16=None, H=None, U=None, classes=None, bits_per_weight=2.0, n_salient=4, prm=None, alpha=1.05,
+                  signs=None, sign_seed=0, damp=0.1, gain=None, dist=None, A=None, cs=0, threads=0):
+    """Slot bytes from f32 weights [rows][K] (every class, LDLQ feedback from H or U, class allocation).
+    classes: (rows/32, K/256) uint8 per sorted tile or None; H: (K, K) input second moment; U: (K, K) rotated factor."""
+    L = lib()
+    W = np.ascontiguousarray(W, np.float32)
+    rows, K = W.shape
+    keep = []
+
+    def ptr(a, dt, shape=None):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dt)
+        if shape is not None and a.shape != shape:
+            raise P8xError(f"encode_tensor: expected shape {shape}, got {a.shape}")
+        keep.append(a)
+        return a.ctypes.data
+
+    p = EncodeParams()
+    L.p8x_encode_defaults(ctypes.byref(p))
+    p.c16 = ptr(c16, np.uint16, (K,))
+    p.signs = ptr(signs, np.int8, (256,))
+    p.sign_seed = sign_seed
+    p.H = ptr(H, np.float32, (K, K))
+    p.U = ptr(U, np.float64, (K, K))
+    p.damp = damp
+    p.classes = ptr(classes, np.uint8, (rows // 32, K // 256))
+    p.bits_per_weight = bits_per_weight
+    p.n_salient = n_salient
+    p.prm = ptr(prm, np.int16, (rows,))
+    p.alpha = alpha
+    p.gain = ptr(gain, np.float64, (8,))
+    p.dist = ptr(dist, np.float64, (8,))
+    p.A = ptr(A, np.uint32, (256,))
+    p.cs = cs
+    p.threads = threads
+    out = ctypes.c_void_p()
+    n = ctypes.c_size_t(0)
+    check(L.p8x_encode_tensor(W.ctypes.data, rows, K, ctypes.byref(p), ctypes.byref(out), ctypes.byref(n)), "encode_tensor")
+    try:
+        buf = np.frombuffer((ctypes.c_uint8 * n.value).from_address(out.value), np.uint8).copy()
+    finally:
+        L.p8x_encode_free(out)
+    return buf
+
+
+def encode_factor(H, c16=None, signs=None, sign_seed=0, damp=0.1, threads=0):
+    """(K, K) float64 upper factor U of the damped rotated inverse second moment"""
+    L = lib()
+    H = np.ascontiguousarray(H, np.float32)
+    K = H.shape[0]
+    c = None if c16 is None else np.ascontiguousarray(c16, np.uint16)
+    sg = None if signs is None else np.ascontiguousarray(signs, np.int8)
+    U = np.empty((K, K), np.float64)
+    check(L.p8x_encode_factor(H.ctypes.data, None if c is None else c.ctypes.data, None if sg is None else sg.ctypes.data,
+                              sign_seed, K, damp, threads, U.ctypes.data), "encode_factor")
+    return U
+
+
+def encode_alloc(E, budget_bits, dist=None, floor=None):
+    """class per tile (uint8, E's shape) from per-tile distortion weights E within budget_bits"""
+    L = lib()
+    E = np.ascontiguousarray(E, np.float64)
+    d = None if dist is None else np.ascontiguousarray(dist, np.float64)
+    f = None if floor is None else np.ascontiguousarray(floor, np.uint8)
+    out = np.empty(E.shape, np.uint8)
+    check(L.p8x_encode_alloc(E.ctypes.data, E.size, budget_bits, None if d is None else d.ctypes.data,
+                             None if f is None else f.ctypes.data, out.ctypes.data), "encode_alloc")
+    return out
 
 
 def quantize_tensor(W, c16=None, sign_seed=0):

@@ -142,3 +142,103 @@ def tie_case(rng, K=512, k=2):
     x[0], x[1] = a * sg[0], b * sg[1]
     x[256], x[257] = b * sg[0], a * sg[1]
     return buf, x, k
+
+
+W1 = [0, 4, 6, 8, 8, 8, 8, 8]
+W2 = [0, 0, 0, 0, 2, 4, 8, 8]
+W3 = [0, 0, 0, 0, 0, 0, 0, 8]
+
+
+def _put(lw, wb, W, k, v):
+    pos = W * k
+    wi, bb = wb + (pos >> 5), pos & 31
+    x = (int(v) & ((1 << W) - 1)) << bb
+    lw[wi] |= x & 0xFFFFFFFF
+    if bb + W > 32:
+        lw[wi + 1] |= x >> 32
+
+
+def pack_codes(idx, cls, prm):
+    """Payload words (tile order) from stage indices idx [rows][K/4][3] by ORIGINAL row, classes cls [ng][nb] per
+    sorted tile and prm (sorted -> original). Field layout per lane (CPU.patch:285-309): stage 1 of width W1 < 8 as
+    the 32 stored MSBs in word 0 plus (W1 - 1)-bit low fields from word 1, W1 = 8 as 8-bit fields from word 0; stage 2
+    from word W1, stage 3 from word W1 + W2; lane j's k-th field is chunk (j + k) & 31; words [i >> 1][j][i & 1]."""
+    ng, nb = cls.shape
+    words = []
+    for g in range(ng):
+        for b in range(nb):
+            c = int(cls[g, b])
+            nw = NW[c]
+            if not nw:
+                continue
+            tile = np.zeros(64 * nw, np.uint32)
+            for hs in range(2):
+                for j in range(32):
+                    r = int(prm[32 * g + j])
+                    ch = idx[r, (256 * b + 128 * hs) // 4:(256 * b + 128 * hs) // 4 + 32]
+                    lw = [0] * nw
+                    for k in range(32):
+                        f = ch[(j + k) & 31]
+                        if W1[c] == 8:
+                            _put(lw, 0, 8, k, f[0])
+                        else:
+                            lw[0] |= ((int(f[0]) >> (W1[c] - 1)) & 1) << k
+                            _put(lw, 1, W1[c] - 1, k, f[0])
+                        if W2[c]:
+                            _put(lw, W1[c], W2[c], k, f[1])
+                        if W3[c]:
+                            _put(lw, W1[c] + W2[c], W3[c], k, f[2])
+                    for i in range(nw):
+                        tile[hs * nw * 32 + ((i >> 1) << 6) + 2 * j + (i & 1)] = lw[i]
+            words.append(tile)
+    return np.concatenate(words) if words else np.zeros(0, np.uint32)
+
+
+def _get(w, wb, W, k):
+    pos = W * k
+    wi, bb = wb + (pos >> 5), pos & 31
+    v = int(w[wi]) | ((int(w[wi + 1]) << 32) if wi + 1 < len(w) else 0)
+    return (v >> bb) & ((1 << W) - 1)
+
+
+def slot_codes(slot, rows, K):
+    """(cls [ng][nb], idx [rows][K/4][3] by SORTED row, h [rows][K/4] coset bits) read back from a slot's payload;
+    the coset bit of chunk t is u_{t-2} of the recursion u_t = z_t ^ u_{t-1} ^ u_{t-3} over the stored stage-1 MSBs
+    z in chunk order (CPU.patch:299-304)."""
+    ng, nb = rows // 32, K // 256
+    nt = ng * nb
+    M = slot[2064:2064 + 4 * nt].view(np.uint32)
+    offD = a16(2064 + 68 * nt)
+    D = slot[offD:offD + 4 * ((slot.size - offD) // 4)].view(np.uint32)
+    cls = (M >> 29).astype(np.int64).reshape(ng, nb)
+    idx = np.zeros((rows, K // 4, 3), np.int64)
+    hb = np.zeros((rows, K // 4), np.int64)
+    for g in range(ng):
+        for b in range(nb):
+            c = int(cls[g, b])
+            nw = NW[c]
+            if not nw:
+                continue
+            base = int(M[g * nb + b] & 0x1FFFFFFF)
+            for hs in range(2):
+                for j in range(32):
+                    lw = [int(D[base + hs * nw * 32 + ((i >> 1) << 6) + 2 * j + (i & 1)]) for i in range(nw)]
+                    z = [0] * 32
+                    for k in range(32):
+                        t = (j + k) & 31
+                        col = (256 * b + 128 * hs) // 4 + t
+                        if W1[c] == 8:
+                            f1 = _get(lw, 0, 8, k)
+                        else:
+                            f1 = _get(lw, 1, W1[c] - 1, k) | (((lw[0] >> k) & 1) << (W1[c] - 1))
+                        idx[32 * g + j, col, 0] = f1
+                        if W2[c]:
+                            idx[32 * g + j, col, 1] = _get(lw, W1[c], W2[c], k)
+                        if W3[c]:
+                            idx[32 * g + j, col, 2] = _get(lw, W1[c] + W2[c], W3[c], k)
+                        z[t] = f1 >> (W1[c] - 1)
+                    u = [0] * 32
+                    for t in range(32):
+                        u[t] = z[t] ^ (u[t - 1] if t >= 1 else 0) ^ (u[t - 3] if t >= 3 else 0)
+                        hb[32 * g + j, (256 * b + 128 * hs) // 4 + t] = u[t - 2] if t >= 2 else 0
+    return cls, idx, hb

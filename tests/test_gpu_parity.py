@@ -167,6 +167,31 @@ def test_quantized_4096_config():
     assert rel_l2(t.mul_mat_vec(x)[0], orc.gemv_f64(x)) < 1e-5
 
 
+def test_encoded_ldlq_slot_all_classes():
+    """A 512 x 2048 slot from the host encoder with H-weighted feedback and allocated classes (mixed 0..7, sorted
+    rows, clamp deltas): GPU decode and dequant bit-exact to the oracle, GEMV within the fp64 bar."""
+    rng = np.random.default_rng(77)
+    rows, K = 512, 2048
+    W = (rng.standard_normal((rows, K)) * 0.02).astype(np.float32)
+    W *= rng.lognormal(0, 1.0, rows).astype(np.float32)[:, None]      # row energies spread: classes 0..7 all used
+    W[rng.random(W.shape) < 0.002] *= 12
+    W[:4] = np.where(W[:4] > 0, 1, -1) * np.abs(W).max()            # |W| = max: overshoots become clamp deltas
+    X = rng.standard_normal((2 * K, K)).astype(np.float32)
+    X[:, 1:] += 0.8 * X[:, :-1]
+    H = (X.T @ X / X.shape[0]).astype(np.float32)
+    c16 = rng.uniform(0.6, 1.8, K).astype(np.float16).view(np.uint16)
+    slot = p8x.encode_tensor(W, c16=c16, H=H, bits_per_weight=2.5, n_salient=8, sign_seed=5)
+    t = p8x.Tensor(slot, rows, K)
+    info = t.info()
+    assert sum(1 for c in range(8) if info.class_tiles[c]) >= 6, list(info.class_tiles)
+    orc = O.Oracle(slot, rows, K)
+    assert orc.nd > 0
+    assert np.array_equal(t.decode_rotated(p8x.I16), orc.decode_all())
+    assert np.array_equal(t.dequantize(p8x.F32).view(np.uint32), orc.dequant().view(np.uint32))
+    x = rng.standard_normal(K).astype(np.float32)
+    assert rel_l2(t.mul_mat_vec(x)[0], orc.gemv_f64(x)) < REL_L2
+
+
 def test_prepare_rejects_bad_slots():
     rng = np.random.default_rng(3)
     import slotgen
