@@ -340,13 +340,26 @@ def measure_dependent_step(tensors, kinds, stream, steps):
     graph = p8x.Graph(enqueue, stream)
     g_ms = timed_steps(lambda: graph.launch(stream), stream, 3, steps)
     graph.release()
+    # the same chain as one cooperative launch (p8x_step): stages separated by grid barriers
+    chain = []
+    for qkv, xin, yqkv, (o, xo, yo), (gate, up, xg, yg), (down, xd, yd) in plan:
+        chain += [(list(qkv), xin, list(yqkv)), ([o], xo, [yo]), ([gate, up], xg, None, yg), ([down], xd, [yd])]
+    chain.append((head, cur, yh))
+    step = p8x.Step(chain)
+    s_ms = timed_steps(lambda: step.run(stream), stream, 3, steps)
+    step.check()
+    sinfo = step.info()
+    step.release()
     step_bytes = sum(t.stream_bytes for t in tensors)
     launches = 4 * nl + 1
-    log(f"dependent step: eager {eager_ms * 1e3:.0f} us, graph {g_ms * 1e3:.0f} us ({launches} launches)")
+    log(f"dependent step: eager {eager_ms * 1e3:.0f} us, graph {g_ms * 1e3:.0f} us ({launches} launches), "
+        f"one launch {s_ms * 1e3:.0f} us ({sinfo['grid']} workgroups, {sinfo['stages']} stages)")
     for b in bufs:
         b.free()
     return {"workload": f"{nl} layers: q/k/v in one launch -> o -> silu(gate) * up in one launch -> down, then the head "
                         "shards in one launch; each launch reads its producer's output", "launches": launches,
+            "step_kernel": {"ms_per_step": round(s_ms, 4), "GB/s": round(step_bytes / (s_ms * 1e-3) / 1e9, 1),
+                            "stages": sinfo["stages"], "workgroups": sinfo["grid"]},
             "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)},
             "eager": {"ms_per_step": round(eager_ms, 4), "GB/s": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)}}
 

@@ -147,6 +147,31 @@ int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *
  * clamp deltas), each row's pair meets through the gate tensor's workspace (calls with one gate tensor are ordered
  * on one stream). */
 int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream);
+
+/* ---- a decode step's chain of linears in one launch ----
+ * The graph-level form of the per-node calls above: where the reference walks the graph's MUL_MAT nodes once
+ * (ggml_cuda_f44_prepare_graph, CPU.patch:1955-2004) and then launches one kernel per node (CPU.patch:2615-2631),
+ * a step object takes the chain of a batch-1 step's linears once and runs it as one cooperative launch: stage s
+ * computes p8x_mul_mat_vec_multi (or, with glu_out, p8x_mul_mat_vec_glu) of its tensors on its input x, and reads
+ * x only after every earlier stage has finished (a grid barrier between stages), so a stage's input may be an
+ * earlier stage's output. Results equal those per-node calls bit for bit. Stage tensors share one codebook; each
+ * stage's tensors share K and the input rotation; x and outputs are device vectors (x 16-byte aligned). The step
+ * keeps pointers: the tensors and buffers must outlive it. Calls of one step object are ordered on one stream. */
+typedef struct p8x_step_stage {
+    int n;                               /* 1..4 tensors on the same input */
+    const p8x_tensor *tensors[4];
+    const float *x;                      /* input, K floats */
+    float *y[4];                         /* outputs, rows floats each (unused with glu_out) */
+    float *glu_out;                      /* non-NULL: n == 2, glu_out = silu(tensors[0] x) * (tensors[1] x) */
+} p8x_step_stage;
+typedef struct p8x_step p8x_step;
+int p8x_step_create(const p8x_step_stage *stages, int n, p8x_step **out);
+int p8x_step_run(p8x_step *step, void *stream);
+/* Synchronizes the device and reports whether every barrier of the launches so far completed (P8X_ERR_HIP if a
+ * barrier wait gave up; the step then refuses further runs). */
+int p8x_step_check(p8x_step *step);
+int p8x_step_info(const p8x_step *step, int *grid, int *stages, int *class_set);
+void p8x_step_release(p8x_step *step);
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
  * X in P8X_F32 or P8X_BF16 (16-byte aligned, ldx % 8 == 0). The Hadamard rotation is applied to X (fp16 x'),
  * weight tiles are decoded from the LDS coset table straight into fp16 MFMA operands (v S), fp32 accumulation,

@@ -575,21 +575,24 @@ __device__ __forceinline__ T pick(int jb, T a0, T a1, T a2, T a3) { return jb ==
 
 // The second of a row's two arrivals computes silu(gate) * up: each lane stores its row's value (agent-coherent),
 // waits for the stores (as in arrive_after_stores), counts its arrival on the row's counter, and the lane that saw
-// the partner's arrival reads the partner's value and writes the output (the counter goes back to 0).
-__device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v, bool active) {
-    const gptr<float> pair = as_global_rw(R.glu_pair);
-    const int rows = R.j0.rows;
+// the partner's arrival reads the partner's value and writes the output, agent-coherent (the counter goes back to 0).
+// pair: [2][rows] gate, up values; cnt: [rows] counters; out: [rows].
+__device__ __forceinline__ void glu_meet(float *pair_, unsigned *cnt, float *out, int rows, int jb, int r, float v, bool active) {
+    const gptr<float> pair = as_global_rw(pair_);
     if (active) __hip_atomic_store(&pair[(size_t)jb * rows + r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned old = 0;
-    if (active) old = __hip_atomic_fetch_add(&R.glu_cnt[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (active) old = __hip_atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __asm__ volatile("" ::: "memory");
     if (active && old == 1u) {
         const float other = __hip_atomic_load(&pair[(size_t)(1 - jb) * rows + r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const float gate = jb == 0 ? v : other, up = jb == 0 ? other : v;
-        as_global_rw(R.glu_out)[r] = gate / (1.0f + expf(-gate)) * up;
-        __hip_atomic_store(&R.glu_cnt[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&as_global_rw(out)[r], gate / (1.0f + expf(-gate)) * up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&cnt[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+__device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v, bool active) {
+    glu_meet(R.glu_pair, R.glu_cnt, R.glu_out, R.j0.rows, jb, r, v, active);
 }
 
 // SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
@@ -631,7 +634,9 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     const int per = nbk / wpg, rem = nbk % wpg;
     int b0 = c.b0 + wk * per + min(wk, rem), b1 = b0 + per + (wk < rem ? 1 : 0);   // the wave's K range
     if (team >= gc) b1 = b0;
-    // the wave's activation blocks: every load first, the table meanwhile, then the quantization
+    // Loads in the order their data is needed (vector loads return in order): the wave's activation blocks, the
+    // codebook words of the table; then, for a one-class tensor, the wave's first run of tiles (its first row group
+    // over its K range), whose payload stays in flight while the table is written and x is quantized.
     BlockLane in[RQ];
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
@@ -639,7 +644,23 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         if (it < NCOL * nbk) in[i].load(J.x + (size_t)n * J.ldx + 256 * bk, J.ic + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
-    build_coset_table<64 * WAVES>(sm.tab, a2, tid);
+    CosetTableFill<64 * WAVES> fill;
+    fill.load(a2, tid);
+    constexpr int PC = CM == kCmC3 ? 3 : CM == kCmC6 ? 6 : 0;
+    GemvRun<NCOL, P8X_ACT_Q8_128, false, PC ? PC : 3, gemv_nbuf(NCOL, PC ? PC : 3), true> pre;
+    const int gstep = nwg / nks;
+    const int gfirst = wgl / nks + min(team, gc - 1) * gstep;
+    const bool pre_on = PC != 0 && team < gc && gfirst < J.ng && b0 < b1;
+    __asm__ volatile("" ::: "memory");
+    if constexpr (PC != 0) {
+        // on every path (a wave without work requests one in-range tile it never reads), so that no control-flow
+        // merge before the table stores makes the compiler wait for these loads there
+        c.g = min(gfirst, J.ng - 1);
+        const int bb = pre_on ? b0 : min(b0, J.nb - 1);
+        pre.begin(c, bb, pre_on ? b1 : bb + 1);
+    }
+    __asm__ volatile("" ::: "memory");
+    fill.store(sm.tab, tid);
     // the blocks of a wave are independent: quantized G at a time in straight-line code, so their cross-lane
     // chains overlap (one at a time they cost a full chain latency each)
     if (NCOL * nbk <= WAVES) rg_quantize<1, NCOL>(nbk, sm, in, w, lane);
@@ -647,8 +668,8 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     else rg_quantize<4, NCOL>(nbk, sm, in, w, lane);
     __syncthreads();
     int set = 0;
-    const int gstep = nwg / nks;
     const GemvJob &JB = J;
+    bool first = true;
     for (int g0 = wgl / nks; g0 < J.ng; g0 += gstep * gc, set ^= 1) {
         const int g = g0 + min(team, gc - 1) * gstep;   // this wave's row group
         const bool lead = wk == 0 && team < gc && g < J.ng;   // the team's first wave: epilogue of row group g
@@ -659,7 +680,10 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         float yacc[NCOL];
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) yacc[n] = 0.f;
-        for (int b = b0; b < (g < J.ng ? b1 : b0);) {
+        int bstart = b0;
+        if (PC != 0 && first && pre_on) bstart = pre.finish(c, sm, yacc);   // the run begun before the prep
+        first = false;
+        for (int b = bstart; b < (g < J.ng ? b1 : b0);) {
             const uint32_t mt = as_const(JB.M)[(size_t)g * JB.nb + b];
             switch (mt >> 29) {
                 case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
@@ -950,6 +974,11 @@ int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
 int launch_gemv_rg(int ncols, int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);
 int launch_gemv_rg_multi(int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);
+// host planning shared by the multi-linear launch and the decode-step kernel (p8x_gemv.hip)
+int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
+                    RgJobs &R, int &cm, int &ng);
+int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what);
+int class_set(const size_t hist[8]);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
 
 }  // namespace p8x

@@ -253,17 +253,18 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
     return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
 }
 
-// Several linears on the same activations in one row-group launch (out == nullptr), or a gate / up pair with the
-// swiglu epilogue (out != nullptr: n == 2, tensors[0] = gate). Shapes, codebook and rotation are checked by the caller.
-int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
-                      hipStream_t st) {
+// The row-group plan of several linears on the same activations (out == nullptr), or of a gate / up pair with the
+// swiglu epilogue (out != nullptr: n == 2, tensors[0] = gate): jobs, workgroups per job, K-chunks. Also sets the
+// class set of the tensors and their row groups in total. Shapes, codebook and rotation are checked by the caller.
+int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
+                    RgJobs &R, int &cm, int &ng) {
     size_t hist[8] = {0};
-    int ng = 0;
+    ng = 0;
     for (int i = 0; i < n; ++i) {
         for (int c = 0; c < 8; ++c) hist[c] += ts[i]->class_tiles[c];
         ng += ts[i]->ng;
     }
-    const int cm = class_set(hist);
+    cm = class_set(hist);
     // the K plan of the combined row groups: K-chunks that fit the LDS buffer, split in two when they fill at most
     // half the CUs and K is long (the single-call rule)
     const p8x_tensor *t0 = ts[0];
@@ -271,7 +272,7 @@ int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t
     if (nks == 1 && 2 * ng <= num_cus() && t0->nb >= 32) nks = 2;
     const int kc = (t0->nb + nks - 1) / nks;
     nks = (t0->nb + kc - 1) / kc;
-    RgJobs R{};
+    R = RgJobs{};
     R.njobs = n;
     fill_job(R.j0, t0, nullptr, nullptr, x, ldx, out ? nullptr : y[0], out ? 0 : ldy[0], nullptr, nks, kc, 1, 0);
     // workgroups per job: ceil(its row groups / per) per K-chunk, with per = ceil(all row groups / CUs)
@@ -293,7 +294,16 @@ int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t
         R.glu_pair = t0->wglu;
         R.glu_cnt = t0->wglu_cnt;
     }
-    return launch_gemv_rg_multi(cm, R, ng, t0->a2, st);
+    return P8X_OK;
+}
+
+int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
+                      hipStream_t st) {
+    RgJobs R;
+    int cm = 0, ng = 0;
+    const int rc = plan_gemv_multi(ts, n, x, ldx, y, ldy, out, R, cm, ng);
+    if (rc) return rc;
+    return launch_gemv_rg_multi(cm, R, ng, ts[0]->a2, st);
 }
 
 // ------------------------------------------------------------------------------------------------ grouped launches
@@ -392,6 +402,20 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
         for (int i = 0; i < 4; ++i)
             if (r0 + 256 * i < J.rows && !(pd[i] & 0x8000u)) as_global_rw(J.y)[(size_t)n * J.ldy + pd[i]] = v[i];
     }
+}
+
+int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what) {
+    for (int i = 0; i < n; ++i) {
+        if (!ts[i]) return set_error(P8X_ERR_ARG, "%s: tensor %d is null", what, i);
+        if (ts[i]->K != ts[0]->K) return set_error(P8X_ERR_ARG, "%s: tensor %d has K %d, tensor 0 has %d", what, i, ts[i]->K, ts[0]->K);
+        if (memcmp(ts[i]->a2_host, ts[0]->a2_host, sizeof ts[0]->a2_host))
+            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d has a different codebook", what, i);
+        if (ts[i]->ic_hash != ts[0]->ic_hash)
+            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d rotates its input differently (column scales c or signs); call it alone", what, i);
+    }
+    if (!x || ldx < (size_t)ts[0]->K || ldx % 4 || ((uintptr_t)x & 15))
+        return set_error(P8X_ERR_ARG, "%s: x null or ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", what, ldx);
+    return P8X_OK;
 }
 
 }  // namespace p8x
@@ -634,19 +658,6 @@ int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);
 }
 
-static int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what) {
-    for (int i = 0; i < n; ++i) {
-        if (!ts[i]) return set_error(P8X_ERR_ARG, "%s: tensor %d is null", what, i);
-        if (ts[i]->K != ts[0]->K) return set_error(P8X_ERR_ARG, "%s: tensor %d has K %d, tensor 0 has %d", what, i, ts[i]->K, ts[0]->K);
-        if (memcmp(ts[i]->a2_host, ts[0]->a2_host, sizeof ts[0]->a2_host))
-            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d has a different codebook", what, i);
-        if (ts[i]->ic_hash != ts[0]->ic_hash)
-            return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d rotates its input differently (column scales c or signs); call it alone", what, i);
-    }
-    if (!x || ldx < (size_t)ts[0]->K || ldx % 4 || ((uintptr_t)x & 15))
-        return set_error(P8X_ERR_ARG, "%s: x null or ldx %zu (x 16-byte aligned, ldx %% 4 == 0)", what, ldx);
-    return P8X_OK;
-}
 
 int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, void *stream) {
     if (!tensors || !y || !ldy || n < 1 || n > kRgMaxJobs) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi: bad arguments (1..%d tensors)", kRgMaxJobs);

@@ -27,21 +27,33 @@ constexpr int kTabWords = 256 * 64;   // 64 KB coset table
 constexpr int kXcds = 8;
 constexpr int kTabBytes = kTabWords * 4;
 
-// Fill the replicated table from a2 = [h][256] words (h-major), all threads of the block.
+// Fill the replicated table from a2 = [h][256] words (h-major), all threads of the block: every load first, then the
+// stores (one memory round trip for the whole table). The two halves are separate so that a kernel can issue other
+// loads between them.
+template <int NT>
+struct CosetTableFill {
+    static_assert((kTabWords / 4) % NT == 0, "table build: threads must divide the table's 16-byte entries");
+    static constexpr int PER = kTabWords / 4 / NT;
+    uint32_t v[PER];
+    __device__ __forceinline__ void load(const uint32_t *__restrict__ a2, int tid) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid + k * NT;
+            v[k] = ((const __attribute__((address_space(1))) uint32_t *)a2)[((i >> 3) & 1) * 256 + (i >> 4)];
+        }
+    }
+    __device__ __forceinline__ void store(uint32_t *tab, int tid) const {
+        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) t4[tid + k * NT] = make_uint4(v[k], v[k], v[k], v[k]);
+    }
+};
+
 template <int NT>
 __device__ __forceinline__ void build_coset_table(uint32_t *tab, const uint32_t *__restrict__ a2, int tid) {
-    static_assert((kTabWords / 4) % NT == 0, "table build: threads must divide the table's 16-byte entries");
-    constexpr int PER = kTabWords / 4 / NT;
-    uint4 *t4 = reinterpret_cast<uint4 *>(tab);
-    // every load first, then the stores: one memory round trip for the whole table
-    uint32_t v[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = tid + k * NT;
-        v[k] = ((const __attribute__((address_space(1))) uint32_t *)a2)[((i >> 3) & 1) * 256 + (i >> 4)];
-    }
-#pragma unroll
-    for (int k = 0; k < PER; ++k) t4[tid + k * NT] = make_uint4(v[k], v[k], v[k], v[k]);
+    CosetTableFill<NT> f;
+    f.load(a2, tid);
+    f.store(tab, tid);
 }
 
 // global address-space views: pointers read out of descriptors are generic; these make loads global_load

@@ -27,7 +27,8 @@ EXPORTS = [
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_decode_tiles",
     "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
-    "p8x_encode_factor", "p8x_encode_alloc",
+    "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_run", "p8x_step_check", "p8x_step_info",
+    "p8x_step_release",
 ]
 
 
@@ -57,6 +58,11 @@ class EncodeParams(ctypes.Structure):
                 ("bits_per_weight", ctypes.c_double), ("n_salient", ctypes.c_int), ("prm", ctypes.c_void_p),
                 ("alpha", ctypes.c_double), ("gain", ctypes.c_void_p), ("dist", ctypes.c_void_p), ("A", ctypes.c_void_p),
                 ("cs", ctypes.c_uint32), ("threads", ctypes.c_int)]
+
+
+class StepStageC(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_int), ("tensors", ctypes.c_void_p * 4), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p * 4),
+                ("glu_out", ctypes.c_void_p)]
 
 
 _lib = None
@@ -112,6 +118,11 @@ def lib():
     L.p8x_encode_free.argtypes = [vp]; L.p8x_encode_free.restype = None
     L.p8x_encode_factor.argtypes = [vp, vp, vp, u64, i, ctypes.c_double, i, vp]
     L.p8x_encode_alloc.argtypes = [vp, i, ctypes.c_double, vp, vp, vp]
+    L.p8x_step_create.argtypes = [ctypes.POINTER(StepStageC), i, ctypes.POINTER(vp)]
+    L.p8x_step_run.argtypes = [vp, vp]
+    L.p8x_step_check.argtypes = [vp]
+    L.p8x_step_info.argtypes = [vp, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)]
+    L.p8x_step_release.argtypes = [vp]; L.p8x_step_release.restype = None
     L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
@@ -685,6 +696,49 @@ def mul_mat_vec_glu(gate, up, x):
     mul_mat_vec_glu_dev(gate, up, xd, out)
     synchronize()
     return out.to_numpy(np.float32, (gate.rows,))
+
+
+class Step:
+    """A chain of linears in one launch (p8x_step_*). stages: list of (tensors, x, ys) or (tensors, x, None, glu_out)
+    with device buffers; stage s may read an earlier stage's output."""
+
+    def __init__(self, stages):
+        arr = (StepStageC * len(stages))()
+        for k, st in enumerate(stages):
+            tensors, x, ys = st[0], st[1], st[2]
+            glu = st[3] if len(st) > 3 else None
+            arr[k].n = len(tensors)
+            for i, t in enumerate(tensors):
+                arr[k].tensors[i] = t.h.value
+            arr[k].x = x.addr
+            if ys is not None:
+                for i, y in enumerate(ys):
+                    arr[k].y[i] = y.addr
+            arr[k].glu_out = glu.addr if glu is not None else None
+        self.h = ctypes.c_void_p()
+        check(lib().p8x_step_create(arr, len(stages), ctypes.byref(self.h)), "p8x_step_create")
+
+    def run(self, stream=None):
+        check(lib().p8x_step_run(self.h, stream.h if stream else None), "p8x_step_run")
+
+    def check(self):
+        check(lib().p8x_step_check(self.h), "p8x_step_check")
+
+    def info(self):
+        g, n, cm = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().p8x_step_info(self.h, ctypes.byref(g), ctypes.byref(n), ctypes.byref(cm)), "p8x_step_info")
+        return {"grid": g.value, "stages": n.value, "class_set": cm.value}
+
+    def release(self):
+        if self.h:
+            lib().p8x_step_release(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 class GemvBatch:

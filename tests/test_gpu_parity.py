@@ -182,7 +182,7 @@ def test_encoded_ldlq_slot_all_classes():
     c16 = rng.uniform(0.6, 1.8, K).astype(np.float16).view(np.uint16)
     slot = p8x.encode_tensor(W, c16=c16, H=H, bits_per_weight=2.5, n_salient=8, sign_seed=5)
     t = p8x.Tensor(slot, rows, K)
-    info = t.info()
+    info = t.info
     assert sum(1 for c in range(8) if info.class_tiles[c]) >= 6, list(info.class_tiles)
     orc = O.Oracle(slot, rows, K)
     assert orc.nd > 0
