@@ -296,6 +296,288 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(2, 
     });
 }
 
+// ------------------------------------------------------------------------------------------------ dequantize, classes 0-3
+// The same outputs as k_dequant for tensors whose tiles are of classes 0-3 (one codebook stage, |A[f] + h c| <= 128),
+// computed with integer butterflies wherever the reference's f32 arithmetic is exact:
+//   * v S is exact in f32 (|v| <= 128, S an fp16 with 11 significant bits), and so is every sum of up to 64 of them
+//     (64 * 128 * 2047 < 2^24): stages h = 1 .. 32 of the reference never round, and equal the integer transform
+//     times S. Stages 1-2 act inside a 4-column chunk and come from a table (FWHT4 of each codeword, int16 x 4);
+//     stages 4-32 are packed int16 butterflies (|sums| <= 64 * 128).
+//   * stage 64 adds two exact values and rounds once: RN(I_a S +- I_b S) = RN((I_a +- I_b) S), so it is the integer
+//     butterfly (|I| <= 16384) followed by the one f32 multiply by S;
+//   * stage 128, * 0.0625 * ic (0.0625 folded into ic: scaling by a power of two is exact) and the clamp delta are
+//     the reference's f32 operations on the reference's operands; f16 / bf16 are the RNE conversions of that f32.
+// Lane (j, p) of a wave holds row j of the tile, columns 64 p .. 64 p + 63 of both half-slices: stages 4-32 stay in
+// the lane, stage 64 pairs lane j with lane j + 32 (v_permlane32_swap on the packed ints), stage 128 pairs the lane's
+// two half-slices. Each lane then writes 128 contiguous bytes (f16) per half-slice of its output row.
+constexpr int kLoWaves = 4;
+constexpr int kLoThreads = 64 * kLoWaves;
+constexpr int kLoBandWords = 36;   // staging row: 128 bytes + 16 bytes of padding (rows spread over the banks)
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// table entry (f << 1) | h: the first two butterfly stages of the codeword bytes A[f] + h c, as int16 x 4
+__device__ __forceinline__ uint2 fwht4_entry(uint32_t w) {
+    const int b0 = sext8(w, 0), b1 = sext8(w, 1), b2 = sext8(w, 2), b3 = sext8(w, 3);
+    const int s0 = b0 + b1, s1 = b0 - b1, s2 = b2 + b3, s3 = b2 - b3;
+    const int y0 = s0 + s2, y1 = s1 + s3, y2 = s0 - s2, y3 = s1 - s3;
+    return make_uint2((uint32_t)(uint16_t)y0 | ((uint32_t)(uint16_t)y1 << 16), (uint32_t)(uint16_t)y2 | ((uint32_t)(uint16_t)y3 << 16));
+}
+
+// Payload words of lane-slice (hs, j) of a class-C tile, loaded so that after the bit rotation of lo_decode the
+// lane's fields are in chunk order starting at chunk 16 p: the stored field k is chunk (j + k) & 31, so the
+// bitstring is rotated right by d = (16 p - j) & 31 fields (whole words here, the rest in lo_decode).
+template <int C>
+__device__ __forceinline__ void lo_load(uint32_t (&w)[8], const uint32_t *__restrict__ p, int j, int d) {
+    constexpr int W1 = w1_of(C), NW = nw_of(C);
+    if constexpr (W1 == 8) {
+        const int wr = d >> 2;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) w[m] = __builtin_nontemporal_load(p + dev_word((m + wr) & 7, j, NW));
+    } else {
+        constexpr int W = W1 - 1;
+        const int wr = (d * W) >> 5;
+        w[0] = __builtin_nontemporal_load(p + dev_word(0, j, NW));
+#pragma unroll
+        for (int m = 0; m < W; ++m) w[1 + m] = __builtin_nontemporal_load(p + dev_word(1 + (m + wr) % W, j, NW));
+#pragma unroll
+        for (int m = W + 1; m < 8; ++m) w[m] = 0u;
+    }
+}
+
+// chunks 16 p .. 16 p + 15 of the lane-slice -> stage-2 ints, packed P[2 i] = (y0, y1), P[2 i + 1] = (y2, y3)
+template <int C>
+__device__ __forceinline__ void lo_decode(const uint32_t (&w)[8], int d, int p16, const uint2 *tab4, uint32_t (&P)[32]) {
+    constexpr int W1 = w1_of(C);
+    uint32_t r[8], z;
+    if constexpr (W1 == 8) {
+        const int br = 8 * (d & 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = __builtin_amdgcn_alignbit(w[(i + 1) & 7], w[i], br);
+        z = labels_from_bytes(r);
+    } else {
+        constexpr int W = W1 - 1;
+        const int br = (d * W) & 31;
+        r[0] = __builtin_amdgcn_alignbit(w[0], w[0], d);
+#pragma unroll
+        for (int i = 0; i < W; ++i) r[1 + i] = __builtin_amdgcn_alignbit(w[1 + (i + 1) % W], w[1 + i], br);
+        z = r[0];
+    }
+    // coset bits: the trellis runs over chunks 0 .. 31 of the lane-slice; bit i here is chunk 16 p + i
+    const uint32_t zt = __builtin_amdgcn_alignbit(z, z, (32 - p16) & 31);
+    const uint32_t ht = trellis_coset_bits(zt);
+    const uint32_t H = __builtin_amdgcn_alignbit(ht, ht, p16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        uint32_t f;
+        if constexpr (W1 == 8) {
+            f = __builtin_amdgcn_ubfe(r[i >> 2], 8 * (i & 3), 8);
+        } else {
+            constexpr int W = W1 - 1;
+            uint32_t rf[W];
+#pragma unroll
+            for (int q = 0; q < W; ++q) rf[q] = r[1 + q];
+            f = field_of<W>(rf, i) | (__builtin_amdgcn_ubfe(r[0], i, 1) << W);
+        }
+        const uint2 e = tab4[(f << 1) | __builtin_amdgcn_ubfe(H, i, 1)];
+        P[2 * i] = e.x;
+        P[2 * i + 1] = e.y;
+        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // 4 lookups at a time
+    }
+}
+
+template <int CM>
+__device__ __forceinline__ void lo_decode_any(int c, const uint32_t (&w)[8], int d, int p16, const uint2 *tab4, uint32_t (&P)[32]) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) { lo_decode<1>(w, d, p16, tab4, P); break; } [[fallthrough]];
+        case 2: if constexpr ((CM >> 2) & 1) { lo_decode<2>(w, d, p16, tab4, P); break; } [[fallthrough]];
+        case 3: if constexpr ((CM >> 3) & 1) { lo_decode<3>(w, d, p16, tab4, P); break; } [[fallthrough]];
+        default:
+#pragma unroll
+            for (int i = 0; i < 32; ++i) P[i] = 0u;   // class 0: zero weights
+            break;
+    }
+}
+
+template <int CM>
+__device__ __forceinline__ void lo_load_any(int c, uint32_t (&w)[8], const uint32_t *p, int j, int d) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) { lo_load<1>(w, p, j, d); break; } [[fallthrough]];
+        case 2: if constexpr ((CM >> 2) & 1) { lo_load<2>(w, p, j, d); break; } [[fallthrough]];
+        case 3: if constexpr ((CM >> 3) & 1) { lo_load<3>(w, p, j, d); break; } [[fallthrough]];
+        default:
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = 0u;
+            break;
+    }
+}
+
+// butterflies h = 4, 8, 16, 32 of the lane's 64 values (exact int16)
+__device__ __forceinline__ void lo_stages(uint32_t (&P)[32]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int st = 1 << m;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (!(i & st))
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const s16x2 a = as_s16x2(P[2 * i + k]), b = as_s16x2(P[2 * (i + st) + k]);
+                    P[2 * i + k] = as_u32(a + b);
+                    P[2 * (i + st) + k] = as_u32(a - b);
+                }
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) __asm__ volatile("; stages %0" : "+v"(P[k]));   // materialized before the exchange
+}
+
+// butterfly h = 64 across lanes j and j + 32: the lane with p = 0 keeps x0 + x1, the one with p = 1 keeps x0 - x1
+__device__ __forceinline__ void lo_stage64(uint32_t (&P)[32], s16x2 sg) {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const auto pr = __builtin_amdgcn_permlane32_swap(P[k], P[k], false, false);   // [0]: x0, [1]: x1 (both lanes)
+        P[k] = as_u32(as_s16x2(pr[0]) + as_s16x2(pr[1]) * sg);
+        __asm__ volatile("; stage64 %0" : "+v"(P[k]));   // combined here: keeps at most a few exchanged pairs live
+    }
+}
+
+struct LoNext {
+    uint32_t w0[8], w1[8];   // half-slices 0 and 1
+    int c, ro;
+    uint32_t s;
+};
+
+template <int DT, int CM>
+__global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_dequant_lo(const DecodeArgs a) {
+    static_assert(DT == P8X_F16 || DT == P8X_BF16, "16-bit outputs (f32 goes through k_dequant)");
+    __shared__ uint2 tab4[512];
+    __shared__ __align__(16) float icw[kLoWaves][256];
+    __shared__ __align__(16) uint32_t stg[kLoWaves][32 * kLoBandWords];   // one 32-row x 128-byte band per wave
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31, p = lane >> 5, p16 = 16 * p;
+    const int d = (p16 - j) & 31;
+    const s16x2 sg = {(short)(p ? -1 : 1), (short)(p ? -1 : 1)};
+    for (int i = tid; i < 512; i += kLoThreads) tab4[i] = fwht4_entry(a.a2[(i & 1) * 256 + (i >> 1)]);
+    __syncthreads();
+    size_t first, last;
+    wg_range(a, first, last);
+    first += w;
+    if (first >= last) return;
+    LoNext nx;
+    auto issue = [&](size_t q) {
+        int g, b;
+        tile_of(a, q, g, b);
+        const uint32_t mt = a.M[(size_t)g * a.nb + b];
+        nx.c = (int)(mt >> 29);
+        const uint32_t *base = a.D + (mt & 0x1FFFFFFFu);
+        const int nw = nw_of(nx.c);
+        lo_load_any<CM>(nx.c, nx.w0, base, j, d);
+        lo_load_any<CM>(nx.c, nx.w1, base + nw * 32, j, d);
+        nx.s = a.S[(size_t)b * a.rows + 32 * g + j];
+        nx.ro = a.prmd[32 * g + j];
+    };
+    // each tile's words are requested at the top of its iteration: at four waves per SIMD the other waves cover the
+    // latency (a prefetch one tile ahead, which costs registers, measured slower)
+    int icb = -1;
+    for (size_t q = first; q < last; q += kLoWaves) {
+        issue(q);
+        const int c = nx.c, rof = nx.ro, ro = rof & 0x7FFF;
+        const float S = half_to_float((uint16_t)nx.s);
+        // one half-slice at a time through its integer stages (only its 32 packed registers are being built)
+        uint32_t P0[32], P1[32];
+        lo_decode_any<CM>(c, nx.w0, d, p16, tab4, P0);
+        lo_stages(P0);
+        lo_stage64(P0, sg);
+        __asm__ volatile("" ::: "memory");
+        lo_decode_any<CM>(c, nx.w1, d, p16, tab4, P1);
+        lo_stages(P1);
+        lo_stage64(P1, sg);
+        __asm__ volatile("" ::: "memory");
+        int g, b;
+        tile_of(a, q, g, b);
+        if (b != icb) {   // this block's ic / 16 into the wave's row (wave-local)
+            const float4 c4 = reinterpret_cast<const float4 *>(a.ic + 256 * b)[lane];
+            reinterpret_cast<float4 *>(icw[w])[lane] = make_float4(c4.x * 0.0625f, c4.y * 0.0625f, c4.z * 0.0625f, c4.w * 0.0625f);
+            icb = b;
+        }
+        int e0 = 0, e1 = 0;
+        if (rof & 0x8000) { e0 = a.cp[ro]; e1 = a.cp[ro + 1]; }
+        const bool deltas = __builtin_amdgcn_ballot_w64(e0 < e1) != 0;   // wave-uniform
+        const float *icl = icw[w] + 64 * p;
+        // the packed 16-bit outputs: OUT[h][g] holds values 8 g .. 8 g + 7 of half-slice h (columns 64 p + ..)
+        uint32_t OUT[2][8][4];
+#pragma unroll
+        for (int k4 = 0; k4 < 32; k4 += 4) {
+            float o[2][8];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int k = k4 + kk;
+                const s16x2 x = as_s16x2(P0[k]), y = as_s16x2(P1[k]);
+                const float x0 = (float)x.x * S, x1 = (float)x.y * S, y0 = (float)y.x * S, y1 = (float)y.y * S;
+                const float2 c0 = *reinterpret_cast<const float2 *>(icl + 2 * k);
+                const float2 c1 = *reinterpret_cast<const float2 *>(icl + 128 + 2 * k);
+                o[0][2 * kk] = (x0 + y0) * c0.x;
+                o[0][2 * kk + 1] = (x1 + y1) * c0.y;
+                o[1][2 * kk] = (x0 - y0) * c1.x;
+                o[1][2 * kk + 1] = (x1 - y1) * c1.y;
+            }
+            if (deltas) {   // clamp delta (original row, column), in entry order
+                for (int e = e0; e < e1; ++e) {
+                    const int col = (int)a.cc[e] - 256 * b;
+                    const float dv = a.cv[e];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            if (col == 128 * h + 64 * p + 2 * k4 + i) o[h][i] += dv;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    if constexpr (DT == P8X_F16) {   // v_cvt_pk_f16_f32: both RNE
+                        const f16x2 hv = {(_Float16)o[h][2 * q2], (_Float16)o[h][2 * q2 + 1]};
+                        OUT[h][k4 >> 2][q2] = __builtin_bit_cast(uint32_t, hv);
+                    } else {                          // v_cvt_pk_bf16_f32: both RNE
+                        const bf16x2 hv = {(__bf16)o[h][2 * q2], (__bf16)o[h][2 * q2 + 1]};
+                        OUT[h][k4 >> 2][q2] = __builtin_bit_cast(uint32_t, hv);
+                    }
+                    __asm__ volatile("; out %0" : "+v"(OUT[h][k4 >> 2][q2]));
+                }
+            __builtin_amdgcn_sched_barrier(0);   // one group at a time: its packed ints are consumed as its outputs appear
+        }
+        // Out through the wave's LDS band, one (half-slice, quarter) band of the tile at a time: the lanes that own
+        // it write their 128 bytes, then each store instruction covers 8 rows x 128 bytes (whole lines).
+        uint32_t *sw = stg[w];
+        int orows[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) orows[i] = (__shfl(rof, 8 * i + (lane >> 3)) & 0x7FFF) - a.row0;   // row of piece 64 i + lane
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int qq = 0; qq < 2; ++qq) {
+                if (p == qq)
+#pragma unroll
+                    for (int gg = 0; gg < 8; ++gg)
+                        *reinterpret_cast<uint4 *>(sw + j * kLoBandWords + 4 * gg) = make_uint4(OUT[h][gg][0], OUT[h][gg][1], OUT[h][gg][2], OUT[h][gg][3]);
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the band is written
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 8 * i + (lane >> 3), piece = lane & 7;
+                    const uint4 val = *reinterpret_cast<const uint4 *>(sw + row * kLoBandWords + 4 * piece);
+                    if ((unsigned)orows[i] < (unsigned)a.nrows)
+                        *reinterpret_cast<uint4 *>((uint16_t *)a.out + (size_t)orows[i] * a.ld + 256 * b + 128 * h + 64 * qq + 8 * piece) = val;
+                }
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read before the next band overwrites it
+            }
+    }
+}
+
 static DecodeArgs decode_args(const p8x_tensor *t, void *out, size_t ld) {
     DecodeArgs a{};
     a.M = t->M; a.S = t->S; a.D = t->D; a.a2 = t->a2; a.prm = t->prm; a.prmd = t->prmd;
@@ -315,6 +597,18 @@ static int decode_grid(const DecodeArgs &a) {
 static bool only_class3(const p8x_tensor *t) {
     for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) return false;
     return true;
+}
+
+// every tile of class 0-3: the integer-butterfly dequantizer
+static bool classes_upto3(const p8x_tensor *t) {
+    for (int c = 4; c < 8; ++c) if (t->class_tiles[c]) return false;
+    return true;
+}
+
+template <int CM>
+static void launch_deq_lo(int dtype, const DecodeArgs &a, int grid, hipStream_t st) {
+    if (dtype == P8X_F16) hipLaunchKernelGGL((k_dequant_lo<P8X_F16, CM>), dim3(grid), dim3(kLoThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_dequant_lo<P8X_BF16, CM>), dim3(grid), dim3(kLoThreads), 0, st, a);
 }
 
 template <int CM>
@@ -352,8 +646,15 @@ int launch_dequant(const p8x_tensor *t, int dtype, int row0, int nrows, void *ou
         }
         a.g0 = lo; a.gn = hi - lo + 1; a.nt = (size_t)a.gn * a.bn;
     }
-    if (only_class3(t)) launch_deq<(1 << 3)>(t, dtype, a, st);
-    else launch_deq<0xFE>(t, dtype, a, st);
+    if (classes_upto3(t) && dtype != P8X_F32) {
+        const int grid = (int)std::min<size_t>((a.nt + kLoWaves - 1) / kLoWaves, (size_t)num_cus() * 4);
+        if (only_class3(t)) launch_deq_lo<(1 << 3)>(dtype, a, grid, st);
+        else launch_deq_lo<(1 << 1) | (1 << 2) | (1 << 3)>(dtype, a, grid, st);
+    } else if (only_class3(t)) {
+        launch_deq<(1 << 3)>(t, dtype, a, st);
+    } else {
+        launch_deq<0xFE>(t, dtype, a, st);
+    }
     return hip_check(hipGetLastError(), "k_dequant launch");
 }
 

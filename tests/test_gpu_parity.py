@@ -192,6 +192,36 @@ def test_encoded_ldlq_slot_all_classes():
     assert rel_l2(t.mul_mat_vec(x)[0], orc.gemv_f64(x)) < REL_L2
 
 
+@pytest.mark.parametrize("tables", ["shipped", "random", "wrapping"])
+def test_dequant_classes_0_to_3(tables):
+    """tensors of classes 0-3 only (the integer-butterfly dequantizer): f32 bit-exact to the oracle, f16 / bf16 its
+    RNE roundings, with clamp deltas, permuted rows, any int8 codebook (wrapping A + c included) and row ranges"""
+    import slotgen
+    rng = np.random.default_rng({"shipped": 1, "random": 2, "wrapping": 3}[tables])
+    rows, K = 256, 2048
+    slot = slotgen.random_slot(rng, rows, K, classes=(0, 1, 2, 3), class_p=(0.1, 0.2, 0.2, 0.5), tables=tables, nd=40)
+    t = p8x.Tensor(slot, rows, K)
+    W = O.Oracle(slot, rows, K).dequant()
+    got = t.dequantize(p8x.F32)
+    assert np.array_equal(got.view(np.uint32), W.view(np.uint32))
+    assert np.array_equal(t.dequantize(p8x.F16), W.astype(np.float16).view(np.uint16))
+    u = W.view(np.uint32).astype(np.uint64)
+    assert np.array_equal(t.dequantize(p8x.BF16), ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16))
+    for row0, nrows in ((0, 1), (77, 50), (255, 1)):
+        r = t.dequantize_rows(row0, nrows, ld=K + 32)
+        assert np.array_equal(r[:, :K].view(np.uint32), W[row0:row0 + nrows].view(np.uint32)), (row0, nrows)
+        assert not r[:, K:].any()
+
+
+def test_dequant_class3_ffn_shape():
+    """the benchmarked 14336 x 4096 class-3 tensor with clamp deltas, f16 against the oracle's f32 rounded"""
+    rows, K = 14336, 4096
+    slot = p8x.synth_random(rows + K, rows, K, nd=8)
+    t = p8x.Tensor(slot, rows, K)
+    W = O.Oracle(slot, rows, K).dequant()
+    assert np.array_equal(t.dequantize(p8x.F16), W.astype(np.float16).view(np.uint16))
+
+
 def test_prepare_rejects_bad_slots():
     rng = np.random.default_rng(3)
     import slotgen
