@@ -305,7 +305,7 @@ def measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, pl_steps, 
     return per_linear
 
 
-def measure_dependent_step(tensors, kinds, stream, steps):
+def measure_dependent_step(tensors, kinds, stream, steps, graph_replay=True):
     """A batch-1 decode step that respects the data dependencies of the model: per layer, q/k/v as one launch on the
     layer input (p8x_mul_mat_vec_multi), o on q's output, the gated FFN input silu(gate x) * (up x) as one launch on
     o's output (p8x_mul_mat_vec_glu), down on that (the next layer's input); then the head shards as one launch on
@@ -337,9 +337,11 @@ def measure_dependent_step(tensors, kinds, stream, steps):
         p8x.mul_mat_vec_multi_dev(head, cur, yh, stream=s)
 
     eager_ms = timed_steps(lambda: enqueue(stream), stream, 3, steps)
-    graph = p8x.Graph(enqueue, stream)
-    g_ms = timed_steps(lambda: graph.launch(stream), stream, 3, steps)
-    graph.release()
+    g_ms = None
+    if graph_replay:
+        graph = p8x.Graph(enqueue, stream)
+        g_ms = timed_steps(lambda: graph.launch(stream), stream, 3, steps)
+        graph.release()
     # the same chain as one cooperative launch (p8x_step): stages separated by grid barriers
     chain = []
     for qkv, xin, yqkv, (o, xo, yo), (gate, up, xg, yg), (down, xd, yd) in plan:
@@ -352,7 +354,8 @@ def measure_dependent_step(tensors, kinds, stream, steps):
     step.release()
     step_bytes = sum(t.stream_bytes for t in tensors)
     launches = 4 * nl + 1
-    log(f"dependent step: eager {eager_ms * 1e3:.0f} us, graph {g_ms * 1e3:.0f} us ({launches} launches), "
+    gtxt = f"graph {g_ms * 1e3:.0f} us" if g_ms is not None else "graph not replayed"
+    log(f"dependent step: eager {eager_ms * 1e3:.0f} us, {gtxt} ({launches} launches), "
         f"one launch {s_ms * 1e3:.0f} us ({sinfo['grid']} workgroups, {sinfo['stages']} stages)")
     for b in bufs:
         b.free()
@@ -360,7 +363,7 @@ def measure_dependent_step(tensors, kinds, stream, steps):
                         "shards in one launch; each launch reads its producer's output", "launches": launches,
             "step_kernel": {"ms_per_step": round(s_ms, 4), "GB/s": round(step_bytes / (s_ms * 1e-3) / 1e9, 1),
                             "stages": sinfo["stages"], "workgroups": sinfo["grid"]},
-            "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)},
+            "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)} if g_ms else None,
             "eager": {"ms_per_step": round(eager_ms, 4), "GB/s": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)}}
 
 
@@ -447,7 +450,7 @@ def main():
     ap.add_argument("--no-dependent", action="store_true", help="skip the dependency-respecting decode step")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM and dequantize measurements")
     ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
-    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replays (per-linear and dependent steps)")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replays of the per-linear and dependent steps (the one-launch step still runs)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -473,8 +476,8 @@ def main():
     # step, the prompt GEMM and dequantize; reported beside the headline and timed before it
     per_linear = measure_per_linear(tensors, kinds, xs, ybufs, stream, step_bytes, max(3, args.steps // 3),
                                     not args.no_graph) if not args.no_per_linear else None
-    dependent = measure_dependent_step(tensors, kinds, stream, max(5, args.steps // 4)) \
-        if not (args.no_dependent or args.no_graph) else None
+    dependent = measure_dependent_step(tensors, kinds, stream, max(5, args.steps // 4), not args.no_graph) \
+        if not args.no_dependent else None
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
 
