@@ -30,9 +30,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int kMmRows = 256;     // weight rows per workgroup tile (4 waves x 2 row groups)
 constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles of 32)
-constexpr int kMmThreads = 256;
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the
@@ -133,6 +131,10 @@ __device__ __forceinline__ half8v decode_pair(const AnySlice<NWMAX> &ls, const u
 constexpr int kMmCmC3 = 1 << 3, kMmCmAll = 0xFE;
 constexpr int kMmMain = 3;   // the class with a branch-free path in every instantiation (the 2-bit bulk)
 __host__ __device__ constexpr int mm_nwmax(int cm) { return cm == kMmCmC3 ? 8 : 24; }
+// Waves per workgroup (each: 64 weight rows x 128 tokens, 128 accumulator registers): the class-3 kernel fits in 256
+// registers per wave and runs two waves per SIMD (one's decode overlaps the other's MFMAs) in 8-wave workgroups of
+// 512 rows that share the x' tile and the table; the every-class kernel needs more and runs one wave per SIMD.
+__host__ __device__ constexpr int mm_waves(int cm) { return cm == kMmCmC3 ? 8 : 4; }
 
 template <int CM, int NWMAX>
 __device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
@@ -154,12 +156,15 @@ __device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, c
 // 16 consecutive tokens cover all 64 banks once.
 constexpr int kMmXsHalfs = kMmTok * 128;
 
-// Stage half sh of block b: instruction i of wave w fills token rows 4 (8 w + i) + (0..3); lane l lands at the
-// instruction's LDS base + 16 l (direct-to-LDS), i.e. row + (l >> 4), position l & 15.
+// Stage half sh of block b: with IPW = 128 / (4 NWAVES) instructions per wave, instruction i of wave w fills token
+// rows 4 (IPW w + i) + (0..3); lane l lands at the instruction's LDS base + 16 l (direct-to-LDS), i.e. row + (l >> 4),
+// position l & 15.
+template <int NWAVES>
 __device__ __forceinline__ void mm_stage(const MmJob &J, _Float16 *xb, int tok0, int b, int sh, int w, int lane) {
+    constexpr int IPW = kMmTok / (4 * NWAVES);   // instructions per wave
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int row = 4 * (8 * w + i), t = row + (lane >> 4);
+    for (int i = 0; i < IPW; ++i) {
+        const int row = 4 * (IPW * w + i), t = row + (lane >> 4);
         const int ts = min(tok0 + t, J.N - 1);   // rows past N repeat the last token (never written out)
         const int c = (lane & 15) ^ (t & 15);
         const _Float16 *src = J.xr + (size_t)ts * J.K + 256 * b + 128 * (c >> 3) + 64 * sh + 8 * (c & 7);
@@ -267,13 +272,13 @@ __device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const A
     }
 }
 
-// One 4-wave workgroup per CU (each wave: 64 weight rows x 128 tokens, 128 accumulator registers). K advances
-// by half-blocks; the x' of the next half-block and the next block's payload are in flight while the current
+// One workgroup per CU of mm_waves(CM) waves (each: 64 weight rows x 128 tokens, 128 accumulator registers). K
+// advances by half-blocks; the x' of the next half-block and the next block's payload are in flight while the current
 // half-block is multiplied.
 template <int CM>
-__global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(64 * mm_waves(CM)) __attribute__((amdgpu_waves_per_eu(mm_waves(CM) / 4, mm_waves(CM) / 4)))
 void k_mm(MmJob J) {
-    constexpr int NWMAX = mm_nwmax(CM);
+    constexpr int NWMAX = mm_nwmax(CM), NWAVES = mm_waves(CM), kMmThreads = 64 * NWAVES, kMmRows = 64 * NWAVES;
     __shared__ uint32_t tab[kTabWords];   // first: LDS address 0, replicated coset table (bytes offset by 128)
     __shared__ __attribute__((aligned(16))) _Float16 xs0[kMmXsHalfs];   // half 0 of a block
     __shared__ __attribute__((aligned(16))) _Float16 xs1[kMmXsHalfs];   // half 1
@@ -309,7 +314,7 @@ void k_mm(MmJob J) {
     AnySlice<NWMAX> ls[2];
     AnyRaw<NWMAX> raw[2];
     int cl[2], ncl[2];
-    mm_stage(J, xs0, tok0, b0, 0, w, lane);
+    mm_stage<NWAVES>(J, xs0, tok0, b0, 0, w, lane);
     mm_issue<CM>(J, raw, cl, g, b0, j, kh);
     __builtin_amdgcn_s_waitcnt(0);
     mm_prepare<CM>(ls, cl, raw, j);
@@ -317,12 +322,12 @@ void k_mm(MmJob J) {
     // The two x' buffers are separate LDS objects named statically (half 0 always in xs0, half 1 in xs1), so
     // the compiler can tell the operand reads from the in-flight direct-to-LDS writes and does not wait for them.
     for (int b = b0; b < b1; ++b) {
-        mm_stage(J, xs1, tok0, b, 1, w, lane);
+        mm_stage<NWAVES>(J, xs1, tok0, b, 1, w, lane);
         if (b + 1 < b1) mm_issue<CM>(J, raw, ncl, g, b + 1, j, kh);
         mm_half<CM>(xs0, ls, cl, tab, bankbytes, 0, j, kh, acc);
         __builtin_amdgcn_s_waitcnt(0);   // half 1 of b landed (and the next block's payload)
         __syncthreads();
-        if (b + 1 < b1) mm_stage(J, xs0, tok0, b + 1, 0, w, lane);
+        if (b + 1 < b1) mm_stage<NWAVES>(J, xs0, tok0, b + 1, 0, w, lane);
         mm_half<CM>(xs1, ls, cl, tab, bankbytes, 1, j, kh, acc);
         __builtin_amdgcn_s_waitcnt(0);   // half 0 of b + 1 landed
         if (b + 1 < b1) {
@@ -413,12 +418,21 @@ struct MmPlan {
     int tiles_m, tiles_n, nsplit, kper;
 };
 
-// One workgroup per CU. Estimated time = rounds of workgroups x blocks per workgroup x ~3.4 us (one block of a
-// 256 x 128 tile at about half the MFMA rate) + the sorted-plane traffic of k_mm_finish (written once, read
-// once, ~5 TB/s) when planes are used (K split, or rows to un-permute).
+// One workgroup per CU. Estimated time = rounds of workgroups x blocks per workgroup x the time of one block of a
+// workgroup tile (a relative model: 256 x 128 for the every-class kernel, 512 x 128 at two waves per SIMD for the
+// class-3 one) + the sorted-plane traffic of k_mm_finish (written once, read once, ~5 TB/s) when planes are used (K
+// split, or rows to un-permute).
+static bool mm_only_c3(const p8x_tensor *t) {
+    for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) return false;
+    return true;
+}
+
 static MmPlan mm_plan(const p8x_tensor *t, int N) {
     MmPlan p;
-    p.tiles_m = (t->rows + kMmRows - 1) / kMmRows;
+    const bool c3 = mm_only_c3(t);
+    const int rows_tile = 64 * mm_waves(c3 ? kMmCmC3 : kMmCmAll);
+    const double block_us = c3 ? 4.9 : 3.4;   // one K block of one workgroup tile
+    p.tiles_m = (t->rows + rows_tile - 1) / rows_tile;
     p.tiles_n = (N + kMmTok - 1) / kMmTok;
     const long base = (long)p.tiles_m * p.tiles_n, slots = num_cus();
     const double plane_us = 2.0 * 4.0 * N * t->rows / 5e6;
@@ -426,7 +440,7 @@ static MmPlan mm_plan(const p8x_tensor *t, int N) {
     p.nsplit = 1; p.kper = t->nb;
     for (int ns = 1; ns <= std::min(t->nb, 16); ++ns) {
         const int kper = (t->nb + ns - 1) / ns, nsr = (t->nb + kper - 1) / kper;
-        const double cost = (double)((base * nsr + slots - 1) / slots) * kper * 3.4 + ((nsr > 1 || !t->prm_identity) ? nsr * plane_us : 0.0);
+        const double cost = (double)((base * nsr + slots - 1) / slots) * kper * block_us + ((nsr > 1 || !t->prm_identity) ? nsr * plane_us : 0.0);
         if (best < 0 || cost < best) { best = cost; p.nsplit = nsr; p.kper = kper; }
     }
     return p;
@@ -469,10 +483,8 @@ static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, in
     J.N = N; J.rows = t->rows; J.K = t->K; J.nb = t->nb; J.ng = t->ng;
     J.tiles_m = p.tiles_m; J.tiles_n = p.tiles_n; J.nsplit = p.nsplit; J.kper = p.kper; J.direct = direct;
     const int grid = ((p.tiles_m * p.tiles_n * p.nsplit + kXcds - 1) / kXcds) * kXcds;
-    bool only_c3 = true;
-    for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) only_c3 = false;
-    if (only_c3) hipLaunchKernelGGL(k_mm<kMmCmC3>, dim3(grid), dim3(kMmThreads), 0, st, J);
-    else hipLaunchKernelGGL(k_mm<kMmCmAll>, dim3(grid), dim3(kMmThreads), 0, st, J);
+    if (mm_only_c3(t)) hipLaunchKernelGGL(k_mm<kMmCmC3>, dim3(grid), dim3(64 * mm_waves(kMmCmC3)), 0, st, J);
+    else hipLaunchKernelGGL(k_mm<kMmCmAll>, dim3(grid), dim3(64 * mm_waves(kMmCmAll)), 0, st, J);
     if ((rc = hip_check(hipGetLastError(), "k_mm launch"))) return rc;
     if (!direct) {
         const size_t lds = 4 * (size_t)t->rows;   // rows < 32768: at most 128 KB
