@@ -203,6 +203,10 @@ int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
 /* the launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV (sorted-row
  * partials per K-chunk and column), 2 = partials to original rows with the clamp delta */
 int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream);
+/* No counterpart in the reference; for callers that time the batch's kernels themselves: the same, with hipEvent_t
+ * ev_start / ev_stop (either may be NULL) recorded by the runtime at the stage kernel's own start and end
+ * (hipExtLaunchKernel), so their elapsed time is the kernel's duration without the queue work around it. */
+int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *stream, void *ev_start, void *ev_stop);
 void p8x_gemv_batch_release(p8x_gemv_batch *b);
 /* The launch plan of a batch: work units (a 32-row group over a K-chunk), jobs cut along K, waves of the launch,
  * class_set (bit c: tile class c is decoded), small_launch = 1 when the batch had fewer whole-K units than two

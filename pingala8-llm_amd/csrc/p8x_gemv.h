@@ -11,6 +11,7 @@
 // row group through a fixed-order fix-up by the last-arriving wave, so results are deterministic (the
 // reference accumulates with float atomics, CPU.patch:4014).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -961,10 +962,15 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, const uint32_t *__restrict__ 
     }
 }
 
+// e0 / e1 (optional): HIP events the runtime records at the kernel's own start and end (hipExtLaunchKernel)
 template <int CM, int NCOL>
-static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st) {
+static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
+                              hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
     const int grid = wave_wg_per_cu(CM, NCOL) * num_cus();
-    hipLaunchKernelGGL((k_gemv_wave<CM, NCOL>), dim3(grid), dim3(64 * wave_waves(CM, NCOL)), 0, st, jobs, ujob, units, ctr, a2);
+    if (e0 || e1)
+        hipExtLaunchKernelGGL((k_gemv_wave<CM, NCOL>), dim3(grid), dim3(64 * wave_waves(CM, NCOL)), 0, st, e0, e1, 0, jobs, ujob, units, ctr, a2);
+    else
+        hipLaunchKernelGGL((k_gemv_wave<CM, NCOL>), dim3(grid), dim3(64 * wave_waves(CM, NCOL)), 0, st, jobs, ujob, units, ctr, a2);
     return hip_check(hipGetLastError(), "k_gemv_wave launch");
 }
 
@@ -979,6 +985,7 @@ int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t l
                     RgJobs &R, int &cm, int &ng);
 int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what);
 int class_set(const size_t hist[8]);
-int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st);
+int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
+                     hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 }  // namespace p8x

@@ -638,21 +638,35 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
 }
 
 int p8x_gemv_batch_run_stage(const p8x_gemv_batch *b, int stage, void *stream) {
+    return p8x_gemv_batch_run_stage_timed(b, stage, stream, nullptr, nullptr);
+}
+
+int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *stream, void *ev_start, void *ev_stop) {
     if (!b) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run: null batch");
     hipStream_t st = (hipStream_t)stream;
+    hipEvent_t e0 = (hipEvent_t)ev_start, e1 = (hipEvent_t)ev_stop;
     if (stage == 0) {
-        hipLaunchKernelGGL(k_act_q8_128_batch, dim3((b->total_blocks + 3) / 4, b->ncols), dim3(256), 0, st, (const ActJob *)b->d_act,
-                           (const uint32_t *)b->d_ablk, b->total_blocks);
+        const dim3 grid((b->total_blocks + 3) / 4, b->ncols);
+        if (e0 || e1)
+            hipExtLaunchKernelGGL(k_act_q8_128_batch, grid, dim3(256), 0, st, e0, e1, 0, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk,
+                                  b->total_blocks);
+        else
+            hipLaunchKernelGGL(k_act_q8_128_batch, grid, dim3(256), 0, st, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
         return hip_check(hipGetLastError(), "k_act_q8_128_batch launch");
     }
     if (stage == 1) {
-        return launch_gemv_wave(b->ncols, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st);
+        return launch_gemv_wave(b->ncols, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
     }
     if (stage == 2) {   // partial rows to original rows with the clamp delta
         // the delta blocks first, padded to a multiple of the XCD count so plain block 8k + x still lands on XCD x
         const int ndblk = (b->fin_ndrows + 255) / 256, ndpad = (ndblk + kXcds - 1) / kXcds * kXcds;
-        hipLaunchKernelGGL(k_gemv_finish, dim3(ndpad + b->fin_blocks), dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk,
-                           ndpad, (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
+        const dim3 grid(ndpad + b->fin_blocks);
+        if (e0 || e1)
+            hipExtLaunchKernelGGL(k_gemv_finish, grid, dim3(256), 0, st, e0, e1, 0, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk, ndpad,
+                                  (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
+        else
+            hipLaunchKernelGGL(k_gemv_finish, grid, dim3(256), 0, st, (const FinishJob *)b->d_fin, (const uint32_t *)b->d_fblk, ndpad,
+                               (const FinDelta *)b->d_fdrows, (const FinEntry *)b->d_fent, b->fin_ndrows);
         return hip_check(hipGetLastError(), "k_gemv_finish launch");
     }
     return set_error(P8X_ERR_ARG, "p8x_gemv_batch_run_stage: stage %d", stage);

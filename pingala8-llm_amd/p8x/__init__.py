@@ -23,6 +23,7 @@ EXPORTS = [
     "p8x_tensor_info", "p8x_dequantize", "p8x_decode_rotated", "p8x_quantize_q8_128", "p8x_quantize_q8_1",
     "p8x_vec_dot", "p8x_mul_mat_vec", "p8x_mul_mat_vec_act", "p8x_mul_mat", "p8x_mul_mat_reserve", "p8x_synth_random",
     "p8x_quantize_tensor", "p8x_slot_bytes", "p8x_gemv_batch_create", "p8x_gemv_batch_run", "p8x_gemv_batch_run_stage",
+    "p8x_gemv_batch_run_stage_timed",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_decode_tiles",
@@ -126,6 +127,7 @@ def lib():
     L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
+    L.p8x_gemv_batch_run_stage_timed.argtypes = [vp, i, vp, vp, vp]
     L.p8x_gemv_batch_release.argtypes = [vp]; L.p8x_gemv_batch_release.restype = None
     L.p8x_gemv_batch_info.argtypes = [vp, ctypes.POINTER(BatchInfo)]
     _lib = L
@@ -765,8 +767,13 @@ class GemvBatch:
     def run(self, stream=None):
         check(lib().p8x_gemv_batch_run(self.h, stream.h if stream else None), "p8x_gemv_batch_run")
 
-    def run_stage(self, stage, stream=None):
-        check(lib().p8x_gemv_batch_run_stage(self.h, stage, stream.h if stream else None), "p8x_gemv_batch_run_stage")
+    def run_stage(self, stage, stream=None, events=None):
+        """events = (start, stop) Event pair recorded at the stage kernel's own start and end"""
+        if events is None:
+            check(lib().p8x_gemv_batch_run_stage(self.h, stage, stream.h if stream else None), "p8x_gemv_batch_run_stage")
+        else:
+            check(lib().p8x_gemv_batch_run_stage_timed(self.h, stage, stream.h if stream else None, events[0].h, events[1].h),
+                  "p8x_gemv_batch_run_stage_timed")
 
     def release(self):
         if self.h:

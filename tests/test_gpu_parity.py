@@ -263,6 +263,39 @@ def test_batch_matches_single(ncols):
                 assert rel_l2(Y[n], orcs[i].gemv_f64(hx[i][n])) < 1e-5, (i, n, rep)
 
 
+@pytest.mark.parametrize("ncols", [1, 2])
+def test_batch_timed_stages_match_run(ncols):
+    """p8x_gemv_batch_run_stage_timed: the three stages with kernel-attached events give the bits of
+    p8x_gemv_batch_run, and each event pair spans a positive time no longer than the whole step"""
+    shapes = [(1024, 4096), (4096, 1024), (256, 14336)]
+    rng = np.random.default_rng(60 + ncols)
+    tensors, xs, ys = [], [], []
+    for i, (rows, K) in enumerate(shapes):
+        tensors.append(p8x.Tensor(p8x.synth_random(90 + i, rows, K, nd=2), rows, K))
+        xs.append(p8x.DeviceBuffer.from_numpy(rng.standard_normal((ncols, K)).astype(np.float32)))
+        ys.append(p8x.DeviceBuffer(4 * ncols * rows))
+    batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols)
+    stream = p8x.Stream()
+    batch.run(stream)
+    stream.sync()
+    want = [y.to_numpy(np.float32, (ncols * r,)).copy() for y, (r, _) in zip(ys, shapes)]
+    for y in ys:
+        y.fill(0xFF)
+    ev = [(p8x.Event(), p8x.Event()) for _ in range(3)]
+    a, b = p8x.Event(), p8x.Event()
+    a.record(stream)
+    for stage in range(3):
+        batch.run_stage(stage, stream, events=ev[stage])
+    b.record(stream)
+    stream.sync()
+    for y, w, (r, _) in zip(ys, want, shapes):
+        assert np.array_equal(y.to_numpy(np.float32, (ncols * r,)).view(np.uint32), w.view(np.uint32))
+    whole = a.elapsed_ms(b)
+    for s, t in ev:
+        assert 0.0 < s.elapsed_ms(t) <= whole
+    batch.release()
+
+
 @pytest.mark.parametrize("one_block", [False, True])
 @pytest.mark.parametrize("cp", [(0, 0, 0, 1, 0, 0, 0, 0), (0, 0, 0, 0, 0, 0, 1, 0), (0, 0, 1, 6, 1, 0, 0, 0)])
 def test_batch_one_column_class_sets(cp, one_block):
