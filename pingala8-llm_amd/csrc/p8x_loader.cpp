@@ -194,6 +194,7 @@ static int parse_gguf(p8x_vr_file *F, int fi, const char *path, bool keep_kv) {
     const uint64_t data = (r.pos() + alignment - 1) / alignment * alignment;
     for (auto &it : infos) {
         GgufTensor &t = it.second;
+        if (t.offset > UINT64_MAX - data) return fail("p8x_vr_open: tensor '%s' has a data offset past any file", it.first);
         t.offset += data;
         const int eb = elem_bytes(t.type);
         if (eb) {
