@@ -8,7 +8,7 @@
 // so the f32 result is bit-identical (no contraction: built with -ffp-contract=off); f16/bf16 are the
 // hardware round-to-nearest-even conversions of that f32.
 //
-// Each wave walks tiles with the next tile's payload already in flight (rotated loads into registers), so
+// Each wave walks tiles with the next tile's payload already in flight (loads into registers), so
 // the decode of one tile overlaps the memory latency of the next.
 #include <hip/hip_runtime.h>
 
@@ -147,7 +147,7 @@ __device__ __forceinline__ void walk_tiles(const DecodeArgs &a, size_t first, si
     issue(first);
     for (size_t q = first; q < last; q += stride) {
         AnySlice<NW> ls;
-        prepare_any<CM>(ls, nx.c, nx.raw, j);   // consumes this tile's words
+        prepare_any<CM>(ls, nx.c, nx.raw);   // consumes this tile's words
         const int c = nx.c, ro = nx.ro & 0x7FFF;
         int e0 = 0, e1 = 0;
         if (want_rows && (nx.ro & 0x8000)) { e0 = a.cp[ro]; e1 = a.cp[ro + 1]; }
@@ -329,8 +329,8 @@ __device__ __forceinline__ uint2 fwht4_entry(uint32_t w) {
 }
 
 // Payload words of lane-slice (hs, j) of a class-C tile, loaded so that after the bit rotation of lo_decode the
-// lane's fields are in chunk order starting at chunk 16 p: the stored field k is chunk (j + k) & 31, so the
-// bitstring is rotated right by d = (16 p - j) & 31 fields (whole words here, the rest in lo_decode).
+// lane's fields start at chunk 16 p: the stored field k is chunk k, so the bitstring is rotated right by d = 16 p
+// fields (whole words here, the rest in lo_decode).
 template <int C>
 __device__ __forceinline__ void lo_load(uint32_t (&w)[8], const uint32_t *__restrict__ p, int j, int d) {
     constexpr int W1 = w1_of(C), NW = nw_of(C);
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
     __shared__ __align__(16) uint32_t stg[kLoWaves][32 * kLoBandWords];   // one 32-row x 128-byte band per wave
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, p = lane >> 5, p16 = 16 * p;
-    const int d = (p16 - j) & 31;
+    const int d = p16;
     const s16x2 sg = {(short)(p ? -1 : 1), (short)(p ? -1 : 1)};
     for (int i = tid; i < 512; i += kLoThreads) tab4[i] = fwht4_entry(a.a2[(i & 1) * 256 + (i >> 1)]);
     __syncthreads();

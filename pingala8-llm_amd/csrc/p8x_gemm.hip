@@ -193,11 +193,11 @@ __device__ __forceinline__ void mm_issue(const MmJob &J, AnyRaw<NWMAX> (&raw)[2]
 
 // decode the raw words into the slices the products read (after the loads have landed)
 template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const AnyRaw<NWMAX> (&raw)[2], int j) {
+__device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const AnyRaw<NWMAX> (&raw)[2]) {
 #pragma unroll
     for (int tj = 0; tj < 2; ++tj) {
-        if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj], j);   // zero raw words, S = 0: zero weights
-        else prepare_any<CM>(ls[tj], cl[tj], raw[tj], j);
+        if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj]);   // zero raw words, S = 0: zero weights
+        else prepare_any<CM>(ls[tj], cl[tj], raw[tj]);
     }
 }
 
@@ -317,7 +317,7 @@ void k_mm(MmJob J) {
     mm_stage<NWAVES>(J, xs0, tok0, b0, 0, w, lane);
     mm_issue<CM>(J, raw, cl, g, b0, j, kh);
     __builtin_amdgcn_s_waitcnt(0);
-    mm_prepare<CM>(ls, cl, raw, j);
+    mm_prepare<CM>(ls, cl, raw);
     __syncthreads();   // table and the first half-block's x' are in LDS
     // The two x' buffers are separate LDS objects named statically (half 0 always in xs0, half 1 in xs1), so
     // the compiler can tell the operand reads from the in-flight direct-to-LDS writes and does not wait for them.
@@ -332,7 +332,7 @@ void k_mm(MmJob J) {
         __builtin_amdgcn_s_waitcnt(0);   // half 0 of b + 1 landed
         if (b + 1 < b1) {
             cl[0] = ncl[0]; cl[1] = ncl[1];
-            mm_prepare<CM>(ls, cl, raw, j);
+            mm_prepare<CM>(ls, cl, raw);
         }
         __syncthreads();
     }

@@ -49,10 +49,11 @@ struct GemvJob {
     int g0, gend, prows;             // task kernel: row groups g0 .. gend - 1; partials rows (32 g0 ..) with row stride prows
 };
 
-// LDS activation bytes per task: ncol x kchunk x 512. The step-order kernels keep each 128-column half of a
-// block twice in a row ([n][block][half][64 words], word i = chunk i & 31), so lane j reads its chunks
-// (j + k) & 31 for k = 0..31 at the unwrapped word offsets j + k; the other kernels use the first half.
-// Sized so that two workgroups (64 KB table + this + scales each) share one CU's 160 KB.
+// LDS activation bytes per task: ncol x kchunk x 512. The 16-byte-load kernels keep each 128-column half of a
+// block at [n][block][half][64 words] (word i = chunk i, the second 32 words a copy that nothing reads; the
+// staging writes whole 256-byte rows); the other kernels use the first half of each row pair. Every lane of a half
+// reads chunk k at word k (a broadcast). Sized so that two workgroups (64 KB table + this + scales each) share one
+// CU's 160 KB.
 constexpr int kXBytes = 15360;
 
 __host__ __device__ constexpr int kchunk_max(int ncol) { return kXBytes / (512 * ncol); }
@@ -62,7 +63,7 @@ struct GemvSmem {
     static constexpr int kScales = NCOL * (ACT == P8X_ACT_Q8_128 ? 2 : 8) * kchunk_max(NCOL);
     static constexpr int kXW = kXBytes / 4 / NCOL, kNSC = kScales / NCOL;   // per-column strides of xq, xd
     uint32_t tab[kTabWords];   // first member: LDS address 0, so table addresses need no base add
-    uint32_t xq[kXBytes / 4];  // [ncol][kchunk][2][64] words (step order) or [ncol][kchunk][64] words
+    uint32_t xq[kXBytes / 4];  // [ncol][kchunk][2][64] words (16-byte-load kernels) or [ncol][kchunk][64] words
     float xd[kScales];         // [ncol][scales of the chunk]
 };
 
@@ -72,7 +73,7 @@ struct GemvSmem {
 constexpr int kCmC3 = 1 << 3, kCmC6 = 1 << 6, kCmC234 = (1 << 2) | (1 << 3) | (1 << 4), kCmC2346 = kCmC234 | (1 << 6), kCmAll = 0xFE;
 
 // Waves per workgroup (each owns one row group of a task) and the waves per SIMD the registers are sized for.
-// LDS holds two workgroups per CU; a variant that fits 64 VGPRs (one column, class 3, step order) runs
+// LDS holds two workgroups per CU; a variant that fits 64 VGPRs (one column, class 3, 16-byte loads) runs
 // 16-wave workgroups, 8 waves per SIMD; the others 8-wave workgroups at 4 (<= 128 VGPRs) or 2 waves per SIMD.
 __host__ __device__ constexpr int gemv_waves(int ncol, int act, bool partials, int cm) {
     return ncol == 1 && act == P8X_ACT_Q8_128 && !partials && cm == kCmC3 ? 16 : 8;
@@ -89,12 +90,12 @@ struct TaskCtx {
     const GemvJob *J;   // the task's descriptor (kernel argument, or a copy of the launch's job array entry)
     int g, b0, nbl, hs, j;
     uint32_t bankbytes;
-    int xlane;          // step order: the lane's word offset hs * 64 + j in a block's activation words
+    int xlane;          // 16-byte-load kernels: the half's word offset hs * 64 in a block's activation words
 };
 
-// Q8_128 activations without integer partials run in step order (natural, coalesced payload loads)
+// Q8_128 activations without integer partials load the payload in 16-byte groups (whole lines per instruction)
 template <int ACT, bool PARTIALS>
-__host__ __device__ constexpr bool gemv_step_order() { return ACT == P8X_ACT_Q8_128 && !PARTIALS; }
+__host__ __device__ constexpr bool gemv_quad_loads() { return ACT == P8X_ACT_Q8_128 && !PARTIALS; }
 
 template <int NCOL, int ACT, bool PARTIALS, int C, typename SM>
 __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const SM &sm, const RawSlice<C> &raw, int b, float (&yacc)[NCOL]) {
@@ -103,7 +104,7 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const SM 
     constexpr int XW = SM::kXW;                            // LDS words per column
     constexpr int NSC = SM::kNSC;
     LaneSlice<C> ls;
-    ls.from_raw(raw, c.j);
+    ls.from_raw(raw);
     ls.prepare(c.bankbytes);
     const int bl = b - c.b0;
     int acc[NST][NCOL][NSUB];
@@ -156,17 +157,15 @@ __device__ __forceinline__ void gemv_tile(const TaskCtx<NCOL, ACT> &c, const SM 
     }
 }
 
-// One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
-// order, only summed in another order.
 using lds_cptr = __attribute__((address_space(3))) const uint32_t *;
 
-// Integer sums of one tile in step order: lane (hs, j) reads its activation chunk (j + k) & 31 of column n at
-// xl[n * XW + k] (each 128-column half kept twice in a row), and looks up the codewords in the table at LDS 0.
+// Integer sums of one tile from 16-byte-group payload loads: every lane of a half reads activation chunk k of
+// column n at xl[n * XW + k] (four chunks as one 16-byte LDS broadcast read), and looks up the codewords in the
+// table at LDS 0.
 template <int NCOL, int C, int XW>
-__device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C> &raw, int j, uint32_t bankbytes, lds_cptr xl,
-                                          int (&isum)[NCOL]) {
+__device__ __forceinline__ void quad_isum(const uint32_t *tab, const QuadSlice<C> &raw, uint32_t bankbytes, lds_cptr xl, int (&isum)[NCOL]) {
     constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
-    const uint32_t H = raw.coset_bits(j);
+    const uint32_t H = raw.coset_bits();
     int acc[NST][NCOL];
 #pragma unroll
     for (int s = 0; s < NST; ++s)
@@ -174,11 +173,10 @@ __device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C
         for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        uint32_t xv[NCOL][4];
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 xv[NCOL];
 #pragma unroll
-        for (int n = 0; n < NCOL; ++n)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) xv[n][e] = xl[n * XW + 4 * q + e];
+        for (int n = 0; n < NCOL; ++n) xv[n] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(xl + n * XW + 4 * q);
         const uint32_t hq = coset_bytes(H, bankbytes, q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -188,11 +186,13 @@ __device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C
             if constexpr (NST > 1) w[1] = lds_word(tab, raw.template addr<1>(k, hq));
             if constexpr (NST > 2) w[2] = lds_word(tab, raw.template addr<2>(k, hq));
 #pragma unroll
-            for (int n = 0; n < NCOL; ++n)
+            for (int n = 0; n < NCOL; ++n) {
+                const uint32_t xc = e == 0 ? xv[n].x : e == 1 ? xv[n].y : e == 2 ? xv[n].z : xv[n].w;
 #pragma unroll
-                for (int s = 0; s < NST; ++s) acc[s][n] = __builtin_amdgcn_sdot4((int)w[s], (int)xv[n][e], acc[s][n], false);
+                for (int s = 0; s < NST; ++s) acc[s][n] = __builtin_amdgcn_sdot4((int)w[s], (int)xc, acc[s][n], false);
+            }
         }
-        __asm__ volatile("" ::: "memory");   // one group of 4 steps at a time: bounds the live registers
+        __asm__ volatile("" ::: "memory");   // one group of 4 chunks at a time: bounds the live registers
     }
 #pragma unroll
     for (int n = 0; n < NCOL; ++n) {
@@ -202,10 +202,9 @@ __device__ __forceinline__ void step_isum(const uint32_t *tab, const StepSlice<C
     }
 }
 
-// One tile in step order (8-bit-per-128 activations, no partials): the integer sums are the same as in chunk
-// order, only summed in another order.
+// One tile from 16-byte-group payload loads (8-bit-per-128 activations, no partials)
 template <int NCOL, int C, typename SM>
-__device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const SM &sm, const StepSlice<C> &raw, int b,
+__device__ __forceinline__ void gemv_tile_quad(const TaskCtx<NCOL, P8X_ACT_Q8_128> &c, const SM &sm, const QuadSlice<C> &raw, int b,
                                                float (&yacc)[NCOL]) {
     constexpr int XW = SM::kXW;
     constexpr int NSC = SM::kNSC;
@@ -215,7 +214,7 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
     lds_cptr xl = (lds_cptr)(sm.xq + bl * 128 + c.xlane);
     __asm__ volatile("" : "+v"(xl));
     int isum[NCOL];
-    step_isum<NCOL, C, XW>(sm.tab, raw, c.j, c.bankbytes, xl, isum);
+    quad_isum<NCOL, C, XW>(sm.tab, raw, c.bankbytes, xl, isum);
     const float sc = half_to_float(raw.s);
 #pragma unroll
     for (int n = 0; n < NCOL; ++n) yacc[n] += ((float)isum[n] * sm.xd[n * NSC + 2 * bl + c.hs]) * sc;
@@ -230,14 +229,14 @@ __device__ __forceinline__ void gemv_tile_step(const TaskCtx<NCOL, P8X_ACT_Q8_12
 template <int NCOL, int ACT, bool PARTIALS, int C, int NBUF, bool ONLY_C>
 struct GemvRun {
     static constexpr int NW = nw_of(C);
-    static constexpr bool STEP = gemv_step_order<ACT, PARTIALS>();
-    using Slice = std::conditional_t<STEP, StepSlice<C>, RawSlice<C>>;
+    static constexpr bool QUAD = gemv_quad_loads<ACT, PARTIALS>();
+    using Slice = std::conditional_t<QUAD, QuadSlice<C>, RawSlice<C>>;
     Slice buf[NBUF];
     int b, e;
     uint32_t wn;   // tile word of the next prefetch, read one step ahead so its scalar load is never waited on at once
-    // lane part of the payload offsets: one base (step order) or the NW rotated word offsets
-    std::conditional_t<STEP, uint32_t, uint32_t[NW]> vo;
-    uint32_t vp;   // step order: the lane's trailing-pair offset (classes with NW % 4 == 2)
+    // lane part of the payload offsets: one base (16-byte groups) or the NW word offsets
+    std::conditional_t<QUAD, uint32_t, uint32_t[NW]> vo;
+    uint32_t vp;   // 16-byte groups: the lane's trailing-pair offset (classes with NW % 4 == 2)
     uint32_t vs;
 
     __device__ __forceinline__ kptr<const uint32_t> mrow(const TaskCtx<NCOL, ACT> &c) const {
@@ -251,7 +250,7 @@ struct GemvRun {
         const uint32_t soff = ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
         const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
         __builtin_amdgcn_s_setprio(2);   // loads issued at raised priority (see wave_run)
-        if constexpr (STEP) r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        if constexpr (QUAD) r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         else r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         __builtin_amdgcn_s_setprio(0);
         wn = mrow(c)[min(ta + 1, e - 1)];
@@ -263,9 +262,9 @@ struct GemvRun {
             e = b + 1;
             while (e < bend && (mrow(c)[e] >> 29) == (uint32_t)C) ++e;
         }
-        if constexpr (STEP) {
-            vo = StepSlice<C>::quad_offset(c.hs, c.j);
-            vp = StepSlice<C>::pair_offset(c.hs, c.j);
+        if constexpr (QUAD) {
+            vo = QuadSlice<C>::quad_offset(c.hs, c.j);
+            vp = QuadSlice<C>::pair_offset(c.hs, c.j);
         } else {
             RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
         }
@@ -279,7 +278,7 @@ struct GemvRun {
         Slice r = r0_;
         pin(r.w);
         pin(r.s);
-        if constexpr (STEP) gemv_tile_step<NCOL, C>(c, sm, r, t, yacc);
+        if constexpr (QUAD) gemv_tile_quad<NCOL, C>(c, sm, r, t, yacc);
         else gemv_tile<NCOL, ACT, PARTIALS, C>(c, sm, r, t, yacc);
     }
     template <typename SM>
@@ -403,7 +402,7 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
     TaskCtx<NCOL, ACT> c;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
-    c.xlane = c.hs * 64 + c.j;
+    c.xlane = c.hs * 64;
     build_coset_table<NT>(sm.tab, a2, tid);
     for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
         const GemvJob &J = job0;
@@ -415,7 +414,7 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
         // stage this task's activations and scales
         __syncthreads();
         bool scales_staged = false;
-        if constexpr (gemv_step_order<ACT, PARTIALS>()) {
+        if constexpr (gemv_quad_loads<ACT, PARTIALS>()) {
             // [n][block][half][64]: word i of a half = activation word (i & 31) of that half
             if (J.q) {
                 for (int i = tid; i < NCOL * c.nbl * 128; i += NT) {
@@ -516,7 +515,7 @@ template <int NCOL, int WAVES = rg_waves(NCOL)>
 struct RgSmem {
     static constexpr int kXW = kRgMaxBlocks * 128 / NCOL, kNSC = 2 * kRgMaxBlocks / NCOL;   // per-column strides
     uint32_t tab[kTabWords];             // LDS address 0
-    uint32_t xq[kRgMaxBlocks * 128];     // [column][block][half][64 words] (step order)
+    uint32_t xq[kRgMaxBlocks * 128];     // [column][block][half][64 words] (word i = chunk i of the half)
     float xd[2 * kRgMaxBlocks];          // [column][block][half]
     float red[2][WAVES][NCOL][32];       // per wave: its K range's row sums (two sets, alternating row groups)
 };
@@ -626,7 +625,7 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
-    c.xlane = c.hs * 64 + c.j;
+    c.xlane = c.hs * 64;
     // workgroup b (of the job's nwg): K-chunk ks = b % nks of row groups b / nks, b / nks + nwg / nks, ...
     const int nks = SPLIT ? J.nks : 1;
     const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
@@ -769,15 +768,16 @@ static int launch_gemv_rg_t(const RgJobs &jobs, int ng, const uint32_t *a2, hipS
 // ------------------------------------------------------------------------------------------------ wave-independent GEMV
 // 1..8 columns of 8-bit-per-128 activations, grouped launches (the decode stream). Each wave is its own worker:
 // it takes a unit (job, row group, K-chunk) from a device counter, streams that row group's tiles, and leaves
-// the sorted-row partials for the finishing launch. It keeps each tile's activation blocks (one per column) in
-// a private LDS slot (loaded with the tile, written twice in a row so step-order reads need no wrap). Nothing
-// waits on another wave after the table is built, so a slow wave delays only its own unit and the launch
-// drains with at most one unit per wave. Units are numbered in job order; the job list is ordered by decreasing
-// unit length, so the long units start first.
+// the sorted-row partials for the finishing launch. Activations never pass through LDS: with the payload in chunk
+// order every lane of a half multiplies chunk k by the same activation word, which the v_dot4 instruction takes
+// straight from a DPP broadcast (row_newbcast) of two registers loaded with the tile; LDS serves the codeword
+// lookups alone. Nothing waits on another wave after the table is built, so a slow wave delays only its own unit
+// and the launch drains with at most one unit per wave. Units are numbered in job order; the job list is ordered
+// by decreasing unit length, so the long units start first.
 // One column of class 3 fits 64 VGPRs: 16-wave workgroups, 8 waves per SIMD; one column of classes 6 or 2-4
 // 8-wave workgroups at 4 (128 VGPRs), every class at 2. Two to four columns of one class: 16-wave workgroups
-// (one per CU, the slots take NCOL x 8 KB) at 4 waves per SIMD; five to eight columns or mixed classes (more
-// than 128 VGPRs): 8-wave workgroups at 2.
+// (one per CU) at 4 waves per SIMD; five to eight columns or mixed classes (more than 128 VGPRs): 8-wave
+// workgroups at 2.
 __host__ __device__ constexpr int wave_waves(int cm, int ncol = 1) {
     return ncol == 1 ? (cm == kCmC3 ? 16 : 8) : ncol <= 4 && (cm == kCmC3 || cm == kCmC6) ? 16 : 8;
 }
@@ -788,53 +788,154 @@ __host__ __device__ constexpr int wave_wg_per_cu(int cm, int ncol = 1) { return 
 // prefetch depth of the class-3 runs (register buffers hold NCOL activation words and scales each)
 __host__ __device__ constexpr int wave_nbuf_c3(int ncol) { return ncol == 1 ? GEMV_NBUF_C3 : 2; }
 
-template <int WAVES, int NCOL>
 struct WaveSmem {
-    uint32_t tab[kTabWords];            // LDS address 0
-    uint32_t xs[WAVES][NCOL * 128];     // per wave: [column][half][64 words], word i = activation word (i & 31)
+    uint32_t tab[kTabWords];   // LDS address 0
 };
 
-// A tile's payload with its activation blocks: per column one word per lane (word `lane` of the block) and the
-// lane's half's scale
+// A tile's payload with its activation words: per column, lane 16 r + i holds words i (xa) and 16 + i (xb) of its
+// half's 32 activation words (half hs = r >> 1, the rows of 16 lanes the DPP broadcast works in), and the half's
+// scale
 template <int C, int NCOL>
 struct WaveSlice {
-    StepSlice<C> p;
-    uint32_t xw[NCOL];
+    QuadSlice<C> p;
+    uint32_t xa[NCOL], xb[NCOL];
     float xd[NCOL];
 };
 
-// One tile of a wave: the activation blocks go to the wave's slot, then the step-order integer sums.
+// acc += dot4(x broadcast from lane B of each 16-lane row, w): v_dot4c_i32_i8 with a DPP row_newbcast source
+// (gfx90a and later), as asm: the compiler does not fold a DPP move into this instruction. Wait states, measured on
+// gfx950 against a CPU sum of the same sequences: these dots chain through their accumulators back to back
+// exactly, but an ordinary VALU instruction that reads a dot's result needs two wait states after it, and a DPP
+// read needs two after a VALU write of its source. Every block therefore starts and ends with s_nop 1 (the asm
+// cannot see which instructions the compiler places around it).
+#define P8X_DL(A, X, W, B) "v_dot4c_i32_i8_dpp %" #A ", %" #X ", %" #W " row_newbcast:" #B " row_mask:0xf bank_mask:0xf\n\t"
+#define P8X_R1(W, B) P8X_DL(0, 1, W, B)
+#define P8X_G1(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R1(2, B0) P8X_R1(3, B1) P8X_R1(4, B2) P8X_R1(5, B3) "s_nop 1"
+#define P8X_R2(W, B) P8X_DL(0, 2, W, B) P8X_DL(1, 3, W, B)
+#define P8X_G2(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R2(4, B0) P8X_R2(5, B1) P8X_R2(6, B2) P8X_R2(7, B3) "s_nop 1"
+#define P8X_R3(W, B) P8X_DL(0, 3, W, B) P8X_DL(1, 4, W, B) P8X_DL(2, 5, W, B)
+#define P8X_G3(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R3(6, B0) P8X_R3(7, B1) P8X_R3(8, B2) P8X_R3(9, B3) "s_nop 1"
+#define P8X_R4(W, B) P8X_DL(0, 4, W, B) P8X_DL(1, 5, W, B) P8X_DL(2, 6, W, B) P8X_DL(3, 7, W, B)
+#define P8X_G4(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R4(8, B0) P8X_R4(9, B1) P8X_R4(10, B2) P8X_R4(11, B3) "s_nop 1"
+#define P8X_R5(W, B) P8X_DL(0, 5, W, B) P8X_DL(1, 6, W, B) P8X_DL(2, 7, W, B) P8X_DL(3, 8, W, B) P8X_DL(4, 9, W, B)
+#define P8X_G5(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R5(10, B0) P8X_R5(11, B1) P8X_R5(12, B2) P8X_R5(13, B3) "s_nop 1"
+#define P8X_R6(W, B) P8X_DL(0, 6, W, B) P8X_DL(1, 7, W, B) P8X_DL(2, 8, W, B) P8X_DL(3, 9, W, B) P8X_DL(4, 10, W, B) P8X_DL(5, 11, W, B)
+#define P8X_G6(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R6(12, B0) P8X_R6(13, B1) P8X_R6(14, B2) P8X_R6(15, B3) "s_nop 1"
+#define P8X_R7(W, B) P8X_DL(0, 7, W, B) P8X_DL(1, 8, W, B) P8X_DL(2, 9, W, B) P8X_DL(3, 10, W, B) P8X_DL(4, 11, W, B) P8X_DL(5, 12, W, B) P8X_DL(6, 13, W, B)
+#define P8X_G7(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R7(14, B0) P8X_R7(15, B1) P8X_R7(16, B2) P8X_R7(17, B3) "s_nop 1"
+#define P8X_R8(W, B) P8X_DL(0, 8, W, B) P8X_DL(1, 9, W, B) P8X_DL(2, 10, W, B) P8X_DL(3, 11, W, B) P8X_DL(4, 12, W, B) P8X_DL(5, 13, W, B) P8X_DL(6, 14, W, B) P8X_DL(7, 15, W, B)
+#define P8X_G8(B0, B1, B2, B3) "s_nop 1\n\t" P8X_R8(16, B0) P8X_R8(17, B1) P8X_R8(18, B2) P8X_R8(19, B3) "s_nop 1"
+
+// one group of four chunks (Q & 3 of the register pair) for every column: acc[n] += sum_e dot4(x[n] from lane
+// 4 Q + e, w[e]), the chunks in order, the columns interleaved
+template <int Q, int NCOL>
+__device__ __forceinline__ void dot4_bcast(int (&a)[NCOL], const uint32_t (&x)[NCOL], const uint32_t (&w)[4]) {
+    static_assert(Q >= 0 && Q < 4 && NCOL >= 1 && NCOL <= 8, "four groups per register pair, 1..8 columns");
+#define P8X_PASS(...) __VA_ARGS__
+#define P8X_GQ(G, OUTS, INS) \
+    if constexpr (Q == 0) __asm__(G(0, 1, 2, 3) : OUTS : INS); \
+    else if constexpr (Q == 1) __asm__(G(4, 5, 6, 7) : OUTS : INS); \
+    else if constexpr (Q == 2) __asm__(G(8, 9, 10, 11) : OUTS : INS); \
+    else __asm__(G(12, 13, 14, 15) : OUTS : INS);
+#define P8X_W "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3])
+    if constexpr (NCOL == 1) {
+        P8X_GQ(P8X_G1, P8X_PASS("+v"(a[0])), P8X_PASS("v"(x[0]), P8X_W))
+    } else if constexpr (NCOL == 2) {
+        P8X_GQ(P8X_G2, P8X_PASS("+v"(a[0]), "+v"(a[1])), P8X_PASS("v"(x[0]), "v"(x[1]), P8X_W))
+    } else if constexpr (NCOL == 3) {
+        P8X_GQ(P8X_G3, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), P8X_W))
+    } else if constexpr (NCOL == 4) {
+        P8X_GQ(P8X_G4, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), P8X_W))
+    } else if constexpr (NCOL == 5) {
+        P8X_GQ(P8X_G5, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), P8X_W))
+    } else if constexpr (NCOL == 6) {
+        P8X_GQ(P8X_G6, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), P8X_W))
+    } else if constexpr (NCOL == 7) {
+        P8X_GQ(P8X_G7, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), P8X_W))
+    } else if constexpr (NCOL == 8) {
+        P8X_GQ(P8X_G8, P8X_PASS("+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7])), P8X_PASS("v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), P8X_W))
+    }
+#undef P8X_W
+#undef P8X_GQ
+#undef P8X_PASS
+}
+#undef P8X_DL
+#undef P8X_R1
+#undef P8X_G1
+#undef P8X_R2
+#undef P8X_G2
+#undef P8X_R3
+#undef P8X_G3
+#undef P8X_R4
+#undef P8X_G4
+#undef P8X_R5
+#undef P8X_G5
+#undef P8X_R6
+#undef P8X_G6
+#undef P8X_R7
+#undef P8X_G7
+#undef P8X_R8
+#undef P8X_G8
+
+// chunks 4Q .. 4Q + 3 of one tile: the codewords of every stage, then their products with each column's broadcast
+// activation words
+template <int C, int NCOL, int Q>
+__device__ __forceinline__ void wave_group(const uint32_t *tab, const QuadSlice<C> &p, uint32_t H, uint32_t bankbytes,
+                                           const uint32_t (&xa)[NCOL], const uint32_t (&xb)[NCOL], int (&acc)[nstage_of(C)][NCOL]) {
+    constexpr int NST = nstage_of(C);
+    const uint32_t hq = coset_bytes(H, bankbytes, Q);
+    uint32_t w[NST][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        w[0][e] = lds_word(tab, p.template addr<0>(4 * Q + e, hq));
+        if constexpr (NST > 1) w[1][e] = lds_word(tab, p.template addr<1>(4 * Q + e, hq));
+        if constexpr (NST > 2) w[2][e] = lds_word(tab, p.template addr<2>(4 * Q + e, hq));
+    }
+#pragma unroll
+    for (int s = 0; s < NST; ++s) dot4_bcast<Q & 3, NCOL>(acc[s], Q < 4 ? xa : xb, w[s]);
+    __asm__ volatile("" ::: "memory");   // one group of 4 chunks at a time: bounds the live registers
+}
+
+template <int C, int NCOL, int... Q>
+__device__ __forceinline__ void wave_groups(const uint32_t *tab, const QuadSlice<C> &p, uint32_t H, uint32_t bankbytes,
+                                            const uint32_t (&xa)[NCOL], const uint32_t (&xb)[NCOL], int (&acc)[nstage_of(C)][NCOL],
+                                            std::integer_sequence<int, Q...>) {
+    (wave_group<C, NCOL, Q>(tab, p, H, bankbytes, xa, xb, acc), ...);
+}
+
+// One tile of a wave: integer sums per column (isum = sum_s dot_s << SH_s, CPU.patch:646-662), then
+// y += isum * d * S.
 template <int C, int NCOL>
-__device__ __forceinline__ void wave_tile(const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot, int lane,
-                                          const WaveSlice<C, NCOL> &r_, float (&yacc)[NCOL]) {
-    const int hs = lane >> 5, j = lane & 31;
+__device__ __forceinline__ void wave_tile(const uint32_t *tab, int lane, const WaveSlice<C, NCOL> &r_, float (&yacc)[NCOL]) {
+    constexpr int NST = nstage_of(C), SH1 = sh1_of(C), SH2 = sh2_of(C);
+    const int j = lane & 31;
     WaveSlice<C, NCOL> r = r_;
     pin(r.p.w);
     pin(r.p.s);
-    pin(r.xw);
+    pin(r.xa);
+    pin(r.xb);
 #pragma unroll
     for (int n = 0; n < NCOL; ++n) pin(r.xd[n]);
-    // lanes read each other's words: the slot is this wave's alone and LDS operations of one wave run in order,
-    // so compiler barriers on both sides of the writes are all the ordering needed (without them the compiler
-    // may move reads of words other lanes write across the writes)
-    __asm__ volatile("" ::: "memory");
+    const uint32_t H = r.p.coset_bits();
+    int acc[NST][NCOL];
 #pragma unroll
-    for (int n = 0; n < NCOL; ++n) {
-        slot[n * 128 + hs * 64 + j] = r.xw[n];
-        slot[n * 128 + hs * 64 + 32 + j] = r.xw[n];
-    }
-    __asm__ volatile("" ::: "memory");
-    int isum[NCOL];
-    step_isum<NCOL, C, 128>(tab, r.p, j, (uint32_t)(j << 2) * 0x01010101u, slot + hs * 64 + j, isum);
+    for (int s = 0; s < NST; ++s)
+#pragma unroll
+        for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
+    wave_groups<C, NCOL>(tab, r.p, H, (uint32_t)(j << 2) * 0x01010101u, r.xa, r.xb, acc, std::make_integer_sequence<int, 8>{});
     const float sc = half_to_float(r.p.s);
 #pragma unroll
-    for (int n = 0; n < NCOL; ++n) yacc[n] += ((float)isum[n] * r.xd[n]) * sc;
+    for (int n = 0; n < NCOL; ++n) {
+        int isum = acc[0][n] * (1 << SH1);
+        if constexpr (NST > 1) isum += acc[1][n] * (1 << SH2);
+        if constexpr (NST > 2) isum += acc[2][n];
+        yacc[n] += ((float)isum * r.xd[n]) * sc;
+    }
 }
 
 // a run of consecutive tiles of class C in row group g, NBUF tiles in flight (the gemv_run scheme)
 template <int C, int NBUF, bool ONLY_C, int NCOL>
-__device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, __attribute__((address_space(3))) uint32_t *slot,
-                                        int g, int b, int bend, int lane, float (&yacc)[NCOL]) {
+__device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, int g, int b, int bend, int lane, float (&yacc)[NCOL]) {
     const int hs = lane >> 5, j = lane & 31;
     const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)g * J.nb;
     int e = bend;
@@ -844,8 +945,9 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
     }
     // activations [NCOL][K] int8 and scales [NCOL][K / 128]
     const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.K), dbytes = (uint32_t)(NCOL * J.nsl) * 4u;
-    const uint32_t vo = StepSlice<C>::quad_offset(hs, j), vp = StepSlice<C>::pair_offset(hs, j);
-    const uint32_t vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)lane, vd = 4u * (uint32_t)hs;
+    const uint32_t vo = QuadSlice<C>::quad_offset(hs, j), vp = QuadSlice<C>::pair_offset(hs, j);
+    // activation words: lane 16 r + i reads word i (and 16 + i) of its half hs = r >> 1
+    const uint32_t vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)(32 * hs + (lane & 15)), vd = 4u * (uint32_t)hs;
     uint32_t wn = mrow[b];
     auto issue = [&](WaveSlice<C, NCOL> &r, int ta) {
         const bool ok = ta < e;
@@ -860,13 +962,14 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, _
         const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u), rd = buffer_rsrc(J.d, ok ? dbytes : 0u);
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) {
-            r.xw[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
+            r.xa[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
+            r.xb[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq + 64u, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
             r.xd[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vd, 8u * (uint32_t)tc + 4u * (uint32_t)(n * J.nsl), 0));
         }
         __builtin_amdgcn_s_setprio(0);
         wn = mrow[min(ta + 1, e - 1)];
     };
-    auto tile = [&](const WaveSlice<C, NCOL> &r) { wave_tile<C, NCOL>(tab, slot, lane, r, yacc); };
+    auto tile = [&](const WaveSlice<C, NCOL> &r) { wave_tile<C, NCOL>(tab, lane, r, yacc); };
     WaveSlice<C, NCOL> buf[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) issue(buf[i], b + i);
@@ -918,12 +1021,9 @@ __global__ __launch_bounds__(64 * wave_waves(CM, NCOL)) __attribute__((amdgpu_wa
 void k_gemv_wave(const GemvJob *__restrict__ jobs, const uint32_t *__restrict__ ujob, int total_units, unsigned *ctr,
                  const uint32_t *__restrict__ a2) {
     constexpr int WAVES = wave_waves(CM, NCOL);
-    __shared__ WaveSmem<WAVES, NCOL> sm;
+    __shared__ WaveSmem sm;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     build_coset_table<64 * WAVES>(sm.tab, a2, tid);
-    // the slot's base in one register (it lies past the 64 KB table, beyond the LDS offset field)
-    __attribute__((address_space(3))) uint32_t *slot = (__attribute__((address_space(3))) uint32_t *)sm.xs[w];
-    __asm__ volatile("" : "+v"(slot));
     __syncthreads();
     const int np = min(kWaveParts, (int)gridDim.x), part = blockIdx.x % np;
     const int nwp = (((int)gridDim.x - 1 - part) / np + 1) * WAVES;   // waves serving this partition
@@ -942,13 +1042,13 @@ void k_gemv_wave(const GemvJob *__restrict__ jobs, const uint32_t *__restrict__ 
         for (int b = b0; b < bend;) {
             const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
             switch (mt >> 29) {
-                case 1: if constexpr ((CM >> 1) & 1) { b = wave_run<1, 2, CM == (1 << 1), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 2: if constexpr ((CM >> 2) & 1) { b = wave_run<2, 2, CM == (1 << 2), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 3: if constexpr ((CM >> 3) & 1) { b = wave_run<3, wave_nbuf_c3(NCOL), CM == (1 << 3), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 4: if constexpr ((CM >> 4) & 1) { b = wave_run<4, 2, CM == (1 << 4), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 5: if constexpr ((CM >> 5) & 1) { b = wave_run<5, 2, CM == (1 << 5), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 6: if constexpr ((CM >> 6) & 1) { b = wave_run<6, 2, CM == (1 << 6), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
-                case 7: if constexpr ((CM >> 7) & 1) { b = wave_run<7, 2, CM == (1 << 7), NCOL>(J, sm.tab, slot, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 1: if constexpr ((CM >> 1) & 1) { b = wave_run<1, 2, CM == (1 << 1), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 2: if constexpr ((CM >> 2) & 1) { b = wave_run<2, 2, CM == (1 << 2), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 3: if constexpr ((CM >> 3) & 1) { b = wave_run<3, wave_nbuf_c3(NCOL), CM == (1 << 3), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 4: if constexpr ((CM >> 4) & 1) { b = wave_run<4, 2, CM == (1 << 4), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 5: if constexpr ((CM >> 5) & 1) { b = wave_run<5, 2, CM == (1 << 5), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 6: if constexpr ((CM >> 6) & 1) { b = wave_run<6, 2, CM == (1 << 6), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
+                case 7: if constexpr ((CM >> 7) & 1) { b = wave_run<7, 2, CM == (1 << 7), NCOL>(J, sm.tab, g, b, bend, lane, yacc); break; } [[fallthrough]];
                 default: ++b; break;   // class 0: zero weights
             }
         }

@@ -61,14 +61,44 @@ __global__ void k_regroup_scales(const uint16_t *__restrict__ S, uint16_t *__res
     Sg[i] = S[(size_t)b * rows + 32 * g + j];
 }
 
-// tile payloads from the file layout (file_word) to the device layout (dev_word); one 64-thread block per tile,
-// thread (hs, j) moves the NW words of lane j of half-slice hs; every tile lies inside the payload (checked at prepare)
+// Field k of a region of W-bit fields starting at word o of a lane's words (bit string little-endian across words).
+__device__ uint32_t lane_field(const uint32_t *w, int o, int W, int k) {
+    const int pos = W * k, wi = o + (pos >> 5), bb = pos & 31;
+    uint64_t v = w[wi];
+    if (bb + W > 32) v |= (uint64_t)w[wi + 1] << 32;
+    return (uint32_t)(v >> bb) & ((1u << W) - 1u);
+}
+__device__ void lane_field_put(uint32_t *w, int o, int W, int k, uint32_t f) {
+    const int pos = W * k, wi = o + (pos >> 5), bb = pos & 31;
+    w[wi] |= f << bb;
+    if (bb + W > 32) w[wi + 1] |= f >> (32 - bb);
+}
+// lane j's region (32 fields of W bits at word o): stored field k encodes chunk (j + k) & 31 (CPU.patch:155-158);
+// out field t = chunk t
+__device__ void lane_region_to_chunks(const uint32_t *in, uint32_t *out, int o, int W, int j) {
+    for (int t = 0; t < 32; ++t) lane_field_put(out, o, W, t, lane_field(in, o, W, (t - j) & 31));
+}
+
+// Tile payloads from the file layout to the device layout, one 64-thread block per tile, thread (hs, j) for the
+// NW words of lane j of half-slice hs: every region's fields rotated into chunk order (field t = chunk t, so the
+// chunk of a step is the same for every lane), the label word of classes with W1 < 8 likewise (bit t = chunk t),
+// and the words placed in 16-byte groups (file_word -> dev_word). Every tile lies inside the payload (checked at
+// prepare).
 __global__ void k_relayout_payload(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, const uint32_t *__restrict__ M) {
     const uint32_t m = M[blockIdx.x];
-    const int nw = nw_of((int)(m >> 29));
+    const int c = (int)(m >> 29), nw = nw_of(c), w1 = w1_of(c), w2 = w2_of(c), w3 = w3_of(c);
     const int hs = threadIdx.x >> 5, j = threadIdx.x & 31;
     const size_t base = (size_t)(m & 0x1FFFFFFFu) + (size_t)hs * nw * 32;
-    for (int i = 0; i < nw; ++i) dst[base + dev_word(i, j, nw)] = src[base + file_word(i, j)];
+    uint32_t in[24], out[24];
+    for (int i = 0; i < nw; ++i) { in[i] = src[base + file_word(i, j)]; out[i] = 0u; }
+    if (w1 == 8) lane_region_to_chunks(in, out, 0, 8, j);
+    else if (w1 > 0) {
+        out[0] = (in[0] << j) | (j ? in[0] >> (32 - j) : 0u);   // label bit k -> bit (j + k) & 31
+        lane_region_to_chunks(in, out, 1, w1 - 1, j);
+    }
+    if (w2) lane_region_to_chunks(in, out, w1, w2, j);
+    if (w3) lane_region_to_chunks(in, out, w1 + w2, w3, j);
+    for (int i = 0; i < nw; ++i) dst[base + dev_word(i, j, nw)] = out[i];
 }
 
 }  // namespace p8x

@@ -1,12 +1,11 @@
 // p8x_lane.h -- gfx950 lane-slice decoder shared by every kernel.
 //
 // One wave64 owns one tile (g, b): lane L decodes half-slice hs = L >> 5 of sorted row 32g + (L & 31).
-// A lane-slice is NW(c) payload words holding 32 fields per stage; step k of lane j encodes chunk
-// t = (j + k) & 31 (CPU.patch:155-158). Payload words are read in the device layout of p8x_format.h (dev_word:
-// a lane's words in 16-byte groups). The chunk-order loaders (RawSlice, AnyRaw) load every lane's words already
-// rotated by j fields (per-lane load addresses plus one v_alignbit per word), so field t of the rotated registers
-// IS chunk t for every lane: all later indexing is compile-time and the activation chunk is the same for all 32
-// lanes of a half-wave (an LDS broadcast). The step-order loader (StepSlice) loads words as stored.
+// A lane-slice is NW(c) payload words holding 32 fields per stage. In the file, step k of lane j encodes chunk
+// t = (j + k) & 31 (CPU.patch:155-158); p8x_prepare rotates every lane's fields once (k_relayout_payload) so that
+// in device memory field t of every region IS chunk t, for every lane, and places the words in 16-byte groups
+// (dev_word, p8x_format.h). Every loader here reads that layout as stored: all field indexing is compile-time and
+// the activation chunk of a step is the same for all 32 lanes of a half-wave.
 //
 // Coset table in LDS: entry (f, h) = A[f] + h * c (bytewise, CPU.patch:221/:255), replicated across the
 // 32 LDS banks: byte address (f << 8) | (h << 7) | (bank << 2) with bank = lane & 31, so the 32 lanes of a
@@ -129,9 +128,8 @@ __device__ __forceinline__ uint32_t coset_bytes(uint32_t H, uint32_t bankbytes, 
     return (__umul24(nib7, 0x00204081u) & 0x80808080u) | bankbytes;
 }
 
-// Raw payload words of one lane-slice of class C, loaded in rotated order (before the v_alignbit step),
-// plus the lane's fp16 row scale. Kept separate from the decode so a wave can hold the next tile's words
-// in flight while it decodes the current one.
+// Raw payload words of one lane-slice of class C (one 32-bit load per word), plus the lane's fp16 row scale.
+// Kept separate from the decode so a wave can hold the next tile's words in flight while it decodes the current one.
 template <int C>
 struct RawSlice {
     static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
@@ -140,9 +138,8 @@ struct RawSlice {
 
     template <int W, int WB, int O>
     static __device__ __forceinline__ void region_offsets(uint32_t hsoff, int j, uint32_t (&vo)[NW]) {
-        const int wr = ((((32 - j) & 31) * W) >> 5);
 #pragma unroll
-        for (int m = 0; m < W; ++m) vo[O + m] = 4u * (hsoff + (uint32_t)dev_word(WB + (m + wr) % W, j, NW));
+        for (int m = 0; m < W; ++m) vo[O + m] = 4u * (hsoff + (uint32_t)dev_word(WB + m, j, NW));
     }
 
     // Byte offsets, within a tile's payload, of the lane's NW words in load order. They depend only on the
@@ -170,10 +167,9 @@ struct RawSlice {
 };
 
 template <int W, int O, int NWT>
-__device__ __forceinline__ void rotate_region(const uint32_t (&w)[NWT], int j, uint32_t (&R)[W]) {
-    const int br = (((32 - j) & 31) * W) & 31;
+__device__ __forceinline__ void copy_region(const uint32_t (&w)[NWT], uint32_t (&R)[W]) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) R[i] = __builtin_amdgcn_alignbit(w[O + (i + 1) % W], w[O + i], br);
+    for (int i = 0; i < W; ++i) R[i] = w[O + i];
 }
 
 // Decoded state of one lane-slice of class C.
@@ -190,15 +186,15 @@ struct LaneSlice {
     uint32_t bankbytes;
 
     // same state from words already in registers
-    __device__ __forceinline__ void from_raw(const RawSlice<C> &raw, int j) {
+    __device__ __forceinline__ void from_raw(const RawSlice<C> &raw) {
         if constexpr (W1 == 8) {
-            rotate_region<8, 0>(raw.w, j, r1);
+            copy_region<8, 0>(raw.w, r1);
         } else {
-            r0 = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
-            rotate_region<W1 - 1, 1>(raw.w, j, r1);
+            r0 = raw.w[0];
+            copy_region<W1 - 1, 1>(raw.w, r1);
         }
-        if constexpr (W2 > 0) rotate_region<W2, W1>(raw.w, j, r2);
-        if constexpr (W3 > 0) rotate_region<W3, W1 + W2>(raw.w, j, r3);
+        if constexpr (W2 > 0) copy_region<W2, W1>(raw.w, r2);
+        if constexpr (W3 > 0) copy_region<W3, W1 + W2>(raw.w, r3);
     }
 
     __device__ __forceinline__ void prepare(uint32_t bb) {
@@ -231,12 +227,10 @@ struct LaneSlice {
     }
 };
 
-// ------------------------------------------------------------------------------------------------ step order
-// The same lane-slice decoded in step order: payload words exactly as stored, so a wave loads each pair of
-// words [i >> 1][j][i & 1] of its half-slice as one contiguous 8-byte-per-lane access (whole cache lines per
-// instruction). Field k of a region is step k of lane j, which encodes chunk (j + k) & 31: the activation
-// chunk is then lane-dependent (the caller reads it at a per-lane offset), while the coset bits come from the
-// trellis in chunk order, rotated into step order.
+// ------------------------------------------------------------------------------------------------ 16-byte loads
+// The same lane-slice loaded in 16-byte groups: a wave loads group q of its half-slice as one contiguous
+// 16-byte-per-lane access (512 bytes per 32 lanes, whole cache lines per instruction). Field k of a region is
+// chunk k (the device payload is in chunk order), so the activation chunk of step k is the same for all lanes.
 template <int W, int OFF, int NW>
 __device__ __forceinline__ uint32_t field_at(const uint32_t (&w)[NW], int k) {
     const int pos = W * k, wi = OFF + (pos >> 5), bb = pos & 31;
@@ -245,7 +239,7 @@ __device__ __forceinline__ uint32_t field_at(const uint32_t (&w)[NW], int k) {
 }
 
 template <int C>
-struct StepSlice {
+struct QuadSlice {
     static constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C), NW = nw_of(C);
     static constexpr int NQ = NW / 4, NP = (NW % 4) / 2;   // 16-byte groups and a trailing word pair per lane
     static constexpr int O1 = W1 == 8 ? 0 : 1, O2 = W1, O3 = W1 + W2;   // first word of each stage's fields
@@ -275,8 +269,8 @@ struct StepSlice {
         s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, soff, kBufNT);
     }
 
-    // coset bits in step order for lane j
-    __device__ __forceinline__ uint32_t coset_bits(int j) const {
+    // coset bits, chunk order
+    __device__ __forceinline__ uint32_t coset_bits() const {
         uint32_t z;
         if constexpr (W1 == 8) {
             uint32_t r[8];
@@ -286,12 +280,10 @@ struct StepSlice {
         } else {
             z = w[0];
         }
-        const uint32_t zc = __builtin_amdgcn_alignbit(z, z, (32 - j) & 31);   // bit k -> bit (j + k) & 31
-        const uint32_t hc = trellis_coset_bits(zc);
-        return __builtin_amdgcn_alignbit(hc, hc, j & 31);                      // back to step order
+        return trellis_coset_bits(z);
     }
 
-    // LDS byte address of stage S at step k, hq = coset_bytes(H, bankbytes, k >> 2)
+    // LDS byte address of stage S at chunk k, hq = coset_bytes(H, bankbytes, k >> 2)
     template <int S>
     __device__ __forceinline__ uint32_t addr(int k, uint32_t hq) const {
         const int e = k & 3;
@@ -311,8 +303,8 @@ struct StepSlice {
 };
 
 // ------------------------------------------------------------------------------------------------ any class
-// Raw payload words of one lane-slice (any class up to NWMAX words) in rotated load order, plus the lane's
-// fp16 row scale: issued ahead of use, then decoded into an AnySlice (per-lane rotation, labels, trellis).
+// Raw payload words of one lane-slice (any class up to NWMAX words), plus the lane's fp16 row scale: issued ahead
+// of use, then decoded into an AnySlice (labels, trellis).
 template <int NWMAX>
 struct AnyRaw {
     uint32_t w[NWMAX];
@@ -320,9 +312,8 @@ struct AnyRaw {
 
     template <int W, int WB, int NW>
     __device__ __forceinline__ void region(const uint32_t *__restrict__ p, int j) {
-        const int wr = (((32 - j) & 31) * W) >> 5;
 #pragma unroll
-        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + dev_word(WB + (m + wr) % W, j, NW));
+        for (int m = 0; m < W; ++m) w[WB + m] = __builtin_nontemporal_load(p + dev_word(WB + m, j, NW));
     }
     // p = the tile's half-slice base (tile payload + hs * NW * 32 words)
     template <int C>
@@ -339,8 +330,8 @@ struct AnyRaw {
     }
 };
 
-// Rotated lane-slice words of any class up to NWMAX words (chunk order after the per-lane rotation), plus the
-// coset bits in chunk order. Region layout as stored: [label word if W1 < 8] stage-1 fields, stage 2, stage 3.
+// Lane-slice words of any class up to NWMAX words (chunk order), plus the coset bits in chunk order. Region
+// layout as stored: [label word if W1 < 8] stage-1 fields, stage 2, stage 3.
 template <int NWMAX>
 struct AnySlice {
     uint32_t r[NWMAX];
@@ -348,28 +339,27 @@ struct AnySlice {
     uint32_t s;   // fp16 row scale, zero-extended by its load
 
     template <int W, int WB>
-    __device__ __forceinline__ void rotate(const AnyRaw<NWMAX> &raw, int j) {
-        const int br = (((32 - j) & 31) * W) & 31;
+    __device__ __forceinline__ void copy(const AnyRaw<NWMAX> &raw) {
 #pragma unroll
-        for (int i = 0; i < W; ++i) r[WB + i] = __builtin_amdgcn_alignbit(raw.w[WB + (i + 1) % W], raw.w[WB + i], br);
+        for (int i = 0; i < W; ++i) r[WB + i] = raw.w[WB + i];
     }
     template <int C>
-    __device__ __forceinline__ void from_raw(const AnyRaw<NWMAX> &raw, int j) {
+    __device__ __forceinline__ void from_raw(const AnyRaw<NWMAX> &raw) {
         constexpr int W1 = w1_of(C), W2 = w2_of(C), W3 = w3_of(C);
         uint32_t z;
         if constexpr (W1 == 8) {
-            rotate<8, 0>(raw, j);
+            copy<8, 0>(raw);
             uint32_t R[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) R[i] = r[i];
             z = labels_from_bytes(R);
         } else {
-            r[0] = __builtin_amdgcn_alignbit(raw.w[0], raw.w[0], (32 - j) & 31);
+            r[0] = raw.w[0];
             z = r[0];
-            rotate<W1 - 1, 1>(raw, j);
+            copy<W1 - 1, 1>(raw);
         }
-        if constexpr (W2 > 0) rotate<W2, W1>(raw, j);
-        if constexpr (W3 > 0) rotate<W3, W1 + W2>(raw, j);
+        if constexpr (W2 > 0) copy<W2, W1>(raw);
+        if constexpr (W3 > 0) copy<W3, W1 + W2>(raw);
         H = trellis_coset_bits(z);
         s = raw.s;
     }
@@ -448,15 +438,15 @@ __device__ __forceinline__ void load_any(AnyRaw<NWMAX> &raw, int c, const uint32
 }
 
 template <int CM, int NWMAX>
-__device__ __forceinline__ void prepare_any(AnySlice<NWMAX> &ls, int c, const AnyRaw<NWMAX> &raw, int j) {
+__device__ __forceinline__ void prepare_any(AnySlice<NWMAX> &ls, int c, const AnyRaw<NWMAX> &raw) {
     switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) ls.template from_raw<1>(raw, j); break;
-        case 2: if constexpr ((CM >> 2) & 1) ls.template from_raw<2>(raw, j); break;
-        case 3: if constexpr ((CM >> 3) & 1) ls.template from_raw<3>(raw, j); break;
-        case 4: if constexpr ((CM >> 4) & 1) ls.template from_raw<4>(raw, j); break;
-        case 5: if constexpr ((CM >> 5) & 1) ls.template from_raw<5>(raw, j); break;
-        case 6: if constexpr ((CM >> 6) & 1) ls.template from_raw<6>(raw, j); break;
-        case 7: if constexpr ((CM >> 7) & 1) ls.template from_raw<7>(raw, j); break;
+        case 1: if constexpr ((CM >> 1) & 1) ls.template from_raw<1>(raw); break;
+        case 2: if constexpr ((CM >> 2) & 1) ls.template from_raw<2>(raw); break;
+        case 3: if constexpr ((CM >> 3) & 1) ls.template from_raw<3>(raw); break;
+        case 4: if constexpr ((CM >> 4) & 1) ls.template from_raw<4>(raw); break;
+        case 5: if constexpr ((CM >> 5) & 1) ls.template from_raw<5>(raw); break;
+        case 6: if constexpr ((CM >> 6) & 1) ls.template from_raw<6>(raw); break;
+        case 7: if constexpr ((CM >> 7) & 1) ls.template from_raw<7>(raw); break;
         default: break;
     }
 }

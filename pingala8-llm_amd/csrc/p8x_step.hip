@@ -72,7 +72,7 @@ __device__ __forceinline__ void step_stage(kptr<const StepStage> sp, int v, RgSm
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
-    c.xlane = c.hs * 64 + c.j;
+    c.xlane = c.hs * 64;
     const int ks = wgl % nks, nbk = min(J.kchunk, J.nb - ks * J.kchunk);
     c.b0 = ks * J.kchunk; c.nbl = nbk;
     const int wpg = WAVES / gc, team = w / wpg, wk = w % wpg;   // waves beyond gc teams stay idle
