@@ -36,7 +36,8 @@ struct GemvJob {
     const uint32_t *D; const int16_t *prm;
     const uint16_t *prmd;            // prm with bit 15 set on rows that carry clamp-delta entries
     const int *cp; const uint16_t *cc; const float *cv;
-    const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32]
+    const void *q; const float *d;   // Q8_128: int8 [ncol][K] + f32 [ncol][K/128]; Q8_1: block_q8_1 [ncol][K/32];
+                                     // grouped launches (k_gemv_wave): q in the broadcast layout, d unused
                                      // (Q8_128 with q null: each task quantizes its chunk of x itself, with ic)
     const float *ic;
     const float *x; unsigned ldx;    // original activations for the clamp delta (nullptr: no delta)
@@ -788,18 +789,22 @@ __host__ __device__ constexpr int wave_wg_per_cu(int cm, int ncol = 1) { return 
 // prefetch depth of the class-3 runs (register buffers hold NCOL activation words and scales each)
 __host__ __device__ constexpr int wave_nbuf_c3(int ncol) { return ncol == 1 ? GEMV_NBUF_C3 : 2; }
 
+// bytes per 256-column block and column of the grouped launch's activations (k_act_q8_128_batch)
+constexpr uint32_t kBcastBlockBytes = 512;
+
 struct WaveSmem {
     uint32_t tab[kTabWords];   // LDS address 0
 };
 
-// A tile's payload with its activation words: per column, lane 16 r + i holds words i (xa) and 16 + i (xb) of its
-// half's 32 activation words (half hs = r >> 1, the rows of 16 lanes the DPP broadcast works in), and the half's
-// scale
+// A tile's payload with its activation words: per column, the lane's broadcast-layout entry {word i, word 16 + i,
+// d, 0} of its half (lane 16 r + i, half hs = r >> 1: the rows of 16 lanes the DPP broadcast works in). All four
+// words are kept: the compiler (ROCm 7.2) shrinks a 16-byte buffer load of which only three words are used to an
+// 8-byte load and reads the wrong word for the third.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 template <int C, int NCOL>
 struct WaveSlice {
     QuadSlice<C> p;
-    uint32_t xa[NCOL], xb[NCOL];
-    float xd[NCOL];
+    u32x4_t x[NCOL];
 };
 
 // acc += dot4(x broadcast from lane B of each 16-lane row, w): v_dot4c_i32_i8 with a DPP row_newbcast source
@@ -912,24 +917,30 @@ __device__ __forceinline__ void wave_tile(const uint32_t *tab, int lane, const W
     WaveSlice<C, NCOL> r = r_;
     pin(r.p.w);
     pin(r.p.s);
-    pin(r.xa);
-    pin(r.xb);
+    uint32_t xa[NCOL], xb[NCOL];
+    float xd[NCOL];
 #pragma unroll
-    for (int n = 0; n < NCOL; ++n) pin(r.xd[n]);
+    for (int n = 0; n < NCOL; ++n) {
+        uint32_t v[4] = {r.x[n][0], r.x[n][1], r.x[n][2], r.x[n][3]};
+        pin(v);
+        xa[n] = v[0];
+        xb[n] = v[1];
+        xd[n] = __builtin_bit_cast(float, v[2]);
+    }
     const uint32_t H = r.p.coset_bits();
     int acc[NST][NCOL];
 #pragma unroll
     for (int s = 0; s < NST; ++s)
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) acc[s][n] = 0;
-    wave_groups<C, NCOL>(tab, r.p, H, (uint32_t)(j << 2) * 0x01010101u, r.xa, r.xb, acc, std::make_integer_sequence<int, 8>{});
+    wave_groups<C, NCOL>(tab, r.p, H, (uint32_t)(j << 2) * 0x01010101u, xa, xb, acc, std::make_integer_sequence<int, 8>{});
     const float sc = half_to_float(r.p.s);
 #pragma unroll
     for (int n = 0; n < NCOL; ++n) {
         int isum = acc[0][n] * (1 << SH1);
         if constexpr (NST > 1) isum += acc[1][n] * (1 << SH2);
         if constexpr (NST > 2) isum += acc[2][n];
-        yacc[n] += ((float)isum * r.xd[n]) * sc;
+        yacc[n] += ((float)isum * xd[n]) * sc;
     }
 }
 
@@ -943,11 +954,11 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, i
         e = b + 1;
         while (e < bend && (mrow[e] >> 29) == (uint32_t)C) ++e;
     }
-    // activations [NCOL][K] int8 and scales [NCOL][K / 128]
-    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.K), dbytes = (uint32_t)(NCOL * J.nsl) * 4u;
+    // activations [NCOL][nb] blocks in the broadcast layout: lane 16 r + i loads entry (hs = r >> 1, i) =
+    // {word i, word 16 + i, d, 0} of its column's block
+    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u, qbytes = (uint32_t)(NCOL * J.nb) * kBcastBlockBytes;
     const uint32_t vo = QuadSlice<C>::quad_offset(hs, j), vp = QuadSlice<C>::pair_offset(hs, j);
-    // activation words: lane 16 r + i reads word i (and 16 + i) of its half hs = r >> 1
-    const uint32_t vs = 2u * (uint32_t)j, vq = 4u * (uint32_t)(32 * hs + (lane & 15)), vd = 4u * (uint32_t)hs;
+    const uint32_t vs = 2u * (uint32_t)j, vq = 256u * (uint32_t)hs + 16u * (uint32_t)(lane & 15);
     uint32_t wn = mrow[b];
     auto issue = [&](WaveSlice<C, NCOL> &r, int ta) {
         const bool ok = ta < e;
@@ -959,12 +970,10 @@ __device__ __forceinline__ int wave_run(const GemvJob &J, const uint32_t *tab, i
         // ahead of other waves' decode work (about 1% on the class-3 stream).
         __builtin_amdgcn_s_setprio(2);
         r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
-        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u), rd = buffer_rsrc(J.d, ok ? dbytes : 0u);
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u);
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) {
-            r.xa[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
-            r.xb[n] = __builtin_amdgcn_raw_buffer_load_b32(rq, vq + 64u, 256u * (uint32_t)tc + (uint32_t)(n * J.K), 0);
-            r.xd[n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vd, 8u * (uint32_t)tc + 4u * (uint32_t)(n * J.nsl), 0));
+            r.x[n] = __builtin_amdgcn_raw_buffer_load_b128(rq, vq, ((uint32_t)n * (uint32_t)J.nb + (uint32_t)tc) * kBcastBlockBytes, 0);
         }
         __builtin_amdgcn_s_setprio(0);
         wn = mrow[min(ta + 1, e - 1)];

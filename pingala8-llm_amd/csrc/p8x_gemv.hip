@@ -308,13 +308,16 @@ int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t
 
 // ------------------------------------------------------------------------------------------------ grouped launches
 struct ActJob {
-    const float *x; unsigned ldx; const float *ic; int K;
-    int8_t *q; float *d;   // [ncols][K], [ncols][K / 128]
+    const float *x; unsigned ldx; const float *ic; int K, nb;
+    int8_t *q;             // [ncols][nb] blocks in the broadcast layout of k_act_q8_128_batch
     int blk0;              // first 256-block of this job in the launch
 };
 
 // grid (ceil(total blocks / 4), ncols), block 256: the k_act_q8_128 body for a list of jobs, one 256-block per
-// wave; blk_job gives each block's job
+// wave; blk_job gives each block's job. Output in the grouped kernel's broadcast layout (kBcastBlockBytes per block
+// and column): entry (hs, i) at hs * 256 + 16 i holds {word i, word 16 + i, d, 0} of half hs (word t = the four
+// int8 of chunk t, d = the half's scale as f32), so a lane of row r = 2 hs + (0|1) loads everything its tile needs
+// from one column with one 16-byte load.
 __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int total) {
     const int gb = 4 * blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = blockIdx.y, lane = threadIdx.x & 63;
     if (gb >= total) return;
@@ -324,8 +327,15 @@ __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restri
     float dd;
     int s;
     quantize_block_q8_128(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane, packed, dd, s);
-    reinterpret_cast<uint32_t *>(J.q + (size_t)n * J.K + 256 * b)[lane] = packed;
-    if ((lane & 31) == 0) J.d[(size_t)n * (J.K / 128) + 2 * b + (lane >> 5)] = dd;
+    const int hs = lane >> 5, t = lane & 31;
+    uint32_t *e = reinterpret_cast<uint32_t *>(J.q + ((size_t)n * J.nb + b) * kBcastBlockBytes + 256 * hs + 16 * (t & 15));
+    if (t < 16) {
+        e[0] = packed;
+        e[2] = __builtin_bit_cast(uint32_t, dd);
+        e[3] = 0u;
+    } else {
+        e[1] = packed;
+    }
 }
 
 // Finishing launch of a grouped GEMV. Rows that carry clamp-delta entries (bit 15 of prmd) go to the first blocks,
@@ -471,10 +481,11 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: job %d has a different codebook", i);
         for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
     }
-    // workspace layout: unit counters | per job: q [ncols][K] | d [ncols][nsl] | partials [nks][ncols][rows]
+    // workspace layout: unit counters | per job: activations [ncols][nb] in the broadcast layout | partials
+    // [nks][ncols][rows]
     std::vector<GemvJob> jobs(njobs);
     std::vector<ActJob> act(njobs);
-    std::vector<size_t> off_q(njobs), off_d(njobs), off_p(njobs);
+    std::vector<size_t> off_q(njobs), off_p(njobs);
     size_t bytes = 0;
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
     const size_t off_ctr = take(kWaveCtrBytes);
@@ -513,11 +524,10 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         const p8x_tensor *t = tensors[i];
         const int kc = kcs[i];
         const int nks = (t->nb + kc - 1) / kc;
-        off_q[i] = take((size_t)ncols * t->K);
-        off_d[i] = take(4 * (size_t)ncols * t->nsl);
+        off_q[i] = take((size_t)ncols * t->nb * kBcastBlockBytes);
         off_p[i] = take(4 * (size_t)nks * ncols * t->rows);   // partial rows (the finishing launch reads them)
         fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, 1, 0);
-        act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, nullptr, nullptr, blk0};
+        act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, t->nb, nullptr, blk0};
         blk0 += t->nb;
         ablk.insert(ablk.end(), (size_t)t->nb, (uint32_t)i);
     }
@@ -534,9 +544,8 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     b->ctr = (unsigned *)(w + off_ctr);
     for (int i = 0; i < njobs; ++i) {
         jobs[i].q = w + off_q[i];
-        jobs[i].d = (const float *)(w + off_d[i]);
+        jobs[i].d = nullptr;
         act[i].q = (int8_t *)(w + off_q[i]);
-        act[i].d = (float *)(w + off_d[i]);
         jobs[i].wpart = (float *)(w + off_p[i]);
         jobs[i].wcnt = nullptr;
     }
