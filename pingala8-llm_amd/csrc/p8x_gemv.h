@@ -44,7 +44,10 @@ struct GemvJob {
     float *y; unsigned ldy;
     int32_t *partials;               // optional integer partials (sorted rows)
     float *wpart; unsigned *wcnt;    // K-chunk partial rows [nks][ncol][rows] and arrival counters [ng]
+    unsigned long long *wslot;       // one column in two K-chunks: per-row meeting slots [rows], 0 between calls
     int rows, K, nb, ng, nsl;
+    unsigned lin;                    // one-class tensor with its tiles in order: payload words per tile (tile t at
+                                     // word t * lin of D), else 0 (offsets from the tile words M)
     int kchunk, nks, task0, ntasks;
     unsigned dbytes;                 // payload region bytes (D .. end of the slot's payload)
     int g0, gend, prows;             // task kernel: row groups g0 .. gend - 1; partials rows (32 g0 ..) with row stride prows
@@ -243,18 +246,21 @@ struct GemvRun {
     __device__ __forceinline__ kptr<const uint32_t> mrow(const TaskCtx<NCOL, ACT> &c) const {
         return as_const(c.J->M) + (size_t)c.g * c.J->nb;   // tile words: scalar loads
     }
+    // one-class runs compute their payload offsets (the host picks a one-class instantiation only for tensors whose
+    // tiles are in order, GemvJob::lin): no tile-word load ahead of the first tile
+    __device__ __forceinline__ bool linear(const TaskCtx<NCOL, ACT> &) const { return ONLY_C; }
     __device__ __forceinline__ void issue(const TaskCtx<NCOL, ACT> &c, Slice &r, int ta) {
         const GemvJob &J = *c.J;
         const bool ok = ta < e;
         const int tc = ok ? ta : b;
-        const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
+        const uint32_t toff = linear(c) ? ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * J.lin * 4u : (wn & 0x1FFFFFFFu) * 4u;
         const uint32_t soff = ((uint32_t)c.g * (uint32_t)J.nb + (uint32_t)tc) * 64u;   // scales [g][b][32]
         const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
         __builtin_amdgcn_s_setprio(2);   // loads issued at raised priority (see wave_run)
         if constexpr (QUAD) r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         else r.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
         __builtin_amdgcn_s_setprio(0);
-        wn = mrow(c)[min(ta + 1, e - 1)];
+        if (!linear(c)) wn = mrow(c)[min(ta + 1, e - 1)];
     }
     __device__ __forceinline__ void begin(const TaskCtx<NCOL, ACT> &c, int b_, int bend) {
         b = b_;
@@ -270,7 +276,7 @@ struct GemvRun {
             RawSlice<C>::lane_offsets((uint32_t)(c.hs * NW * 32), c.j, vo);
         }
         vs = 2u * (uint32_t)c.j;
-        wn = mrow(c)[b];
+        wn = linear(c) ? 0u : mrow(c)[b];
 #pragma unroll
         for (int i = 0; i < NBUF - 1; ++i) issue(c, buf[i], b + i);
     }
@@ -327,6 +333,23 @@ __device__ __forceinline__ unsigned arrive_after_stores(unsigned *ctr, int lane)
     old = __builtin_amdgcn_readfirstlane(old);
     __asm__ volatile("" ::: "memory");   // the partial loads that follow stay below the arrival
     return old;
+}
+
+// Two producers of one value (the two K-halves of a row, or a row's gate and up products) meet through one 64-bit
+// agent-scope atomic exchange on the row's slot, which holds 0 between calls: each puts (1 + its index) << 32 |
+// bits(value) there; the one that gets a nonzero old value arrived second, takes the partner's index and value from
+// it and puts the slot back to 0. The value travels inside the RMW itself, so nothing has to be ordered before it
+// (no separate partial store, no vmcnt wait, no counter): one memory round trip instead of three. The reset store
+// is complete before anything later in the stream (kernel boundary) or in the step launch (the barrier's vmcnt(0))
+// uses the slot again. Returns true for the second arrival, with the partner's index and value.
+__device__ __forceinline__ bool pair_meet(gptr<unsigned long long> slot, int me, float v, int &other_idx, float &other) {
+    const unsigned long long mine = ((unsigned long long)(1 + me) << 32) | __float_as_uint(v);
+    const unsigned long long old = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old >> 32) == 0ull) return false;
+    other_idx = (int)(old >> 32) - 1;
+    other = __uint_as_float((uint32_t)old);
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
 }
 
 // The row group's sums after one K-chunk: the two half-slices meet through one cross-lane add; the K-chunks of
@@ -567,42 +590,36 @@ struct RgJobs {
     int njobs;
     int glu;
     float *glu_out;        // [rows] original rows
-    float *glu_pair;       // [2][rows]: gate, up values by original row (agent-coherent)
-    unsigned *glu_cnt;     // [rows] arrival counters, 0 between calls
+    unsigned long long *glu_slot;   // [rows] gate / up meeting slots by original row, 0 between calls
 };
 
 template <typename T>
 __device__ __forceinline__ T pick(int jb, T a0, T a1, T a2, T a3) { return jb == 0 ? a0 : jb == 1 ? a1 : jb == 2 ? a2 : a3; }
 
-// The second of a row's two arrivals computes silu(gate) * up: each lane stores its row's value (agent-coherent),
-// waits for the stores (as in arrive_after_stores), counts its arrival on the row's counter, and the lane that saw
-// the partner's arrival reads the partner's value and writes the output, agent-coherent (the counter goes back to 0).
-// pair: [2][rows] gate, up values; cnt: [rows] counters; out: [rows].
-__device__ __forceinline__ void glu_meet(float *pair_, unsigned *cnt, float *out, int rows, int jb, int r, float v, bool active) {
-    const gptr<float> pair = as_global_rw(pair_);
-    if (active) __hip_atomic_store(&pair[(size_t)jb * rows + r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    unsigned old = 0;
-    if (active) old = __hip_atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __asm__ volatile("" ::: "memory");
-    if (active && old == 1u) {
-        const float other = __hip_atomic_load(&pair[(size_t)(1 - jb) * rows + r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The second of a row's two arrivals (gate: job 0, up: job 1) computes silu(gate) * up and writes it, agent-coherent
+// (read by a later stage of the step launch): the values meet through the row's slot (pair_meet).
+__device__ __forceinline__ void glu_meet(unsigned long long *slot, float *out, int jb, int r, float v, bool active) {
+    int oi;
+    float other;
+    if (active && pair_meet(as_global_rw(slot) + r, jb, v, oi, other)) {
         const float gate = jb == 0 ? v : other, up = jb == 0 ? other : v;
         __hip_atomic_store(&as_global_rw(out)[r], gate / (1.0f + expf(-gate)) * up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&cnt[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 __device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v, bool active) {
-    glu_meet(R.glu_pair, R.glu_cnt, R.glu_out, R.j0.rows, jb, r, v, active);
+    glu_meet(R.glu_slot, R.glu_out, jb, r, v, active);
 }
 
 // SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
 // NCOL x (blocks of a chunk) <= kRgMaxBlocks. gc row groups at a time: the waves form gc teams of WAVES / gc,
 // team t takes row group g0 + t * (workgroups per chunk) over the chunk, so that a workgroup with several row
-// groups streams them together instead of one after another. The activations, K plan and rotation come from job 0.
+// groups streams them together instead of one after another. The activations, K plan and rotation come from job 0;
+// the leading arguments repeat what the prologue needs of them (x, ic, the codebook words, nb, kchunk, nks, ldx),
+// so that a build with kernel-argument preloading has them in SGPRs when the waves start.
 template <int CM, bool SPLIT, int NCOL, bool TEAMS, bool MULTI>
 __global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
-void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
+void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, const uint32_t *__restrict__ a2, int nb0, int kchunk0,
+               int nks0, unsigned ldx0, RgJobs jobs, int gc_) {
     const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
@@ -628,9 +645,9 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64;
     // workgroup b (of the job's nwg): K-chunk ks = b % nks of row groups b / nks, b / nks + nwg / nks, ...
-    const int nks = SPLIT ? J.nks : 1;
-    const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
-    c.b0 = ks * J.kchunk; c.nbl = nbk;
+    const int nks = SPLIT ? nks0 : 1;
+    const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(kchunk0, nb0 - ks * kchunk0) : nb0;
+    c.b0 = ks * kchunk0; c.nbl = nbk;
     const int wpg = WAVES / gc, team = w / wpg, wk = w % wpg;   // waves beyond gc teams stay idle
     const int per = nbk / wpg, rem = nbk % wpg;
     int b0 = c.b0 + wk * per + min(wk, rem), b1 = b0 + per + (wk < rem ? 1 : 0);   // the wave's K range
@@ -641,8 +658,8 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     BlockLane in[RQ];
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
-        const int it = w + i * WAVES, n = it / nbk, bk = c.b0 + it % nbk;   // column, block of the tensor
-        if (it < NCOL * nbk) in[i].load(J.x + (size_t)n * J.ldx + 256 * bk, J.ic + 256 * bk, lane);
+        const int it = w + i * WAVES, n = NCOL == 1 ? 0 : it / nbk, bk = c.b0 + (NCOL == 1 ? it : it % nbk);   // column, block
+        if (it < NCOL * nbk) in[i].load(x0 + (size_t)n * ldx0 + 256 * bk, ic0 + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
     CosetTableFill<64 * WAVES> fill;
@@ -657,7 +674,7 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         // on every path (a wave without work requests one in-range tile it never reads), so that no control-flow
         // merge before the table stores makes the compiler wait for these loads there
         c.g = min(gfirst, J.ng - 1);
-        const int bb = pre_on ? b0 : min(b0, J.nb - 1);
+        const int bb = pre_on ? b0 : min(b0, nb0 - 1);
         pre.begin(c, bb, pre_on ? b1 : bb + 1);
     }
     __asm__ volatile("" ::: "memory");
@@ -685,6 +702,10 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         if (PC != 0 && first && pre_on) bstart = pre.finish(c, sm, yacc);   // the run begun before the prep
         first = false;
         for (int b = bstart; b < (g < J.ng ? b1 : b0);) {
+            if constexpr (PC != 0) {   // one class: no tile word to read
+                b = gemv_run<NCOL, P8X_ACT_Q8_128, false, PC, gemv_nbuf(NCOL, PC), true>(c, sm, b, b1, yacc);
+                continue;
+            }
             const uint32_t mt = as_const(JB.M)[(size_t)g * JB.nb + b];
             switch (mt >> 29) {
                 case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<NCOL, P8X_ACT_Q8_128, false, 1, gemv_nbuf(NCOL, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
@@ -713,36 +734,44 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
                 if (lane < 32)
                     for (int i = 0; i < wpg; ++i) v[n] += sm.red[set][w + i][n][lane];
             }
-            if constexpr (SPLIT) {   // K-chunks: the last arrival sums them in chunk order
-                const gptr<float> wpart = as_global_rw(JB.wpart);
-                const gptr<unsigned> wcnt = as_global_rw(JB.wcnt);
-                if (lane < 32)
+            bool fin = lane < 32;   // lanes that finish their row here
+            if constexpr (SPLIT) {
+                if (NCOL == 1 && nks == 2) {   // two K-halves: each row's halves meet in its slot (pair_meet)
+                    int oi;
+                    float other;
+                    fin = fin && pair_meet(as_global_rw(JB.wslot) + 32 * g + lane, ks, v[0], oi, other);
+                    if (fin) v[0] = ks == 0 ? v[0] + other : other + v[0];   // chunk 0 + chunk 1 either way
+                } else {   // K-chunks: the last arrival sums them in chunk order
+                    const gptr<float> wpart = as_global_rw(JB.wpart);
+                    const gptr<unsigned> wcnt = as_global_rw(JB.wcnt);
+                    if (lane < 32)
 #pragma unroll
-                    for (int n = 0; n < NCOL; ++n)
-                        __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * JB.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (arrive_after_stores(JB.wcnt + g, lane) != (unsigned)(nks - 1)) continue;
-                if (lane < 32)
+                        for (int n = 0; n < NCOL; ++n)
+                            __hip_atomic_store(&wpart[((size_t)ks * NCOL + n) * JB.rows + 32 * g + lane], v[n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (arrive_after_stores(JB.wcnt + g, lane) != (unsigned)(nks - 1)) continue;
+                    if (lane < 32)
 #pragma unroll
-                    for (int n = 0; n < NCOL; ++n) {
-                        v[n] = 0.f;
-                        for (int k = 0; k < nks; ++k)
-                            v[n] += __hip_atomic_load(&wpart[((size_t)k * NCOL + n) * JB.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int n = 0; n < NCOL; ++n) {
+                            v[n] = 0.f;
+                            for (int k = 0; k < nks; ++k)
+                                v[n] += __hip_atomic_load(&wpart[((size_t)k * NCOL + n) * JB.rows + 32 * g + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    if (lane == 0) __hip_atomic_store(&wcnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
             const int r = ro & 0x7FFF;
             float vo[NCOL];
 #pragma unroll
             for (int n = 0; n < NCOL; ++n) {
                 vo[n] = v[n];
-                if (lane < 32 && (ro & 0x8000)) {
-                    const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;   // the shared activations
+                if (fin && (ro & 0x8000)) {
+                    const gptr<const float> xr = as_global(x0) + (size_t)n * ldx0;   // the shared activations
                     for (int e = as_global(JB.cp)[r]; e < as_global(JB.cp)[r + 1]; ++e) vo[n] += as_global(JB.cv)[e] * xr[as_global(JB.cc)[e]];
                 }
             }
             if (MULTI && jobs.glu) {
-                glu_meet(jobs, jb, r, vo[0], lane < 32);
-            } else if (lane < 32) {
+                glu_meet(jobs, jb, r, vo[0], fin);
+            } else if (fin) {
 #pragma unroll
                 for (int n = 0; n < NCOL; ++n) as_global_rw(J.y)[(size_t)n * J.ldy + r] = vo[n];
             }
@@ -760,9 +789,12 @@ static int launch_gemv_rg_t(const RgJobs &jobs, int ng, const uint32_t *a2, hipS
     const int nks = jobs.j0.nks;
     // several jobs: each takes ceil(its row groups / per) workgroups per K-chunk (wgbase, set by the caller)
     const int grid = MULTI ? jobs.wgbase[4] : (ng + per - 1) / per * nks;
-    if (nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
-    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, gc);
-    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
+    const GemvJob &j0 = jobs.j0;
+#define P8X_RG_ARGS j0.x, j0.ic, a2, j0.nb, j0.kchunk, j0.nks, j0.ldx, jobs
+    if (nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, 1);
+    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, gc);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, 1);
+#undef P8X_RG_ARGS
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 
@@ -1093,7 +1125,7 @@ int launch_gemv_rg_multi(int cm, const RgJobs &jobs, int ng, const uint32_t *a2,
 int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
                     RgJobs &R, int &cm, int &ng);
 int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what);
-int class_set(const size_t hist[8]);
+int class_set(const size_t hist[8], bool in_order = true);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
                      hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 

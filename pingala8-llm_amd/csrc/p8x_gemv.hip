@@ -127,11 +127,12 @@ __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, si
 
 // K-split of a single-GEMV launch: about one task per workgroup slot, at least two tiles per wave, chunks no
 // larger than the LDS activation buffer allows.
-int class_set(const size_t hist[8]) {
+int class_set(const size_t hist[8], bool in_order) {
     int m = 0;
     for (int c = 1; c < 8; ++c) if (hist[c]) m |= 1 << c;
-    // a one-class set decodes whole runs as its class: only when no tile is class 0 (all-zero, skipped)
-    if (!hist[0])
+    // a one-class set decodes whole runs as its class: only when no tile is class 0 (all-zero, skipped); its
+    // row-group and task kernels compute payload offsets, so the tiles must also be in order (else the enclosing set)
+    if (!hist[0] && in_order)
         for (int cm : {kCmC3, kCmC6})
             if ((m & ~cm) == 0) return cm;
     for (int cm : {kCmC234, kCmC2346})
@@ -151,7 +152,7 @@ int rg_plan(const p8x_tensor *t, int ncols, int *kc) {
 
 GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
     GemvPlan p;
-    const int cm = partials || act != P8X_ACT_Q8_128 ? kCmAll : class_set(t->class_tiles);
+    const int cm = partials || act != P8X_ACT_Q8_128 ? kCmAll : class_set(t->class_tiles, t->lin_words != 0);
     p.gpt = gemv_waves(ncols, act, partials, cm);
     const int octets = (t->ng + p.gpt - 1) / p.gpt;
     const int slots = gemv_wg_per_cu(ncols, act, partials, cm) * num_cus();
@@ -185,8 +186,8 @@ static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float
     g.M = t->M; g.S = t->Sg; g.D = t->D; g.prm = t->prm; g.prmd = t->prmd;
     g.cp = t->cp; g.cc = t->cc; g.cv = t->cv;
     g.q = q; g.d = d; g.x = x; g.ldx = (unsigned)ldx; g.y = y; g.ldy = (unsigned)ldy; g.partials = partials;
-    g.wpart = t->wpart; g.wcnt = t->wcnt;
-    g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl;
+    g.wpart = t->wpart; g.wcnt = t->wcnt; g.wslot = t->wslot;
+    g.rows = t->rows; g.K = t->K; g.nb = t->nb; g.ng = t->ng; g.nsl = t->nsl; g.lin = t->lin_words;
     g.kchunk = kchunk; g.nks = nks; g.task0 = task0; g.ntasks = ((t->ng + gpt - 1) / gpt) * nks;
     g.dbytes = (unsigned)(t->kbytes - offset_D(t->nt));
     g.ic = t->ic;
@@ -197,7 +198,7 @@ static void fill_job(GemvJob &g, const p8x_tensor *t, const void *q, const float
 // call's): y at those groups' original rows, partials [ncols][32 ng][blocks]
 int launch_gemv_range(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                       float *y, size_t ldy, int32_t *partials, int g0, int ng, hipStream_t st) {
-    const int cm = class_set(t->class_tiles);
+    const int cm = class_set(t->class_tiles, t->lin_words != 0);
     if (partials) {   // integer partials: one column per launch
         const GemvPlan p1 = gemv_plan(t, 1, act, true);
         if (p1.nks > 1 && (size_t)p1.nks * t->rows > t->wpart_floats) return set_error(P8X_ERR_UNSUPPORTED, "gemv: partial workspace too small");
@@ -230,7 +231,7 @@ int launch_gemv_range(const p8x_tensor *t, int act, const void *q, const float *
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
                 float *y, size_t ldy, int32_t *partials, hipStream_t st) {
-    const int cm = class_set(t->class_tiles);
+    const int cm = class_set(t->class_tiles, t->lin_words != 0);
     if (partials) return launch_gemv_range(t, act, q, d, ncols, x, ldx, y, ldy, partials, 0, t->ng, st);
     // the row-group kernel: one column, or two columns of a one-class tensor with K <= 8192 (measured faster
     // than the multi-column task kernel there, slower for longer K and more columns)
@@ -259,12 +260,14 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
 int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
                     RgJobs &R, int &cm, int &ng) {
     size_t hist[8] = {0};
+    bool in_order = true;
     ng = 0;
     for (int i = 0; i < n; ++i) {
         for (int c = 0; c < 8; ++c) hist[c] += ts[i]->class_tiles[c];
         ng += ts[i]->ng;
+        in_order = in_order && ts[i]->lin_words != 0;
     }
-    cm = class_set(hist);
+    cm = class_set(hist, in_order);
     // the K plan of the combined row groups: K-chunks that fit the LDS buffer, split in two when they fill at most
     // half the CUs and K is long (the single-call rule)
     const p8x_tensor *t0 = ts[0];
@@ -291,8 +294,7 @@ int plan_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t l
     if (out) {
         R.glu = 1;
         R.glu_out = out;
-        R.glu_pair = t0->wglu;
-        R.glu_cnt = t0->wglu_cnt;
+        R.glu_slot = t0->wglu;
     }
     return P8X_OK;
 }

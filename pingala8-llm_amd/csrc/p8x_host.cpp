@@ -137,7 +137,7 @@ int p8x_probe(const void *slot, size_t n, int rows, int K) {
 
 void p8x_release(p8x_tensor *t) {
     if (!t) return;
-    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->wy, (void *)t->wglu, (void *)t->wglu_cnt, (void *)t->djob, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
+    for (void *p : {(void *)t->owned, (void *)t->Dl, (void *)t->wy, (void *)t->wglu, (void *)t->wslot, (void *)t->djob, (void *)t->Sg, (void *)t->a2, (void *)t->ic, (void *)t->cp, (void *)t->cc, (void *)t->cv, (void *)t->wq,
                     (void *)t->wd, (void *)t->wsum, (void *)t->wq81, (void *)t->wpart, (void *)t->wcnt, (void *)t->drows, (void *)t->pinv, (void *)t->prmd, (void *)t->wx16, (void *)t->wmm})
         if (p) (void)hipFree(p);
     delete t;
@@ -243,6 +243,12 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
     t->ic_hash = ic_hash;
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
+    for (int c = 1; c < 8; ++c)
+        if (hist[c] == nt) {   // one class: are the tiles in order (tile i at word i * 64 nw)?
+            t->lin_words = 64u * (unsigned)nw_of(c);
+            for (size_t i = 0; i < nt && t->lin_words; ++i)
+                if ((size_t)(M[i] & 0x1FFFFFFFu) != i * t->lin_words) t->lin_words = 0;
+        }
     memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
     if ((rc = scratch_resolve(t->device))) { delete t; return rc; }   // set-up of the no-allocation entry point
@@ -315,9 +321,10 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->wq81, (size_t)36 * P8X_MAX_COLS * (K / 32), "q8_1"))) return fail(rc);
     if ((rc = alloc((void **)&t->wpart, 4 * t->wpart_floats, "partials"))) return fail(rc);
     if ((rc = alloc((void **)&t->wy, 4 * (size_t)P8X_MAX_COLS * rows, "x16 plane rows"))) return fail(rc);
-    if ((rc = alloc((void **)&t->wglu, 8 * (size_t)rows, "gate / up values"))) return fail(rc);
-    if ((rc = alloc((void **)&t->wglu_cnt, 4 * (size_t)rows, "gate / up counters"))) return fail(rc);
-    if ((rc = hip_check(hipMemset(t->wglu_cnt, 0, 4 * (size_t)rows), "p8x_prepare: gate / up counters"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wglu, 8 * (size_t)rows, "gate / up slots"))) return fail(rc);
+    if ((rc = hip_check(hipMemset(t->wglu, 0, 8 * (size_t)rows), "p8x_prepare: gate / up slots"))) return fail(rc);
+    if ((rc = alloc((void **)&t->wslot, 8 * (size_t)rows, "K-half slots"))) return fail(rc);
+    if ((rc = hip_check(hipMemset(t->wslot, 0, 8 * (size_t)rows), "p8x_prepare: K-half slots"))) return fail(rc);
     if ((rc = alloc((void **)&t->wcnt, 4 * (size_t)ng, "counters"))) return fail(rc);
     {
         std::vector<int16_t> pinv(rows);

@@ -44,8 +44,9 @@ struct p8x_tensor {
     int32_t *wsum = nullptr;         // [P8X_MAX_COLS][nsl]
     uint8_t *wq81 = nullptr;         // block_q8_1 [P8X_MAX_COLS][K / 32]
     float *wy = nullptr;             // x16 products: plane rows [2 x 4][rows]
-    float *wglu = nullptr;           // gate / up meeting (this tensor as the gate): values [2][rows]
-    unsigned *wglu_cnt = nullptr;    // and arrival counters [rows], 0 between calls
+    unsigned lin_words = 0;               // one class, tiles in order: payload words per tile (else 0)
+    unsigned long long *wglu = nullptr;   // gate / up meeting slots (this tensor as the gate) [rows], 0 between calls
+    unsigned long long *wslot = nullptr;  // K-half meeting slots of one-column two-chunk plans [rows], 0 between calls
     uint64_t ic_hash = 0;            // hash of the rotation sg / c (tensors with equal hashes share quantized inputs)
     p8x::GemvJob *djob = nullptr;    // the tensor's metadata as a device-side GEMV job (launches over several tensors)
     float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan

@@ -120,6 +120,10 @@ __device__ __forceinline__ void step_stage(kptr<const StepStage> sp, int v, RgSm
         if (PC != 0 && first && pre_on) bstart = pre.finish(c, sm, yacc);
         first = false;
         for (int b = bstart; b < (g < J.ng ? b1 : b0);) {
+            if constexpr (PC != 0) {   // one class: no tile word to read
+                b = gemv_run<1, P8X_ACT_Q8_128, false, PC, gemv_nbuf(1, PC), true>(c, sm, b, b1, yacc);
+                continue;
+            }
             const uint32_t mt = as_const(J.M)[(size_t)g * J.nb + b];
             switch (mt >> 29) {
                 case 1: if constexpr ((CM >> 1) & 1) { b = gemv_run<1, P8X_ACT_Q8_128, false, 1, gemv_nbuf(1, 1), CM == (1 << 1)>(c, sm, b, b1, yacc); break; } [[fallthrough]];
@@ -139,7 +143,13 @@ __device__ __forceinline__ void step_stage(kptr<const StepStage> sp, int v, RgSm
             float vr = 0.f;
             if (lane < 32)
                 for (int i = 0; i < wpg; ++i) vr += sm.red[set][w + i][0][lane];
-            if (nks > 1) {   // K-chunks: the last arrival sums them in chunk order
+            bool fin = lane < 32;   // lanes that finish their row here
+            if (nks == 2) {   // two K-halves: each row's halves meet in its slot (pair_meet)
+                int oi;
+                float other;
+                fin = fin && pair_meet(as_global_rw(J.wslot) + 32 * g + lane, ks, vr, oi, other);
+                if (fin) vr = ks == 0 ? vr + other : other + vr;   // chunk 0 + chunk 1 either way
+            } else if (nks > 2) {   // K-chunks: the last arrival sums them in chunk order
                 const gptr<float> wpart = as_global_rw(J.wpart);
                 const gptr<unsigned> wcnt = as_global_rw(J.wcnt);
                 if (lane < 32) __hip_atomic_store(&wpart[(size_t)ks * J.rows + 32 * g + lane], vr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -153,13 +163,13 @@ __device__ __forceinline__ void step_stage(kptr<const StepStage> sp, int v, RgSm
             }
             const int r = ro & 0x7FFF;
             float vo = vr;
-            if (lane < 32 && (ro & 0x8000)) {
+            if (fin && (ro & 0x8000)) {
                 float *xr = const_cast<float *>(J.x);
                 for (int e = as_global(J.cp)[r]; e < as_global(J.cp)[r + 1]; ++e)
                     vo += as_global(J.cv)[e] * __hip_atomic_load(&xr[as_global(J.cc)[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (glu) glu_meet(sp->R.glu_pair, sp->R.glu_cnt, sp->R.glu_out, sp->R.j0.rows, jb, r, vo, lane < 32);
-            else if (lane < 32) __hip_atomic_store(&as_global_rw(J.y)[r], vo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (glu) glu_meet(sp->R.glu_slot, sp->R.glu_out, jb, r, vo, fin);
+            else if (fin) __hip_atomic_store(&as_global_rw(J.y)[r], vo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -250,6 +260,7 @@ int p8x_step_create(const p8x_step_stage *stages, int n, p8x_step **out) {
     *out = nullptr;
     std::vector<StepStage> hs(n);
     size_t hist[8] = {0};
+    bool in_order = true;
     const p8x_tensor *t0 = nullptr;
     for (int s = 0; s < n; ++s) {
         const p8x_step_stage &st = stages[s];
@@ -262,6 +273,7 @@ int p8x_step_create(const p8x_step_stage *stages, int n, p8x_step **out) {
             if (memcmp(t->a2_host, t0->a2_host, sizeof t->a2_host))
                 return set_error(P8X_ERR_UNSUPPORTED, "p8x_step_create: stage %d tensor %d has a different codebook", s, i);
             for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
+            in_order = in_order && t->lin_words != 0;
         }
         const bool glu = st.glu_out != nullptr;
         if (glu && (st.n != 2 || st.tensors[0]->rows != st.tensors[1]->rows))
@@ -281,7 +293,7 @@ int p8x_step_create(const p8x_step_stage *stages, int n, p8x_step **out) {
     }
     p8x_step *sp = new p8x_step();
     sp->nst = n;
-    sp->cm = class_set(hist) == kCmC3 ? kCmC3 : kCmAll;
+    sp->cm = class_set(hist, in_order) == kCmC3 ? kCmC3 : kCmAll;
     sp->a2 = t0->a2;
     int rc = sp->cm == kCmC3 ? step_grid<kCmC3>(&sp->grid) : step_grid<kCmAll>(&sp->grid);
     if (!rc && hipMalloc((void **)&sp->dstages, sizeof(StepStage) * n) != hipSuccess) rc = set_error(P8X_ERR_NOMEM, "p8x_step_create: hipMalloc stages");

@@ -127,6 +127,30 @@ def random_slot(rng, rows, K, classes=(3,), class_p=None, tables="shipped", nd=0
     return build_slot(A, cs, cls, payload, S, c16v, prm, sg, drow, dcol, dval, extra=extra)
 
 
+def shuffle_tiles(buf, rows, K, rng):
+    """The same tensor with its tiles stored in D in a random order (M offsets follow): every tile's class, words
+    and decoded values are unchanged; only the physical order differs (the contract allows any order)."""
+    ng, nb = rows // 32, K // 256
+    nt = ng * nb
+    M = buf[2064:2064 + 4 * nt].view(np.uint32).copy()
+    offD = a16(2064 + 68 * nt)
+    cls = (M >> 29).astype(np.int64)
+    size = np.array([64 * NW[c] for c in cls], np.int64)
+    old = (M & 0x1FFFFFFF).astype(np.int64)
+    D = buf[offD:offD + 4 * int(size.sum())].view(np.uint32)
+    newD = np.empty_like(D)
+    new = np.zeros(nt, np.int64)
+    off = 0
+    for t in rng.permutation(nt):
+        new[t] = off
+        newD[off:off + size[t]] = D[old[t]:old[t] + size[t]]
+        off += size[t]
+    out = buf.copy()
+    out[2064:2064 + 4 * nt] = (new.astype(np.uint32) | (cls.astype(np.uint32) << 29)).view(np.uint8)
+    out[offD:offD + 4 * off] = newD.view(np.uint8)
+    return out
+
+
 def tie_case(rng, K=512, k=2):
     """A 32 x K class-3 tensor with c16 = 1 and an activation x whose rotated values x' land exactly on quantizer
     ties. In 256-block b = 0, 1 only x'[0] = a, x'[1] = b are non-zero before the transform, so after FWHT256 / 16

@@ -14,8 +14,9 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "pingala8-llm_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
-# the single-call row-group kernel (one and two columns, K split) and the task kernel (K-chunk fix-up)
-UNITS = ["p8x_gemv_w.hip", "p8x_gemv_rgm.hip", "p8x_gemv_q81.hip"]
+# the single-call row-group kernel (one and two columns, K split), the task kernel (K-chunk fix-up) and the
+# one-launch step (K-chunk fix-up, stage barrier)
+UNITS = ["p8x_gemv_rg1.hip", "p8x_gemv_rgm.hip", "p8x_gemv_q81.hip", "p8x_step.hip"]
 
 
 def hipflags():

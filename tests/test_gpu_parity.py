@@ -518,3 +518,31 @@ def slotgen_offsets(slot, rows, K):
     import slotgen
     nd = int(np.frombuffer(slot[-32:].tobytes(), np.uint32)[3])
     return slotgen.offsets(slot.size, rows, K, nd)
+
+
+@pytest.mark.parametrize("cls", [3, 6])
+def test_one_class_tiles_out_of_order(cls):
+    """A one-class tensor whose tiles lie in D out of (row group, block) order: the one-class kernels compute payload
+    offsets, so the host must route it to the kernels that read the tile words. Same tensor stored both ways: equal
+    results (single calls, two columns, several linears in one launch, swiglu, dequantize) and the fp64 oracle."""
+    import slotgen
+    rng = np.random.default_rng(90 + cls)
+    rows, K = 256, 8192   # 8 row groups, 32 blocks: the single call splits K in two (pair meet)
+    slot = slotgen.random_slot(rng, rows, K, classes=(cls,), nd=3)
+    shuf = slotgen.shuffle_tiles(slot, rows, K, rng)
+    assert not np.array_equal(shuf, slot)
+    t_in, t_sh = p8x.Tensor(slot, rows, K), p8x.Tensor(shuf, rows, K)
+    orc = O.Oracle(shuf, rows, K)
+    X = rng.standard_normal((2, K)).astype(np.float32)
+    y_in, y_sh = t_in.mul_mat_vec(X[0])[0], t_sh.mul_mat_vec(X[0])[0]
+    assert rel_l2(y_sh, orc.gemv_f64(X[0])) < REL_L2
+    assert np.array_equal(y_sh, y_in)
+    Y = t_sh.mul_mat_vec(X)
+    for n in range(2):
+        assert rel_l2(Y[n], orc.gemv_f64(X[n])) < REL_L2
+    a, b = p8x.mul_mat_vec_multi([t_in, t_sh], X[0])
+    assert np.array_equal(a, y_in) and np.array_equal(b, y_sh)
+    g = p8x.mul_mat_vec_glu(t_in, t_sh, X[0])
+    ref = (y_in.astype(np.float64) / (1.0 + np.exp(-y_in.astype(np.float64)))) * y_sh
+    assert rel_l2(g, ref) < 1e-6
+    assert np.array_equal(t_sh.dequantize(p8x.F32).view(np.uint32), t_in.dequantize(p8x.F32).view(np.uint32))
