@@ -613,13 +613,10 @@ __device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v
 // SPLIT: J.nks K-chunks (else the whole K, J.nks == 1). NCOL columns of x (stride J.ldx) and y (stride J.ldy);
 // NCOL x (blocks of a chunk) <= kRgMaxBlocks. gc row groups at a time: the waves form gc teams of WAVES / gc,
 // team t takes row group g0 + t * (workgroups per chunk) over the chunk, so that a workgroup with several row
-// groups streams them together instead of one after another. The activations, K plan and rotation come from job 0;
-// the leading arguments repeat what the prologue needs of them (x, ic, the codebook words, nb, kchunk, nks, ldx),
-// so that a build with kernel-argument preloading has them in SGPRs when the waves start.
+// groups streams them together instead of one after another. The activations, K plan and rotation come from job 0.
 template <int CM, bool SPLIT, int NCOL, bool TEAMS, bool MULTI>
 __global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
-void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, const uint32_t *__restrict__ a2, int nb0, int kchunk0,
-               int nks0, unsigned ldx0, RgJobs jobs, int gc_) {
+void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
@@ -645,9 +642,9 @@ void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, cons
     c.bankbytes = (uint32_t)(c.j << 2) * 0x01010101u;
     c.xlane = c.hs * 64;
     // workgroup b (of the job's nwg): K-chunk ks = b % nks of row groups b / nks, b / nks + nwg / nks, ...
-    const int nks = SPLIT ? nks0 : 1;
-    const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(kchunk0, nb0 - ks * kchunk0) : nb0;
-    c.b0 = ks * kchunk0; c.nbl = nbk;
+    const int nks = SPLIT ? J.nks : 1;
+    const int ks = SPLIT ? wgl % nks : 0, nbk = SPLIT ? min(J.kchunk, J.nb - ks * J.kchunk) : J.nb;
+    c.b0 = ks * J.kchunk; c.nbl = nbk;
     const int wpg = WAVES / gc, team = w / wpg, wk = w % wpg;   // waves beyond gc teams stay idle
     const int per = nbk / wpg, rem = nbk % wpg;
     int b0 = c.b0 + wk * per + min(wk, rem), b1 = b0 + per + (wk < rem ? 1 : 0);   // the wave's K range
@@ -659,7 +656,7 @@ void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, cons
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
         const int it = w + i * WAVES, n = NCOL == 1 ? 0 : it / nbk, bk = c.b0 + (NCOL == 1 ? it : it % nbk);   // column, block
-        if (it < NCOL * nbk) in[i].load(x0 + (size_t)n * ldx0 + 256 * bk, ic0 + 256 * bk, lane);
+        if (it < NCOL * nbk) in[i].load(J.x + (size_t)n * J.ldx + 256 * bk, J.ic + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
     CosetTableFill<64 * WAVES> fill;
@@ -674,7 +671,7 @@ void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, cons
         // on every path (a wave without work requests one in-range tile it never reads), so that no control-flow
         // merge before the table stores makes the compiler wait for these loads there
         c.g = min(gfirst, J.ng - 1);
-        const int bb = pre_on ? b0 : min(b0, nb0 - 1);
+        const int bb = pre_on ? b0 : min(b0, J.nb - 1);
         pre.begin(c, bb, pre_on ? b1 : bb + 1);
     }
     __asm__ volatile("" ::: "memory");
@@ -765,7 +762,7 @@ void k_gemv_rg(const float *__restrict__ x0, const float *__restrict__ ic0, cons
             for (int n = 0; n < NCOL; ++n) {
                 vo[n] = v[n];
                 if (fin && (ro & 0x8000)) {
-                    const gptr<const float> xr = as_global(x0) + (size_t)n * ldx0;   // the shared activations
+                    const gptr<const float> xr = as_global(J.x) + (size_t)n * J.ldx;   // the shared activations
                     for (int e = as_global(JB.cp)[r]; e < as_global(JB.cp)[r + 1]; ++e) vo[n] += as_global(JB.cv)[e] * xr[as_global(JB.cc)[e]];
                 }
             }
@@ -789,12 +786,9 @@ static int launch_gemv_rg_t(const RgJobs &jobs, int ng, const uint32_t *a2, hipS
     const int nks = jobs.j0.nks;
     // several jobs: each takes ceil(its row groups / per) workgroups per K-chunk (wgbase, set by the caller)
     const int grid = MULTI ? jobs.wgbase[4] : (ng + per - 1) / per * nks;
-    const GemvJob &j0 = jobs.j0;
-#define P8X_RG_ARGS j0.x, j0.ic, a2, j0.nb, j0.kchunk, j0.nks, j0.ldx, jobs
-    if (nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, 1);
-    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, gc);
-    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, P8X_RG_ARGS, 1);
-#undef P8X_RG_ARGS
+    if (nks > 1) hipLaunchKernelGGL((k_gemv_rg<CM, true, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
+    else if (gc > 1) hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, true, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, gc);
+    else hipLaunchKernelGGL((k_gemv_rg<CM, false, NCOL, false, MULTI>), dim3(grid), dim3(64 * rg_waves(NCOL)), 0, st, jobs, a2, 1);
     return hip_check(hipGetLastError(), "k_gemv_rg launch");
 }
 

@@ -16,7 +16,7 @@ CSRC = os.path.join(ROOT, "pingala8-llm_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 # the single-call row-group kernel (one and two columns, K split), the task kernel (K-chunk fix-up) and the
 # one-launch step (K-chunk fix-up, stage barrier)
-UNITS = ["p8x_gemv_rg1.hip", "p8x_gemv_rgm.hip", "p8x_gemv_q81.hip", "p8x_step.hip"]
+UNITS = ["p8x_gemv_w.hip", "p8x_gemv_rgm.hip", "p8x_gemv_q81.hip", "p8x_step.hip"]
 
 
 def hipflags():
