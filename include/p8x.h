@@ -128,9 +128,9 @@ int p8x_vec_dot_rows(const p8x_tensor *t, int act, const void *q, const float *d
                      float *y, size_t ldy, int32_t *partials, void *stream);
 /* y = W x for 1..8 columns (vr_mul_mat_vec, CPU.patch:4466-4521): activation prep + fused decode-GEMV +
  * un-permute + clamp delta. x [ncols][ldx] f32, y [ncols][ldy] f32, original rows. One launch for one column
- * (and two columns of short K), deterministic. The K-chunk partial rows and arrival counters live in the
- * tensor's handle: calls on one tensor from different streams must not overlap (on one stream they are
- * ordered); the counters are put back by each call. Records kernel launches only (capture-safe). */
+ * (and two columns of short K), deterministic. The K-chunk partial rows, arrival counters and meeting slots live
+ * in the tensor's handle: calls on one tensor from different streams must not overlap (on one stream they are
+ * ordered); counters and slots are put back by each call. Records kernel launches only (capture-safe). */
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 /* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1, or P8X_ACT_X16 (1..4
  * columns: both planes of each column through one GEMV, summed, then the clamp delta; the reference's CPU default) */
