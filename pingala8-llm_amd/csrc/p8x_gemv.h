@@ -580,6 +580,17 @@ __device__ __forceinline__ void rg_quantize(int nbk, RgSmem<NCOL> &sm, const Blo
 // wgbase[i] .. wgbase[i + 1] - 1 take job i, whose tensor metadata comes from its tensor's device copy jt[i] and
 // its output from y[i] / ldy[i] (selected once, by comparisons: indexing the arguments at run time would copy them
 // to scratch). Unused wgbase entries are INT_MAX.
+// Timeline build (make timeline, -DP8X_TIMELINE; never the product library): thread 0 of every row-group workgroup
+// records s_memrealtime (100 MHz) at its start, once the kernel-argument fields are in, once its first loads are in
+// (it waits for them there, which the product kernel does not), after the table and the quantization, after the
+// barrier, after its tiles and at its end, into records [kTimelineRecords][8] = {block << 32 | grid, 7 stamps}.
+#ifdef P8X_TIMELINE
+constexpr unsigned kTimelineRecords = 65536;
+unsigned long long *timeline_buf();   // device: the records, then the record counter
+#define P8X_STAMP(k) do { if (threadIdx.x == 0) stamp[k] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define P8X_STAMP(k) do {} while (0)
+#endif
 constexpr int kRgMaxJobs = 4;
 struct RgJobs {
     GemvJob j0;                        // job 0: activations, K plan and rotation of every job
@@ -591,6 +602,9 @@ struct RgJobs {
     int glu;
     float *glu_out;        // [rows] original rows
     unsigned long long *glu_slot;   // [rows] gate / up meeting slots by original row, 0 between calls
+#ifdef P8X_TIMELINE
+    unsigned long long *tl;
+#endif
 };
 
 template <typename T>
@@ -636,6 +650,14 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     }
     const GemvJob &J = JL;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+#ifdef P8X_TIMELINE
+    unsigned long long stamp[7] = {0, 0, 0, 0, 0, 0, 0};
+    unsigned slot = 0;
+    if (tid == 0) {
+        stamp[0] = __builtin_amdgcn_s_memrealtime();
+        slot = __hip_atomic_fetch_add((unsigned *)(jobs.tl + kTimelineRecords * 8), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#endif
     TaskCtx<NCOL, P8X_ACT_Q8_128> c;
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
@@ -659,6 +681,10 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         if (it < NCOL * nbk) in[i].load(J.x + (size_t)n * J.ldx + 256 * bk, J.ic + 256 * bk, lane);
         else in[i] = BlockLane{};   // quantized alongside (results dropped): defined values
     }
+#ifdef P8X_TIMELINE
+    __asm__ volatile("" :: "s"(J.M), "s"(J.ng));
+#endif
+    P8X_STAMP(1);
     CosetTableFill<64 * WAVES> fill;
     fill.load(a2, tid);
     constexpr int PC = CM == kCmC3 ? 3 : CM == kCmC6 ? 6 : 0;
@@ -675,13 +701,19 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         pre.begin(c, bb, pre_on ? b1 : bb + 1);
     }
     __asm__ volatile("" ::: "memory");
+#ifdef P8X_TIMELINE
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+    P8X_STAMP(2);
     fill.store(sm.tab, tid);
     // the blocks of a wave are independent: quantized G at a time in straight-line code, so their cross-lane
     // chains overlap (one at a time they cost a full chain latency each)
     if (NCOL * nbk <= WAVES) rg_quantize<1, NCOL>(nbk, sm, in, w, lane);
     else if (NCOL * nbk <= 2 * WAVES) rg_quantize<2, NCOL>(nbk, sm, in, w, lane);
     else rg_quantize<4, NCOL>(nbk, sm, in, w, lane);
+    P8X_STAMP(3);
     __syncthreads();
+    P8X_STAMP(4);
     int set = 0;
     const GemvJob &JB = J;
     bool first = true;
@@ -715,6 +747,7 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
                 default: ++b; break;   // class 0: zero weights
             }
         }
+        P8X_STAMP(5);
 #pragma unroll
         for (int n = 0; n < NCOL; ++n) {
             yacc[n] += __shfl_xor(yacc[n], 32);
@@ -774,11 +807,26 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
             }
         }
     }
+#ifdef P8X_TIMELINE
+    if (tid == 0) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        stamp[6] = __builtin_amdgcn_s_memrealtime();
+        if (slot < kTimelineRecords) {
+            unsigned long long *o = jobs.tl + (size_t)slot * 8;
+            o[0] = ((unsigned long long)blockIdx.x << 32) | gridDim.x;
+            for (int k = 0; k < 7; ++k) o[1 + k] = stamp[k];
+        }
+    }
+#endif
 }
 
 // ng = the row groups of all jobs; the K plan (nks) is job 0's
 template <int CM, int NCOL, bool MULTI>
-static int launch_gemv_rg_t(const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st) {
+static int launch_gemv_rg_t(const RgJobs &jobs_, int ng, const uint32_t *a2, hipStream_t st) {
+    RgJobs jobs = jobs_;
+#ifdef P8X_TIMELINE
+    jobs.tl = timeline_buf();
+#endif
     // whole row groups per workgroup, evenly: ceil(ng / ceil(ng / CUs)) workgroups per K-chunk, one per CU
     const int per = (ng + num_cus() - 1) / num_cus();
     // a workgroup's row groups are streamed together (teams of waves), up to 4 at a time

@@ -26,6 +26,15 @@
 
 namespace p8x {
 
+#ifdef P8X_TIMELINE
+unsigned long long *timeline_buf() {
+    static unsigned long long *b = nullptr;
+    const size_t bytes = ((size_t)kTimelineRecords * 8 + 1) * 8;
+    if (!b && hipMalloc((void **)&b, bytes) == hipSuccess) (void)hipMemset(b, 0, bytes);
+    return b;
+}
+#endif
+
 struct StepStage {
     RgJobs R;   // the stage's linears: activations and K plan (R.j0), tensor metadata (R.jt), outputs, swiglu
     int nvwg;   // virtual workgroups of the stage (row-group assignments), R.wgbase[kRgMaxJobs]
@@ -338,6 +347,21 @@ int p8x_step_check(p8x_step *sp) {
     }
     return P8X_OK;
 }
+
+#ifdef P8X_TIMELINE
+// timeline build only: the row-group kernel's records (first n bytes) and their count; reset sets the count to 0
+// (call it before capturing launches: it allocates the buffer on first use)
+int p8x_timeline_read(void *host, size_t n, unsigned *count) {
+    if (!timeline_buf()) return set_error(P8X_ERR_NOMEM, "p8x_timeline_read: no buffer");
+    int rc = hip_check(hipMemcpy(host, timeline_buf(), n, hipMemcpyDeviceToHost), "p8x_timeline_read");
+    if (!rc) rc = hip_check(hipMemcpy(count, timeline_buf() + (size_t)kTimelineRecords * 8, 4, hipMemcpyDeviceToHost), "p8x_timeline_read");
+    return rc;
+}
+int p8x_timeline_reset(void) {
+    if (!timeline_buf()) return set_error(P8X_ERR_NOMEM, "p8x_timeline_reset: no buffer");
+    return hip_check(hipMemset(timeline_buf() + (size_t)kTimelineRecords * 8, 0, 8), "p8x_timeline_reset");
+}
+#endif
 
 int p8x_step_info(const p8x_step *sp, int *grid, int *stages, int *class_set_) {
     if (!sp) return set_error(P8X_ERR_ARG, "p8x_step_info: null step");

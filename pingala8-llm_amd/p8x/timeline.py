@@ -1,0 +1,106 @@
+"""Where a row-group GEMV launch spends its time: per-workgroup timestamps over the dependency-respecting decode step.
+
+Needs the timeline build (`make -C pingala8-llm_amd/csrc timeline` -> p8x/libp8x_timeline.so): thread 0 of every
+k_gemv_rg workgroup records s_memrealtime (100 MHz) at its start, when the kernel-argument fields are in, when its first
+loads are in (the timeline build waits for them there), after the coset table and the activation quantization, after
+the workgroup barrier, after its tiles, and at its end. The chain replayed from one HIP graph is the one bench.py's
+dependent_step measures: per layer {q,k,v} -> o -> {gate,up}+swiglu -> down, then the head shards, each launch reading
+its producer's output (Llama-3.1-8B shapes, class-3 tensors).
+
+    python -m p8x.timeline [--layers 32]
+
+prints, per kind of launch, the median and maximum over workgroups of each stamp (us from the launch's first
+workgroup start), averaged over the launches of that kind, and the gap from the previous launch's last workgroup end
+to this launch's first workgroup start.
+"""
+import argparse
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+import p8x
+
+STAMPS = ["start", "args in", "loads in", "table+quant", "barrier", "tiles", "end"]
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--replays", type=int, default=20, help="untimed graph replays before the recorded one")
+    args = ap.parse_args()
+    p8x.LIB_PATH = os.path.join(p8x.HERE, "libp8x_timeline.so")
+    L = p8x.lib()
+    if not hasattr(L, "p8x_timeline_read"):
+        raise p8x.P8xError(f"{p8x.LIB_PATH} is not the timeline build")
+    L.p8x_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint)]
+    p8x.check(L.p8x_timeline_reset(), "p8x_timeline_reset")   # allocates the record buffer before any capture
+    root = os.path.dirname(os.path.dirname(p8x.HERE))
+    sys.path.insert(0, root)
+    import bench
+    tensors, kinds, _ = bench.build_stack(args.layers, "c3", 0)
+    nl = args.layers
+    layer = [tensors[7 * l:7 * l + 7] for l in range(nl)]
+    head = tensors[7 * nl:]
+    x0 = p8x.DeviceBuffer.from_numpy(np.random.default_rng(9).standard_normal(layer[0][0].K).astype(np.float32))
+    plan, cur = [], x0
+    for q, k, v, o, gate, up, down in layer:
+        yq, yk, yv = (p8x.DeviceBuffer(4 * t.rows) for t in (q, k, v))
+        yo, yg, yd = p8x.DeviceBuffer(4 * o.rows), p8x.DeviceBuffer(4 * gate.rows), p8x.DeviceBuffer(4 * down.rows)
+        plan.append(((q, k, v), cur, (yq, yk, yv), (o, yq, yo), (gate, up, yo, yg), (down, yg, yd)))
+        cur = yd
+    yh = [p8x.DeviceBuffer(4 * t.rows) for t in head]
+
+    def enqueue(s):
+        for qkv, xin, yqkv, (o, xo, yo), (gate, up, xg, yg), (down, xd, yd) in plan:
+            p8x.mul_mat_vec_multi_dev(list(qkv), xin, list(yqkv), stream=s)
+            o.mul_mat_vec_dev(xo, yo, stream=s)
+            p8x.mul_mat_vec_glu_dev(gate, up, xg, yg, stream=s)
+            down.mul_mat_vec_dev(xd, yd, stream=s)
+        p8x.mul_mat_vec_multi_dev(head, cur, yh, stream=s)
+
+    st = p8x.Stream()
+    graph = p8x.Graph(enqueue, st)
+    for _ in range(args.replays):
+        graph.launch(st)
+    st.sync()
+    p8x.check(L.p8x_timeline_reset(), "p8x_timeline_reset")
+    graph.launch(st)
+    st.sync()
+    nrec = 65536
+    buf = np.zeros((nrec, 8), np.uint64)
+    n = ctypes.c_uint()
+    p8x.check(L.p8x_timeline_read(buf.ctypes.data, buf.nbytes, ctypes.byref(n)), "p8x_timeline_read")
+    graph.release()
+    rec = buf[:min(n.value, nrec)].astype(np.int64)
+    # records in arrival order; launches on one stream do not overlap, so consecutive runs of `grid` records are
+    # one launch each
+    grid = rec[:, 0] & 0xFFFFFFFF
+    launches, i = [], 0
+    while i < len(rec):
+        launches.append(rec[i:i + grid[i], 1:8])
+        i += int(grid[i])
+    names = ["q/k/v", "o", "gate/up+swiglu", "down"]
+    rows = {}
+    prev_end = None
+    for li, t in enumerate(launches):
+        kind = names[li % 4] if li < 4 * nl else "head"
+        base = t[:, 0].min()
+        med = [(np.median(t[:, j]) - base) / 100.0 for j in range(7)]
+        mx = [(t[:, j].max() - base) / 100.0 for j in range(7)]
+        gap = (base - prev_end) / 100.0 if prev_end is not None else np.nan
+        prev_end = t[:, 6].max()
+        rows.setdefault(kind, []).append(med + mx + [gap, len(t)])
+    print(f"{len(launches)} launches, {len(rec)} workgroup records; us from the launch's first workgroup start")
+    print("| launch | workgroups | " + " | ".join(STAMPS[1:]) + " | gap before |")
+    print("|---|---|" + "---|" * 7)
+    for kind, v in rows.items():
+        m = np.nanmean(np.array(v, np.float64), axis=0)
+        cells = [f"{m[j]:.2f} / {m[7 + j]:.2f}" for j in range(1, 7)]
+        print(f"| {kind} | {int(m[15])} | " + " | ".join(cells) + f" | {m[14]:.2f} |")
+    print("(each cell: median / maximum over the workgroups, averaged over the launches of that kind)")
+
+
+if __name__ == "__main__":
+    main()
