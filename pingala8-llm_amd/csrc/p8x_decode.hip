@@ -328,22 +328,22 @@ __device__ __forceinline__ uint2 fwht4_entry(uint32_t w) {
     return make_uint2((uint32_t)(uint16_t)y0 | ((uint32_t)(uint16_t)y1 << 16), (uint32_t)(uint16_t)y2 | ((uint32_t)(uint16_t)y3 << 16));
 }
 
-// Payload words of lane-slice (hs, j) of a class-C tile, loaded so that after the bit rotation of lo_decode the
-// lane's fields start at chunk 16 p: the stored field k is chunk k, so the bitstring is rotated right by d = 16 p
-// fields (whole words here, the rest in lo_decode).
+// Payload words of lane-slice (hs, j) of a class-C tile (p: the half-slice's words of the wave's LDS copy, device
+// layout), read so that after the bit rotation of lo_decode the lane's fields start at chunk 16 p: the stored field
+// k is chunk k, so the bitstring is rotated right by d = 16 p fields (whole words here, the rest in lo_decode).
 template <int C>
-__device__ __forceinline__ void lo_load(uint32_t (&w)[8], const uint32_t *__restrict__ p, int j, int d) {
+__device__ __forceinline__ void lo_read(uint32_t (&w)[8], const uint32_t *p, int j, int d) {
     constexpr int W1 = w1_of(C), NW = nw_of(C);
     if constexpr (W1 == 8) {
         const int wr = d >> 2;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) w[m] = __builtin_nontemporal_load(p + dev_word((m + wr) & 7, j, NW));
+        for (int m = 0; m < 8; ++m) w[m] = p[dev_word((m + wr) & 7, j, NW)];
     } else {
         constexpr int W = W1 - 1;
         const int wr = (d * W) >> 5;
-        w[0] = __builtin_nontemporal_load(p + dev_word(0, j, NW));
+        w[0] = p[dev_word(0, j, NW)];
 #pragma unroll
-        for (int m = 0; m < W; ++m) w[1 + m] = __builtin_nontemporal_load(p + dev_word(1 + (m + wr) % W, j, NW));
+        for (int m = 0; m < W; ++m) w[1 + m] = p[dev_word(1 + (m + wr) % W, j, NW)];
 #pragma unroll
         for (int m = W + 1; m < 8; ++m) w[m] = 0u;
     }
@@ -404,11 +404,11 @@ __device__ __forceinline__ void lo_decode_any(int c, const uint32_t (&w)[8], int
 }
 
 template <int CM>
-__device__ __forceinline__ void lo_load_any(int c, uint32_t (&w)[8], const uint32_t *p, int j, int d) {
+__device__ __forceinline__ void lo_read_any(int c, uint32_t (&w)[8], const uint32_t *p, int j, int d) {
     switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) { lo_load<1>(w, p, j, d); break; } [[fallthrough]];
-        case 2: if constexpr ((CM >> 2) & 1) { lo_load<2>(w, p, j, d); break; } [[fallthrough]];
-        case 3: if constexpr ((CM >> 3) & 1) { lo_load<3>(w, p, j, d); break; } [[fallthrough]];
+        case 1: if constexpr ((CM >> 1) & 1) { lo_read<1>(w, p, j, d); break; } [[fallthrough]];
+        case 2: if constexpr ((CM >> 2) & 1) { lo_read<2>(w, p, j, d); break; } [[fallthrough]];
+        case 3: if constexpr ((CM >> 3) & 1) { lo_read<3>(w, p, j, d); break; } [[fallthrough]];
         default:
 #pragma unroll
             for (int i = 0; i < 8; ++i) w[i] = 0u;
@@ -445,11 +445,11 @@ __device__ __forceinline__ void lo_stage64(uint32_t (&P)[32], s16x2 sg) {
     }
 }
 
-struct LoNext {
-    uint32_t w0[8], w1[8];   // half-slices 0 and 1
+struct LoNext {   // the next tile: class, flagged row and scale (its payload is in the wave's LDS copy)
     int c, ro;
     uint32_t s;
 };
+constexpr int kLoTileWords = 512;   // a tile of classes 0-3 (nw <= 8): at most 2 KB
 
 template <int DT, int CM>
 __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_dequant_lo(const DecodeArgs a) {
@@ -457,6 +457,7 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
     __shared__ uint2 tab4[512];
     __shared__ __align__(16) float icw[kLoWaves][256];
     __shared__ __align__(16) uint32_t stg[kLoWaves][32 * kLoBandWords];   // one 32-row x 128-byte band per wave
+    __shared__ __align__(16) uint32_t pay[kLoWaves][kLoTileWords];         // the next tile's payload, per wave
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, p = lane >> 5, p16 = 16 * p;
     const int d = p16;
@@ -468,32 +469,41 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
     first += w;
     if (first >= last) return;
     LoNext nx;
+    // The next tile's payload is copied into the wave's LDS buffer (direct-to-LDS loads, no registers held) and its
+    // scale and row into registers, all before this tile's output stores: stores count in vmcnt like loads, so data
+    // requested after them could only be waited for together with them.
     auto issue = [&](size_t q) {
         int g, b;
         tile_of(a, q, g, b);
         const uint32_t mt = a.M[(size_t)g * a.nb + b];
         nx.c = (int)(mt >> 29);
-        const uint32_t *base = a.D + (mt & 0x1FFFFFFFu);
-        const int nw = nw_of(nx.c);
-        lo_load_any<CM>(nx.c, nx.w0, base, j, d);
-        lo_load_any<CM>(nx.c, nx.w1, base + nw * 32, j, d);
+        const int chunks = 16 * nw_of(nx.c);   // 16-byte pieces of the tile (both half-slices)
+        if (chunks) {
+            const uint32_t *base = a.D + (mt & 0x1FFFFFFFu);
+#pragma unroll
+            for (int i = 0; i < kLoTileWords / 256; ++i)   // lanes past the tile repeat its last piece
+                __builtin_amdgcn_global_load_lds(base + 4 * min(64 * i + lane, chunks - 1), pay[w] + 256 * i, 16, 0, 0);
+        }
         nx.s = a.S[(size_t)b * a.rows + 32 * g + j];
         nx.ro = a.prmd[32 * g + j];
     };
-    // each tile's words are requested at the top of its iteration: at four waves per SIMD the other waves cover the
-    // latency (a prefetch one tile ahead, which costs registers, measured slower)
     int icb = -1;
+    issue(first);
     for (size_t q = first; q < last; q += kLoWaves) {
-        issue(q);
         const int c = nx.c, rof = nx.ro, ro = rof & 0x7FFF;
         const float S = half_to_float((uint16_t)nx.s);
+        uint32_t w0[8], w1[8];
+        lo_read_any<CM>(c, w0, pay[w], j, d);
+        lo_read_any<CM>(c, w1, pay[w] + nw_of(c) * 32, j, d);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read before the next tile's copy overwrites it
+        if (q + kLoWaves < last) issue(q + kLoWaves);
         // one half-slice at a time through its integer stages (only its 32 packed registers are being built)
         uint32_t P0[32], P1[32];
-        lo_decode_any<CM>(c, nx.w0, d, p16, tab4, P0);
+        lo_decode_any<CM>(c, w0, d, p16, tab4, P0);
         lo_stages(P0);
         lo_stage64(P0, sg);
         __asm__ volatile("" ::: "memory");
-        lo_decode_any<CM>(c, nx.w1, d, p16, tab4, P1);
+        lo_decode_any<CM>(c, w1, d, p16, tab4, P1);
         lo_stages(P1);
         lo_stage64(P1, sg);
         __asm__ volatile("" ::: "memory");
