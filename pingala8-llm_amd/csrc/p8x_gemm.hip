@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "p8x_internal.h"
+#include "p8x_act.h"
 #include "p8x_lane.h"
 
 namespace p8x {
@@ -34,11 +35,15 @@ constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles 
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the
-// lane, 4 .. 128 across lanes.
+// lane, 4 .. 128 across lanes (DPP row moves for distances 1-8, ds_bpermute for 16 and 32). One wave per block,
+// kMmActWaves blocks of one token per workgroup.
+constexpr int kMmActWaves = 4;
 template <typename XT>
-__global__ __launch_bounds__(64) void k_mm_act(const XT *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
-                                               _Float16 *__restrict__ xr) {
-    const int b = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kMmActWaves) void k_mm_act(const XT *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
+                                                             _Float16 *__restrict__ xr) {
+    const int lane = threadIdx.x & 63, b = kMmActWaves * (int)blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = blockIdx.y;
+    if (256 * b >= K) return;
     const XT *xp = x + (size_t)n * ldx + 256 * b + 4 * lane;
     const float4 cv = *reinterpret_cast<const float4 *>(ic + 256 * b + 4 * lane);
     float v[4];
@@ -52,15 +57,12 @@ __global__ __launch_bounds__(64) void k_mm_act(const XT *__restrict__ x, size_t 
     v[0] *= cv.x; v[1] *= cv.y; v[2] *= cv.z; v[3] *= cv.w;
     { const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3]; v[0] = a0 + b0; v[1] = a0 - b0; v[2] = a1 + b1; v[3] = a1 - b1; }
     { const float a0 = v[0], b0 = v[2], a1 = v[1], b1 = v[3]; v[0] = a0 + b0; v[2] = a0 - b0; v[1] = a1 + b1; v[3] = a1 - b1; }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool upper = (lane & m) != 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float p = __shfl_xor(v[e], m);
-            v[e] = upper ? p - v[e] : v[e] + p;
-        }
-    }
+    fwht_lane_stage<1>(v, lane);
+    fwht_lane_stage<2>(v, lane);
+    fwht_lane_stage<4>(v, lane);
+    fwht_lane_stage<8>(v, lane);
+    fwht_lane_stage<16>(v, lane);
+    fwht_lane_stage<32>(v, lane);
     half2v lo, hi;
     lo.x = (_Float16)(v[0] * 0.0625f); lo.y = (_Float16)(v[1] * 0.0625f);
     hi.x = (_Float16)(v[2] * 0.0625f); hi.y = (_Float16)(v[3] * 0.0625f);
@@ -474,8 +476,9 @@ static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, in
     const MmPlan p = mm_plan(t, N);
     const bool direct = p.nsplit == 1 && t->prm_identity;
     int rc;
-    if (x_dtype == P8X_F32) hipLaunchKernelGGL(k_mm_act<float>, dim3(t->nb, N), dim3(64), 0, st, (const float *)x, ldx, t->ic, t->K, xr);
-    else hipLaunchKernelGGL(k_mm_act<uint16_t>, dim3(t->nb, N), dim3(64), 0, st, (const uint16_t *)x, ldx, t->ic, t->K, xr);
+    const dim3 agrid((t->nb + kMmActWaves - 1) / kMmActWaves, N);
+    if (x_dtype == P8X_F32) hipLaunchKernelGGL(k_mm_act<float>, agrid, dim3(64 * kMmActWaves), 0, st, (const float *)x, ldx, t->ic, t->K, xr);
+    else hipLaunchKernelGGL(k_mm_act<uint16_t>, agrid, dim3(64 * kMmActWaves), 0, st, (const uint16_t *)x, ldx, t->ic, t->K, xr);
     if ((rc = hip_check(hipGetLastError(), "k_mm_act launch"))) return rc;
     MmJob J;
     J.M = t->M; J.S = t->S; J.D = t->D; J.xr = xr;
