@@ -122,3 +122,22 @@ def test_quantizer_outliers_get_clamp_delta():
     Wd = orc.dequant()
     wmax = np.float32(np.float16(np.abs(W).max() * np.float32(1.001)))
     assert np.abs(Wd).max() <= wmax * (1 + 1e-6)
+
+
+def test_product_library_has_no_timeline_instrumentation():
+    """the launch-timeline stamps live only in the separate analysis build (make timeline)"""
+    L = p8x.lib()
+    assert not hasattr(L, "p8x_timeline_read")
+    path = os.path.join(os.path.dirname(p8x.LIB_PATH), "libp8x_timeline.so")
+    if os.path.exists(path):
+        import ctypes
+        T = ctypes.CDLL(path)
+        assert hasattr(T, "p8x_timeline_read") and hasattr(T, "p8x_timeline_reset")
+
+
+def test_timeline_module_parses_arguments():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, "-m", "p8x.timeline", "--help"], cwd=os.path.join(ROOT, "pingala8-llm_amd"),
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "--layers" in r.stdout
