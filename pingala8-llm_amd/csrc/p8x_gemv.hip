@@ -419,6 +419,9 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
 int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, const char *what) {
     for (int i = 0; i < n; ++i) {
         if (!ts[i]) return set_error(P8X_ERR_ARG, "%s: tensor %d is null", what, i);
+        // one tensor twice would share its workspace (K-chunk partial rows, meeting slots) between two jobs
+        for (int k = 0; k < i; ++k)
+            if (ts[k] == ts[i]) return set_error(P8X_ERR_ARG, "%s: tensor %d is listed twice", what, k);
         if (ts[i]->K != ts[0]->K) return set_error(P8X_ERR_ARG, "%s: tensor %d has K %d, tensor 0 has %d", what, i, ts[i]->K, ts[0]->K);
         if (memcmp(ts[i]->a2_host, ts[0]->a2_host, sizeof ts[0]->a2_host))
             return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d has a different codebook", what, i);

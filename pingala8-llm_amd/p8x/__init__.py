@@ -6,6 +6,7 @@ built (`make -C pingala8-llm_amd/csrc`); loading fails loudly when it is missing
 import ctypes
 import ctypes.util
 import os
+import sys
 
 import numpy as np
 
@@ -35,6 +36,12 @@ EXPORTS = [
 
 class P8xError(RuntimeError):
     pass
+
+
+def _finalizing():
+    """True while the interpreter shuts down: objects collected then are not released through HIP (the runtime, or a
+    profiler's tool attached to it, may already be gone); owners release them explicitly before that."""
+    return sys.is_finalizing()
 
 
 class Info(ctypes.Structure):
@@ -237,6 +244,8 @@ class DeviceBuffer:
             self.ptr = ctypes.c_void_p()
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.free()
         except Exception:
@@ -280,6 +289,14 @@ class Graph:
         if self.g:
             hip().hipGraphDestroy(self.g)
             self.g = ctypes.c_void_p()
+
+    def __del__(self):
+        if _finalizing():
+            return
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 class Event:
@@ -464,6 +481,8 @@ class VrFile:
             self.h = ctypes.c_void_p()
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -520,6 +539,8 @@ class Tensor:
             self.h = ctypes.c_void_p()
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.release()
         except Exception:
@@ -702,9 +723,11 @@ def mul_mat_vec_glu(gate, up, x):
 
 class Step:
     """A chain of linears in one launch (p8x_step_*). stages: list of (tensors, x, ys) or (tensors, x, None, glu_out)
-    with device buffers; stage s may read an earlier stage's output."""
+    with device buffers; stage s may read an earlier stage's output. The step keeps the tensors and buffers alive
+    until release() (the library holds their addresses)."""
 
     def __init__(self, stages):
+        self._keep = [list(st) for st in stages]
         arr = (StepStageC * len(stages))()
         for k, st in enumerate(stages):
             tensors, x, ys = st[0], st[1], st[2]
@@ -727,16 +750,22 @@ class Step:
         check(lib().p8x_step_check(self.h), "p8x_step_check")
 
     def info(self):
+        """grid, stages, the class set of the chain and the kernel that runs it ("chain": the dataflow kernel for
+        class-3 chains, "barrier": the grid-barrier kernel)"""
         g, n, cm = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         check(lib().p8x_step_info(self.h, ctypes.byref(g), ctypes.byref(n), ctypes.byref(cm)), "p8x_step_info")
-        return {"grid": g.value, "stages": n.value, "class_set": cm.value}
+        return {"grid": g.value, "stages": n.value, "class_set": cm.value & 0xFF,
+                "kernel": "chain" if cm.value & 0x100 else "barrier"}
 
     def release(self):
         if self.h:
             lib().p8x_step_release(self.h)
             self.h = ctypes.c_void_p()
+        self._keep = None
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.release()
         except Exception:
@@ -781,6 +810,8 @@ class GemvBatch:
             self.h = ctypes.c_void_p()
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.release()
         except Exception:

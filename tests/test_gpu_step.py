@@ -1,10 +1,15 @@
 """The decode-step object (p8x_step_*): a chain of linears in one cooperative launch, each stage reading an earlier
-stage's output, against the same chain run as one launch per node (p8x_mul_mat_vec_multi / p8x_mul_mat_vec /
-p8x_mul_mat_vec_glu), which the parity tests pin to the oracle. Bar: every stage's output bit-identical to the
-per-node chain, on consecutive runs; one stage also against the fp64 oracle.
+stage's output.
 
-Shapes reach every stage variant: q/k/v as one multi-linear stage, gate/up with teams of waves (more row groups than
-CUs), down with two K-chunks (K = 8192, the split-K fix-up), two head shards."""
+Class-3 chains run the dataflow kernel (k_chain): every stage's output is checked against the fp64 oracle on that
+stage's actual input (the buffer the step wrote for it; 1e-5 relative L2, as the single-call GEMV tests), including
+swiglu outputs and K-split outputs that the consumers of the next stage combine and write; consecutive runs and HIP
+graph replays are bitwise identical (the run counter lives on the device). Other class sets run the grid-barrier
+kernel (k_step): every stage's output bit-identical to the per-node chain (p8x_mul_mat_vec_multi / p8x_mul_mat_vec /
+p8x_mul_mat_vec_glu), which the parity tests pin to the oracle, on consecutive runs and graph replays.
+
+Shapes reach every stage variant: q/k/v as one multi-linear stage, gate/up with several row groups per workgroup,
+down with two K-chunks (K = 8192), two head shards."""
 import numpy as np
 import pytest
 
@@ -17,6 +22,7 @@ HIDDEN, KV, FFN = 1024, 256, 8192
 HEAD = (16384, 16384)
 C3 = [0, 0, 0, 1, 0, 0, 0, 0]
 MIXED = [0.05, 0.1, 0.1, 0.35, 0.1, 0.1, 0.15, 0.05]
+SHAPES = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN), (HIDDEN, FFN)]
 
 
 def group(seed, shapes, class_p):
@@ -27,21 +33,20 @@ def group(seed, shapes, class_p):
 
 
 def build(class_p, layers=2, seed=100):
-    L, host = [], {}
-    for l in range(layers):
-        qkv = group(seed, [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN)], class_p)
-        o = group(seed + 10, [(HIDDEN, HIDDEN)], class_p)
-        gu = group(seed + 20, [(FFN, HIDDEN), (FFN, HIDDEN)], class_p)
-        d = group(seed + 30, [(HIDDEN, FFN)], class_p)
+    """device tensors per layer, head shards, and the host slots of every tensor (same order)"""
+    L, hosts = [], []
+    for _ in range(layers):
+        qkv = group(seed, SHAPES[0:3], class_p)
+        o = group(seed + 10, SHAPES[3:4], class_p)
+        gu = group(seed + 20, SHAPES[4:6], class_p)
+        d = group(seed + 30, SHAPES[6:7], class_p)
         seed += 100
-        shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN), (HIDDEN, FFN)]
         slots = qkv + o + gu + d
-        L.append([p8x.Tensor(s, r, K) for s, (r, K) in zip(slots, shapes)])
-        if l == 0:
-            host["o"] = (slots[3], HIDDEN, HIDDEN)
+        L.append([p8x.Tensor(s, r, K) for s, (r, K) in zip(slots, SHAPES)])
+        hosts.append(list(zip(slots, SHAPES)))
     hs = group(seed, [(r, HIDDEN) for r in HEAD], class_p)
     head = [p8x.Tensor(s, r, HIDDEN) for s, r in zip(hs, HEAD)]
-    return L, head, host
+    return L, head, hosts, [(s, (r, HIDDEN)) for s, r in zip(hs, HEAD)]
 
 
 def chain(L, head, x0):
@@ -76,11 +81,34 @@ def read(outs):
     return [b.to_numpy(np.float32, (n,)).copy() for b, n in outs]
 
 
+def rel(a, ref):
+    return float(np.linalg.norm(a.astype(np.float64) - ref) / np.linalg.norm(ref))
+
+
+def check_against_oracle(got, x0, hosts, head_hosts):
+    """every stage's output vs the fp64 oracle on that stage's input as the step wrote it"""
+    orc = [[O.Oracle(s, r, K) for s, (r, K) in layer] for layer in hosts]
+    orh = [O.Oracle(s, r, K) for s, (r, K) in head_hosts]
+    cur = x0
+    for l, layer in enumerate(orc):
+        yq, yk, yv, yo, yg, yd = got[6 * l:6 * l + 6]
+        for y, o, name in ((yq, layer[0], "q"), (yk, layer[1], "k"), (yv, layer[2], "v")):
+            assert rel(y, o.gemv_f64(cur)) < 1e-5, (l, name)
+        assert rel(yo, layer[3].gemv_f64(yq)) < 1e-5, (l, "o")
+        g, u = layer[4].gemv_f64(yo), layer[5].gemv_f64(yo)
+        assert rel(yg, g / (1.0 + np.exp(-g)) * u) < 1e-5, (l, "swiglu")
+        assert rel(yd, layer[6].gemv_f64(yg)) < 1e-5, (l, "down")
+        cur = yd
+    for i, o in enumerate(orh):
+        assert rel(got[6 * len(orc) + i], o.gemv_f64(cur)) < 1e-5, ("head", i)
+
+
 @pytest.mark.parametrize("mix", ["c3", "mixed"])
-def test_step_equals_per_node_chain(mix):
-    L, head, host = build(C3 if mix == "c3" else MIXED)
+def test_step_chain(mix):
+    L, head, hosts, head_hosts = build(C3 if mix == "c3" else MIXED)
     rng = np.random.default_rng(1)
-    x0 = p8x.DeviceBuffer.from_numpy(rng.standard_normal(HIDDEN).astype(np.float32))
+    x0h = rng.standard_normal(HIDDEN).astype(np.float32)
+    x0 = p8x.DeviceBuffer.from_numpy(x0h)
     stages, outs = chain(L, head, x0)
     run_per_node(stages)
     want = read(outs)
@@ -89,28 +117,68 @@ def test_step_equals_per_node_chain(mix):
     info = step.info()
     assert info["stages"] == len(stages) and info["grid"] >= 1
     assert info["class_set"] == (8 if mix == "c3" else 0xFE)
+    assert info["kernel"] == ("chain" if mix == "c3" else "barrier")
+    first = None
     for rep in range(3):
         for b, _ in outs:   # poison the outputs (NaN bytes): the step must write every value
             b.fill(0xFF)
         step.run()
         step.check()
         got = read(outs)
-        for i, (g, w) in enumerate(zip(got, want)):
-            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), (mix, rep, i)
-    # the first o stage against the fp64 oracle on its own input (the q output)
-    slot, rows, K = host["o"]
-    orc = O.Oracle(slot, rows, K)
-    yo = got[3]
-    ref = orc.gemv_f64(got[0])
-    assert np.linalg.norm(yo - ref) / np.linalg.norm(ref) < 1e-3
+        if first is None:
+            first = got
+        for i, (g, f) in enumerate(zip(got, first)):
+            assert np.array_equal(g.view(np.uint32), f.view(np.uint32)), (mix, rep, i)   # deterministic
+    if mix == "c3":
+        check_against_oracle(first, x0h, hosts, head_hosts)
+        # on the same input (the first stage) the per-node calls agree; later stages see inputs that differ in the
+        # last bits (products summed in another order), which the 8-bit activation rounding can amplify
+        for g, w in zip(first[:3], want[:3]):
+            assert rel(g, w.astype(np.float64)) < 1e-5
+    else:
+        for i, (g, w) in enumerate(zip(first, want)):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), (mix, i)
+    # replays of one HIP graph capture, with eager runs and synchronizations between them
+    st = p8x.Stream()
+    graph = p8x.Graph(lambda s: step.run(s), st)
+    for rep in range(3):
+        for b, _ in outs:
+            b.fill(0xFF)
+        graph.launch(st)
+        st.sync()
+        step.check()
+        got = read(outs)
+        for i, (g, f) in enumerate(zip(got, first)):
+            assert np.array_equal(g.view(np.uint32), f.view(np.uint32)), (mix, "replay", rep, i)
+        step.run(st)
+        st.sync()
+    graph.release()
     step.release()
 
 
 def test_step_rejects_mismatched_stage():
-    L, head, _ = build(C3, layers=1)
+    L, head, _, _ = build(C3, layers=1)
     x0 = p8x.DeviceBuffer(4 * HIDDEN)
     q, k, v, o, gate, up, down = L[0]
     with pytest.raises(p8x.P8xError, match="K"):
         p8x.Step([([q, down], x0, [p8x.DeviceBuffer(4 * HIDDEN), p8x.DeviceBuffer(4 * HIDDEN)])])
     with pytest.raises(p8x.P8xError, match="swiglu"):
         p8x.Step([([gate], x0, None, p8x.DeviceBuffer(4 * FFN))])
+    with pytest.raises(p8x.P8xError, match="twice"):
+        p8x.Step([([gate, gate], x0, None, p8x.DeviceBuffer(4 * FFN))])
+
+
+def test_step_falls_back_for_aliased_outputs():
+    """A chain whose stage reads an output that a later stage also writes keeps the barrier kernel's ordering."""
+    L, head, _, _ = build(C3, layers=1)
+    q, k, v, o, gate, up, down = L[0]
+    rng = np.random.default_rng(2)
+    x0 = p8x.DeviceBuffer.from_numpy(rng.standard_normal(HIDDEN).astype(np.float32))
+    yo, yq = p8x.DeviceBuffer(4 * HIDDEN), p8x.DeviceBuffer(4 * HIDDEN)
+    # stage 0 reads x0, stage 1 reads q's output and writes x0 again
+    stages = [([q], x0, [yq]), ([o], yq, [x0])]
+    step = p8x.Step(stages)
+    assert step.info()["kernel"] == "barrier"
+    step.run()
+    step.check()
+    step.release()
