@@ -356,14 +356,14 @@ def measure_dependent_step(tensors, kinds, stream, steps, graph_replay=True):
     launches = 4 * nl + 1
     gtxt = f"graph {g_ms * 1e3:.0f} us" if g_ms is not None else "graph not replayed"
     log(f"dependent step: eager {eager_ms * 1e3:.0f} us, {gtxt} ({launches} launches), "
-        f"one launch {s_ms * 1e3:.0f} us ({sinfo['kernel']} kernel, {sinfo['grid']} workgroups, {sinfo['stages']} stages)")
+        f"one launch {s_ms * 1e3:.0f} us ({sinfo['grid']} workgroups, {sinfo['stages']} stages)")
     for b in bufs:
         b.free()
     return {"workload": f"{nl} layers: q/k/v in one launch -> o -> silu(gate) * up in one launch -> down, then the head "
                         "shards in one launch; each launch reads its producer's output", "launches": launches,
             "step_kernel": {"ms_per_step": round(s_ms, 4), "GB/s": round(step_bytes / (s_ms * 1e-3) / 1e9, 1),
                             "frac_of_peak": round(step_bytes / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                            "stages": sinfo["stages"], "workgroups": sinfo["grid"], "kernel": sinfo["kernel"]},
+                            "stages": sinfo["stages"], "workgroups": sinfo["grid"]},
             "graph_replay": {"ms_per_step": round(g_ms, 4), "GB/s": round(step_bytes / (g_ms * 1e-3) / 1e9, 1)} if g_ms else None,
             "eager": {"ms_per_step": round(eager_ms, 4), "GB/s": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)}}
 

@@ -24,8 +24,12 @@ struct BlockLane {
 
 // The 32-bit value held by lane (lane ^ M). M = 1, 2, 4, 8 stay inside 16-lane rows and use DPP row moves (VALU,
 // no LDS traffic): quad_perm [1,0,3,2] and [2,3,0,1], row_ror:8, and for M = 4 row_ror:12 (lane i reads lane
-// (i + 4) mod 16, the partner of lanes with bit 2 clear) or row_ror:4 (lane i - 4, for bit 2 set). Larger M:
-// ds_bpermute. Only the data movement differs from __shfl_xor; the arithmetic on the values is unchanged.
+// (i + 4) mod 16, the partner of lanes with bit 2 clear) or row_ror:4 (lane i - 4, for bit 2 set). M = 16 and 32
+// use gfx950's lane swaps on two copies of the value (VALU): v_permlane16_swap exchanges the odd 16-lane rows of its
+// first operand with the even rows of its second, so the copy that received row r ^ 1 is the second for even rows
+// and the first for odd rows; v_permlane32_swap exchanges the upper 32 lanes of the first with the lower 32 of the
+// second, so lanes 0..31 take the second copy and lanes 32..63 the first. Only the data movement differs from
+// __shfl_xor; the arithmetic on the values is unchanged.
 template <int M, typename T>
 __device__ __forceinline__ T lane_xor(T v, int lane) {
     static_assert(sizeof(T) == 4, "32-bit values");
@@ -38,7 +42,13 @@ __device__ __forceinline__ T lane_xor(T v, int lane) {
         const int down = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false);
         r = (lane & 4) ? down : up;
     } else if constexpr (M == 8) r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false);
-    else r = __shfl_xor(iv, M);
+    else if constexpr (M == 16) {
+        const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)iv, (unsigned)iv, false, false);
+        r = (int)((lane & 16) ? sw[0] : sw[1]);
+    } else if constexpr (M == 32) {
+        const auto sw = __builtin_amdgcn_permlane32_swap((unsigned)iv, (unsigned)iv, false, false);
+        r = (int)((lane & 32) ? sw[0] : sw[1]);
+    } else r = __shfl_xor(iv, M);
     return __builtin_bit_cast(T, r);
 }
 

@@ -750,12 +750,10 @@ class Step:
         check(lib().p8x_step_check(self.h), "p8x_step_check")
 
     def info(self):
-        """grid, stages, the class set of the chain and the kernel that runs it ("chain": the dataflow kernel for
-        class-3 chains, "barrier": the grid-barrier kernel)"""
+        """grid (workgroups of the launch), stages, and the class set of the chain's tensors"""
         g, n, cm = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         check(lib().p8x_step_info(self.h, ctypes.byref(g), ctypes.byref(n), ctypes.byref(cm)), "p8x_step_info")
-        return {"grid": g.value, "stages": n.value, "class_set": cm.value & 0xFF,
-                "kernel": "chain" if cm.value & 0x100 else "barrier"}
+        return {"grid": g.value, "stages": n.value, "class_set": cm.value}
 
     def release(self):
         if self.h:

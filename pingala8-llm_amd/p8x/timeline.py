@@ -15,12 +15,14 @@ to this launch's first workgroup start.
 
     python -m p8x.timeline --step [--layers 32]
 
-runs the same chain as one step object (the dataflow kernel for these class-3 tensors) and prints, per kind of stage,
-where a stage's time goes: sync wave 0 of every workgroup records s_memrealtime at the start of its input phase, when
-its input blocks are polled and quantized into LDS, after the workgroup barrier that starts the compute phase, after
-the one that ends it, and after its epilogue (partial rows summed, outputs published); compute wave 0 records when its
-tiles of the stage are done. Per stage: the median / maximum over the workgroups with work of each phase, and the
-stage's span (last epilogue end of the previous stage to last epilogue end of this one).
+runs the same chain as one step object (k_step: one cooperative launch, a grid barrier between stages) and prints,
+per kind of stage, where a stage's time goes: thread 0 of every workgroup records s_memrealtime at its stage start,
+when its first virtual workgroup's input is in LDS, at the end of its virtual workgroups, when its stores are
+complete, after its arrival and when it sees the release; within the first virtual workgroup also when its
+activation loads are in (the timeline build waits for them there), when its tile prefetch is issued, when its
+quantization is done, and, for its first round of row groups, when its tiles are done, the partial rows exchanged
+and the epilogue done. Per stage: the median / maximum over workgroups of each phase, and the stage's span (the
+previous stage's last release to this stage's last release).
 """
 import argparse
 import ctypes
@@ -34,7 +36,59 @@ import p8x
 STAMPS = ["start", "args in", "loads in", "table+quant", "barrier", "tiles", "end"]
 
 
-STEP_PHASES = ["input", "to compute", "compute", "to epilogue", "epilogue"]
+BARRIER_PHASES = ["input", "tiles + epilogue", "stores done", "arrival", "release wait", "to next stage"]
+
+
+def barrier_timeline(rec, info, nl):
+    """per-stage phases of the grid-barrier step kernel: thread 0 of every workgroup records its stage start, its first
+    virtual workgroup's input in LDS, the end of its virtual workgroups, its stores complete, its arrival done and the
+    release seen"""
+    nst, G = info["stages"], info["grid"]
+    names = ["q/k/v", "o", "gate/up+swiglu", "down"]
+    rows = {}
+    prev_end = None
+    for s in range(nst - 1):   # the last stage has no barrier after it
+        r, nxt = rec[s], rec[s + 1]
+        act = (r[:, 6] & 0xFFFF) > 0
+        kind = names[s % 4] if s < 4 * nl else "head"
+        ph = [r[act, 1] - r[act, 0], r[act, 2] - r[act, 1], r[:, 3] - r[:, 2], r[:, 4] - r[:, 3], r[:, 5] - r[:, 4], nxt[:, 0] - r[:, 5]]
+        end = r[:, 5].max()
+        span = (end - prev_end) if prev_end is not None else np.nan
+        prev_end = end
+        rows.setdefault(kind, []).append([np.median(x) / 100.0 for x in ph] + [x.max() / 100.0 for x in ph] + [span / 100.0, act.sum()])
+    total = (rec[nst - 1, :, 0].max() - rec[0, :, 0].min()) / 100.0
+    nph = len(BARRIER_PHASES)
+    print(f"step kernel (barrier): {nst} stages, {G} workgroups, {total:.1f} us from the first workgroup's start to the last "
+          "stage's start; us per phase")
+    print("| stage | workgroups with work | " + " | ".join(BARRIER_PHASES) + " | stage span |")
+    print("|---|---|" + "---|" * (nph + 1))
+    for kind, v in rows.items():
+        m = np.nanmean(np.array(v, np.float64), axis=0)
+        cells = [f"{m[j]:.2f} / {m[nph + j]:.2f}" for j in range(nph)]
+        print(f"| {kind} | {int(m[2 * nph + 1])} | " + " | ".join(cells) + f" | {m[2 * nph]:.2f} |")
+    print("(each phase cell: median / maximum over the workgroups (input, tiles: those with work), averaged over the stages "
+          "of that kind; stage span: from the previous stage's last release to this stage's last release)")
+    # inside the first virtual workgroup: 16-bit tick counts packed into rec[6] (from the stage start) and rec[7]
+    # (quantization from the stage start, the rest from the input in LDS)
+    sub = {}
+    for s in range(nst - 1):
+        r = rec[s]
+        act = (r[:, 6] & 0xFFFF) > 0
+        f6, f7 = r[act, 6], r[act, 7]
+        field = lambda v, sh: ((v >> sh) & 0xFFFF) / 100.0
+        inp = (r[act, 1] - r[act, 0]) / 100.0
+        vals = [field(f6, 16), field(f6, 32), field(f7, 0), inp, inp + field(f7, 16), inp + field(f7, 32), inp + field(f7, 48)]
+        kind = names[s % 4] if s < 4 * nl else "head"
+        sub.setdefault(kind, []).append([np.median(v) for v in vals])
+    print()
+    print("| stage | activations in | tile prefetch issued | quantized | input in LDS (all waves) | tiles done | "
+          "partials exchanged | epilogue done |")
+    print("|---|---|---|---|---|---|---|---|")
+    for kind, v in sub.items():
+        m = np.mean(np.array(v, np.float64), axis=0)
+        print(f"| {kind} | " + " | ".join(f"{x:.2f}" for x in m) + " |")
+    print("(us from the stage start, thread 0 of the first virtual workgroup, median over workgroups with work; the "
+          "timeline build waits for the activation loads where it records them)")
 
 
 def step_timeline(args, L):
@@ -70,31 +124,7 @@ def step_timeline(args, L):
     step.release()
     if args.dump:
         np.save(args.dump, buf)
-    rec = buf.astype(np.int64)
-    t0 = rec[:, :, 0].min()
-    names = ["q/k/v", "o", "gate/up+swiglu", "down"]
-    rows = {}
-    prev_end = rec[0, :, 0].min()
-    for s in range(nst):
-        r = rec[s]
-        act = r[:, 6] > 0
-        kind = names[s % 4] if s < 4 * nl else "head"
-        ph = [r[act, 1] - r[act, 0], r[act, 2] - r[act, 1], r[act, 5] - r[act, 2], r[act, 3] - r[act, 5], r[act, 4] - r[act, 3]]
-        end = r[act, 4].max()
-        span = end - prev_end
-        prev_end = end
-        rows.setdefault(kind, []).append([np.median(x) / 100.0 for x in ph] + [x.max() / 100.0 for x in ph] + [span / 100.0, act.sum()])
-    total = (rec[:, :, 4].max() - t0) / 100.0
-    print(f"step kernel ({info['kernel']}): {nst} stages, {G} workgroups, {total:.1f} us from the first workgroup's start "
-          "to the last epilogue end; us per phase")
-    print("| stage | workgroups with work | " + " | ".join(STEP_PHASES) + " | stage span |")
-    print("|---|---|" + "---|" * 6)
-    for kind, v in rows.items():
-        m = np.mean(np.array(v, np.float64), axis=0)
-        cells = [f"{m[j]:.2f} / {m[5 + j]:.2f}" for j in range(5)]
-        print(f"| {kind} | {int(m[11])} | " + " | ".join(cells) + f" | {m[10]:.2f} |")
-    print("(each phase cell: median / maximum over the workgroups with work, averaged over the stages of that kind; "
-          "stage span: from the previous stage's last epilogue end to this stage's last epilogue end)")
+    barrier_timeline(buf.astype(np.int64), info, nl)
 
 
 def main():
