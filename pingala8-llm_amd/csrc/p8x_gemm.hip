@@ -17,9 +17,9 @@
 // Q8_0 slab (k_r51_k1, CPU.patch:2138-2235) and calls the stock integer MMQ.
 #include <hip/hip_runtime.h>
 
-#include <mutex>
-
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "p8x_internal.h"
 #include "p8x_act.h"
@@ -471,6 +471,25 @@ static void mm_workspace(const p8x_tensor *t, int N, size_t *x_bytes, size_t *pl
 
 // the launches of one prompt GEMM with its workspace given: xr >= N K fp16, wmm >= the plane bytes (unused when the
 // output is written directly)
+
+// k_mm_finish keeps a row of the output (up to 128 KB) in dynamic LDS. The attribute that allows it is per device:
+// set once on each device this process launches on (callers on several threads serialize here).
+static int finish_lds_attribute() {
+    int dev = 0;
+    int rc = hip_check(hipGetDevice(&dev), "k_mm_finish attribute: hipGetDevice");
+    if (rc) return rc;
+    static std::mutex mu;
+    static std::vector<char> done;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev >= done.size()) done.resize((size_t)dev + 1, 0);
+    if (done[dev]) return P8X_OK;
+    if ((rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<float>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")) ||
+        (rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")))
+        return rc;
+    done[dev] = 1;
+    return P8X_OK;
+}
+
 static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, _Float16 *xr,
                              float *wmm, hipStream_t st) {
     const MmPlan p = mm_plan(t, N);
@@ -491,13 +510,7 @@ static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, in
     if ((rc = hip_check(hipGetLastError(), "k_mm launch"))) return rc;
     if (!direct) {
         const size_t lds = 4 * (size_t)t->rows;   // rows < 32768: at most 128 KB
-        static bool attr_set = false;
-        if (!attr_set) {
-            if ((rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<float>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")) ||
-                (rc = hip_check(hipFuncSetAttribute((const void *)k_mm_finish<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072), "k_mm_finish attribute")))
-                return rc;
-            attr_set = true;
-        }
+        if ((rc = finish_lds_attribute())) return rc;
         if (x_dtype == P8X_F32)
             hipLaunchKernelGGL(k_mm_finish<float>, dim3(N), dim3(1024), lds, st, (const float *)wmm, p.nsplit, N, t->rows, t->pinv, t->cp, t->cc, t->cv,
                                (const float *)x, ldx, y, ldy);

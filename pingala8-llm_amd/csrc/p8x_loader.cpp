@@ -294,17 +294,17 @@ int p8x_vr_open(const char *const *paths, int npaths, p8x_vr_file **out) {
     int rc;
     for (int i = 0; i < npaths; ++i)
         if (!paths[i] || (rc = parse_gguf(F, i, paths[i], i == 0))) return bail(rc ? rc : set_error(P8X_ERR_ARG, "p8x_vr_open: null path"));
-    if (!F->kv.count("vr.format")) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: no vr.format key: not a native VR file"));
+    if (!F->kv.count("vr.format")) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: the file has no vr.format entry, so it is not a Pingala-8 model"));
     const GgufValue *ns = kv_u32(F, "vr.ns");
-    if (!ns) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: KV vr.ns (uint32) is missing; this format needs NS 108"));
-    if (ns->u != kNS) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: vr.ns = %llu, the kernels support only %u", (unsigned long long)ns->u, kNS));
+    if (!ns) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: the uint32 entry vr.ns is absent (this library reads files with 108 trellis states)"));
+    if (ns->u != kNS) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: the file declares %llu trellis states; this library decodes %u only", (unsigned long long)ns->u, kNS));
     const GgufValue *trl = kv_u32(F, "vr.trl"), *nlin = kv_u32(F, "vr.n_linear");
-    if (!trl || trl->u != kTRL || !nlin) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: KV vr.trl must be 2 and vr.n_linear must be present"));
+    if (!trl || trl->u != kTRL || !nlin) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: expected entries vr.trl == 2 and vr.n_linear"));
     {
         const auto it = F->kv.find("vr.layout");
-        if (it != F->kv.end() && it->second.type != kGgufU32) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: KV vr.layout must be uint32"));
+        if (it != F->kv.end() && it->second.type != kGgufU32) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: the entry vr.layout has a type other than uint32"));
         F->layout = it == F->kv.end() ? 2 : (int)it->second.u;
-        if (F->layout != 2 && F->layout != 3) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: vr.layout = %d (supported: 2, 3)", F->layout));
+        if (F->layout != 2 && F->layout != 3) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: unknown side-data layout %d (this library reads 2 and 3)", F->layout));
     }
     long long n_layer = -1;
     {
@@ -324,11 +324,11 @@ int p8x_vr_open(const char *const *paths, int npaths, p8x_vr_file **out) {
         p8x_vr_entry e;
         e.name = base + ".weight";
         const GgufTensor *w = find(e.name);
-        if (!w) return bail(fail("p8x_vr_open: '%s' has vr_c but no weight", base));
-        if (w->type != kGgmlI8 || w->ne.size() != 1) return bail(fail("p8x_vr_open: '%s' must be I8 1-D", e.name));
+        if (!w) return bail(fail("p8x_vr_open: '%s': a vr_c tensor without its weight tensor", base));
+        if (w->type != kGgmlI8 || w->ne.size() != 1) return bail(fail("p8x_vr_open: '%s': the weight bytes must be a one-dimensional I8 tensor", e.name));
         e.w = *w;
         e.c = it.second;
-        if (e.c.type != kGgmlF16) return bail(fail("p8x_vr_open: '%s' vr_c F16 expected", base));
+        if (e.c.type != kGgmlF16) return bail(fail("p8x_vr_open: '%s': vr_c is not F16", base));
         p8x_vr_desc &d = e.d;
         memset(&d, 0, sizeof d);
         d.layout = F->layout;
@@ -336,26 +336,26 @@ int p8x_vr_open(const char *const *paths, int npaths, p8x_vr_file **out) {
         d.fbytes = (size_t)w->ne[0];
         if (F->layout == 2) {
             const GgufTensor *p = find(base + ".vr_prm");
-            if (!p || p->type != kGgmlI16) return bail(fail("p8x_vr_open: '%s' vr_c F16 / vr_prm I16 expected", base));
+            if (!p || p->type != kGgmlI16) return bail(fail("p8x_vr_open: '%s': vr_c must be F16 and vr_prm I16", base));
             e.prm = *p;
             e.has_prm = true;
             d.rows = (int)std::min<uint64_t>(p->ne[0], 1u << 30);
             d.kbytes = d.fbytes;
         } else {   // VR3: rows from the file size, K and header word 515; identity permutation, no vr_prm tensor
-            if (find(base + ".vr_prm")) return bail(fail("p8x_vr_open: '%s' has vr_prm in a vr.layout 3 file", base));
+            if (find(base + ".vr_prm")) return bail(fail("p8x_vr_open: '%s': layout 3 keeps the row order inside the weight, yet a vr_prm tensor is present", base));
             uint32_t w515 = 0;
             if (d.fbytes >= kHeaderBytes && (rc = read_at(F, e.w, 2060, &w515, 4))) return bail(rc);
             d.rows = (int)p8x_vr3_rows(d.fbytes, (size_t)d.K, w515, &d.kbytes);
             if (d.rows == 0)
-                return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s' is not a valid VR3 tensor (%zu B, K %d, word 515 0x%08x)", e.name.c_str(), d.fbytes, d.K, w515));
+                return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s': not a layout-3 weight (%zu bytes, K %d, header word 515 = 0x%08x)", e.name.c_str(), d.fbytes, d.K, w515));
         }
         if (d.K % 256 || d.K <= 0 || d.rows % 32 || d.rows <= 0 || d.rows >= 32768)
-            return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s' bad shape K %d rows %d", base.c_str(), d.K, d.rows));
+            return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s': shape K %d x rows %d is outside the format (K %% 256, rows %% 32, rows < 32768)", base.c_str(), d.K, d.rows));
         const GgufTensor *di = find(base + ".vr_didx"), *dv = find(base + ".vr_dval");
-        if (!di != !dv) return bail(fail("p8x_vr_open: '%s' needs both vr_didx and vr_dval", base));
+        if (!di != !dv) return bail(fail("p8x_vr_open: '%s': clamp-delta tensors come in pairs (vr_didx with vr_dval)", base));
         if (di) {
             if (di->type != kGgmlI16 || dv->type != kGgmlF32 || di->ne.size() < 2 || di->ne[0] != dv->ne[0] || di->ne[1] != 2)
-                return bail(fail("p8x_vr_open: '%s' vr_didx I16 [nd,2] / vr_dval F32 [nd] expected", base));
+                return bail(fail("p8x_vr_open: '%s': clamp-delta tensors must be vr_didx I16 [n][2] and vr_dval F32 [n]", base));
             if (dv->ne[0] >= (1u << 30)) return bail(fail("p8x_vr_open: '%s' too many delta entries", base));
             e.didx = *di;
             e.dval = *dv;
@@ -369,14 +369,14 @@ int p8x_vr_open(const char *const *paths, int npaths, p8x_vr_file **out) {
                 d.slot_bytes = (size_t)(d.K / 256) * st.block_bytes * d.rows;
                 break;
             }
-        if (!d.slot_bytes) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s' needs %zu B, no slot type fits", e.name.c_str(), need));
+        if (!d.slot_bytes) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: '%s': %zu bytes exceed every slot size", e.name.c_str(), need));
         F->vr.push_back(std::move(e));
     }
     const GgufTensor *sg = find("vr.had_signs");
-    if (!sg || sg->type != kGgmlI8 || sg->ne[0] != 256) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: vr.had_signs must be I8 [256]"));
+    if (!sg || sg->type != kGgmlI8 || sg->ne[0] != 256) return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: the rotation signs (vr.had_signs) must be 256 I8 values"));
     F->signs = *sg;
     if (F->vr.size() != nlin->u || (long long)nlin->u != 7 * n_layer)
-        return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: %zu VR tensors, vr.n_linear %llu, expected 7 x %lld", F->vr.size(), (unsigned long long)nlin->u, n_layer));
+        return bail(set_error(P8X_ERR_FORMAT, "p8x_vr_open: found %zu weight tensors; vr.n_linear says %llu and 7 per layer over %lld layers are expected", F->vr.size(), (unsigned long long)nlin->u, n_layer));
     for (auto &e : F->vr) e.d.name = e.name.c_str();
     *out = F;
     return P8X_OK;
@@ -415,20 +415,20 @@ int p8x_vr_load(p8x_vr_file *F, int i, void *slot, size_t cap) {
         memcpy(&w515, f3.data() + 2060, 4);
         size_t kb = 0;
         if (p8x_vr3_rows(d.fbytes, (size_t)d.K, w515, &kb) != (size_t)d.rows || kb != d.kbytes || d.kbytes > n)
-            return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' VR3 header changed since open", d.name);
+            return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': the layout-3 header differs from what p8x_vr_open read", d.name);
         if ((rc = p8x_vr3_expand(f3.data(), d.fbytes, d.rows, d.K, buf, n))) return rc;
     }
     const uint32_t *hw = reinterpret_cast<const uint32_t *>(buf);
     if (d.kbytes < kHeaderBytes || hw[513] != kNS || hw[514] != kTRL)
-        return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' header NS %u TRL %u (need %u / %u)", d.name, d.kbytes >= kHeaderBytes ? hw[513] : 0u,
+        return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': header declares %u states and trellis rate %u; this library needs %u and %u", d.name, d.kbytes >= kHeaderBytes ? hw[513] : 0u,
                          d.kbytes >= kHeaderBytes ? hw[514] : 0u, kNS, kTRL);
     {
         std::lock_guard<std::mutex> lk(F->mu);
         if (F->hdr0.empty()) F->hdr0.assign(buf, buf + 2052);
-        else if (memcmp(F->hdr0.data(), buf, 2052) != 0) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' tables (A, B, c) differ from the first tensor", d.name);
+        else if (memcmp(F->hdr0.data(), buf, 2052) != 0) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': its codebook tables are not those of the first weight (one codebook per file)", d.name);
     }
     const size_t nt = (size_t)(d.rows / 32) * (d.K / 256);
-    if (kHeaderBytes + 4 * nt > d.kbytes) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' too short for M", d.name);
+    if (kHeaderBytes + 4 * nt > d.kbytes) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': the tile-word table runs past the weight bytes", d.name);
     size_t words = 0;
     for (size_t t = 0; t < nt; ++t) {
         uint32_t m;
@@ -436,10 +436,10 @@ int p8x_vr_load(p8x_vr_file *F, int i, void *slot, size_t cap) {
         words += 64 * nw_of_class(m >> 29);
     }
     if (kernel_bytes(d.rows, d.K, words) != d.kbytes)
-        return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' has %zu B, its M words imply %zu B", d.name, d.kbytes, kernel_bytes(d.rows, d.K, words));
+        return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': %zu weight bytes, but the tile words describe %zu", d.name, d.kbytes, kernel_bytes(d.rows, d.K, words));
     size_t off[6];   // delta, c16, prm, pinv, signs, trailer
     side_offsets(n, (size_t)d.rows, (size_t)d.K, (size_t)d.nd, off);
-    if (d.kbytes > off[0]) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' kernel bytes overlap the side regions", d.name);
+    if (d.kbytes > off[0]) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': the weight bytes run into the side data", d.name);
     if ((rc = read_at(F, e.c, 0, buf + off[1], 2 * (size_t)d.K))) return rc;
     int16_t *p = reinterpret_cast<int16_t *>(buf + off[2]);
     if (e.has_prm) {
@@ -450,7 +450,7 @@ int p8x_vr_load(p8x_vr_file *F, int i, void *slot, size_t cap) {
     {   // prm must be a permutation of 0..rows-1; pinv = its inverse
         std::vector<uint8_t> seen(d.rows, 0);
         for (int r = 0; r < d.rows; ++r)
-            if (p[r] < 0 || p[r] >= d.rows || seen[p[r]]++) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' vr_prm is not a permutation", d.name);
+            if (p[r] < 0 || p[r] >= d.rows || seen[p[r]]++) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': the row order repeats or skips a row", d.name);
         int16_t *q = reinterpret_cast<int16_t *>(buf + off[3]);
         for (int r = 0; r < d.rows; ++r) q[p[r]] = (int16_t)r;
     }
@@ -459,12 +459,12 @@ int p8x_vr_load(p8x_vr_file *F, int i, void *slot, size_t cap) {
         if ((rc = read_at(F, e.dval, 0, buf + off[0] + 4 * (size_t)d.nd, 4 * (size_t)d.nd))) return rc;
         const uint16_t *dr = reinterpret_cast<const uint16_t *>(buf + off[0]), *dc = dr + d.nd;
         for (int k = 0; k < d.nd; ++k)
-            if (dr[k] >= d.rows || dc[k] >= d.K) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s' delta index out of range", d.name);
+            if (dr[k] >= d.rows || dc[k] >= d.K) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: '%s': a clamp-delta entry points outside the matrix", d.name);
     }
     if ((rc = read_at(F, F->signs, 0, buf + off[4], 256))) return rc;
     for (int k = 0; k < 256; ++k) {
         const int8_t v = (int8_t)buf[off[4] + k];
-        if (v != 1 && v != -1) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: vr.had_signs must be +-1");
+        if (v != 1 && v != -1) return set_error(P8X_ERR_FORMAT, "p8x_vr_load: a rotation sign other than +1 or -1");
     }
     const uint32_t tr[8] = {kMagic0, kMagic1, (uint32_t)d.kbytes, (uint32_t)d.nd, (uint32_t)d.rows, (uint32_t)d.K, kNS, 1u};
     memcpy(buf + off[5], tr, sizeof tr);

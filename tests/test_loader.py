@@ -170,18 +170,18 @@ def _kv_set(key, t, v):
 OPEN_ERRORS = [
     ("no vr.format", dict(kv_edit=_kv_set("vr.format", G.STR, None)), "vr.format"),
     ("no vr.ns", dict(kv_edit=_kv_set("vr.ns", G.U32, None)), "vr.ns"),
-    ("vr.ns 100", dict(kv_edit=_kv_set("vr.ns", G.U32, 100)), "vr.ns = 100"),
-    ("vr.trl 3", dict(kv_edit=_kv_set("vr.trl", G.U32, 3)), "vr.trl"),
-    ("vr.layout 4", dict(kv_edit=_kv_set("vr.layout", G.U32, 4)), "vr.layout = 4"),
-    ("vr.layout string", dict(kv_edit=_kv_set("vr.layout", G.STR, "3")), "vr.layout must be uint32"),
-    ("n_linear 6", dict(kv_edit=_kv_set("vr.n_linear", G.U32, 6)), "expected 7 x 1"),
-    ("no block_count", dict(kv_edit=_kv_set("llama.block_count", G.U32, None)), "expected 7 x -1"),
-    ("no vr_prm", dict(tensor_edit=_drop("blk.0.attn_q.vr_prm")), "vr_prm I16 expected"),
-    ("no weight", dict(tensor_edit=_drop("blk.0.attn_k.weight")), "has vr_c but no weight"),
-    ("didx without dval", dict(tensor_edit=_drop("blk.0.ffn_gate.vr_dval")), "needs both vr_didx and vr_dval"),
+    ("vr.ns 100", dict(kv_edit=_kv_set("vr.ns", G.U32, 100)), "declares 100 trellis states"),
+    ("vr.trl 3", dict(kv_edit=_kv_set("vr.trl", G.U32, 3)), "vr.trl == 2"),
+    ("vr.layout 4", dict(kv_edit=_kv_set("vr.layout", G.U32, 4)), "unknown side-data layout 4"),
+    ("vr.layout string", dict(kv_edit=_kv_set("vr.layout", G.STR, "3")), "vr.layout has a type other than uint32"),
+    ("n_linear 6", dict(kv_edit=_kv_set("vr.n_linear", G.U32, 6)), "over 1 layers"),
+    ("no block_count", dict(kv_edit=_kv_set("llama.block_count", G.U32, None)), "over -1 layers"),
+    ("no vr_prm", dict(tensor_edit=_drop("blk.0.attn_q.vr_prm")), "vr_prm I16"),
+    ("no weight", dict(tensor_edit=_drop("blk.0.attn_k.weight")), "vr_c tensor without its weight"),
+    ("didx without dval", dict(tensor_edit=_drop("blk.0.ffn_gate.vr_dval")), "come in pairs"),
     ("no signs", dict(tensor_edit=_drop("vr.had_signs")), "had_signs"),
     ("weight F16", dict(tensor_edit=lambda ts: [(n, G.GGML_F16 if n == "blk.0.attn_v.weight" else t, [ne[0] // 2] if n == "blk.0.attn_v.weight" else ne, r)
-                                                  for n, t, ne, r in ts]), "must be I8 1-D"),
+                                                  for n, t, ne, r in ts]), "one-dimensional I8"),
 ]
 
 
@@ -196,13 +196,13 @@ def test_open_rejects_vr3_specific(tmp_path):
     def add_prm(ts):
         return ts + [("blk.0.attn_q.vr_prm", G.GGML_I16, [128], G.as_bytes(np.arange(128, dtype=np.int16)))]
     path, _ = model(tmp_path, 3, tensor_edit=add_prm)
-    with pytest.raises(p8x.P8xError, match="has vr_prm in a vr.layout 3 file"):
+    with pytest.raises(p8x.P8xError, match="a vr_prm tensor is present"):
         p8x.VrFile(path)
 
     def shorten(ts):
         return [(n, t, [ne[0] - 4] if n == "blk.0.attn_q.weight" else ne, r[:-4] if n == "blk.0.attn_q.weight" else r) for n, t, ne, r in ts]
     path, _ = model(tmp_path, 3, tensor_edit=shorten)
-    with pytest.raises(p8x.P8xError, match="not a valid VR3 tensor"):
+    with pytest.raises(p8x.P8xError, match="not a layout-3 weight"):
         p8x.VrFile(path)
 
 
@@ -243,11 +243,11 @@ def _bad_class(b):
 
 
 LOAD_ERRORS = [
-    ("prm duplicate", "blk.0.attn_q.vr_prm", _bad_prm, "blk.0.attn_q.weight", "not a permutation"),
-    ("delta row out of range", "blk.0.attn_k.vr_didx", _bad_didx, "blk.0.attn_k.weight", "delta index out of range"),
-    ("sign zero", "vr.had_signs", _bad_sign, "blk.0.attn_q.weight", r"had_signs must be \+-1"),
-    ("header NS", "blk.0.attn_q.weight", _bad_ns, "blk.0.attn_q.weight", "header NS 104"),
-    ("M class", "blk.0.attn_q.weight", _bad_class, "blk.0.attn_q.weight", "M words imply"),
+    ("prm duplicate", "blk.0.attn_q.vr_prm", _bad_prm, "blk.0.attn_q.weight", "repeats or skips a row"),
+    ("delta row out of range", "blk.0.attn_k.vr_didx", _bad_didx, "blk.0.attn_k.weight", "points outside the matrix"),
+    ("sign zero", "vr.had_signs", _bad_sign, "blk.0.attn_q.weight", "rotation sign other than"),
+    ("header NS", "blk.0.attn_q.weight", _bad_ns, "blk.0.attn_q.weight", "declares 104 states"),
+    ("M class", "blk.0.attn_q.weight", _bad_class, "blk.0.attn_q.weight", "tile words describe"),
 ]
 
 
@@ -260,11 +260,11 @@ def test_load_rejects(tmp_path, what, tname, fn, load, msg):
 
 
 def test_load_rejects_different_tables(tmp_path):
-    """every tensor must carry the first loaded tensor's tables (A, B, c)"""
+    """every tensor must carry the first loaded tensor's codebook tables"""
     path, _ = model(tmp_path, 2, tensor_edit=_edit_tensor("blk.0.attn_k.weight", _bad_tables))
     f = p8x.VrFile(path)
     f.load(f.find("blk.0.attn_q.weight"))
-    with pytest.raises(p8x.P8xError, match="tables"):
+    with pytest.raises(p8x.P8xError, match="codebook tables"):
         f.load(f.find("blk.0.attn_k.weight"))
 
 
@@ -304,5 +304,5 @@ def test_open_rejects_tensor_no_slot_fits(tmp_path):
         assert lin.slot_type is None
         return [t for t in ts if not t[0].startswith("blk.0.attn_k.")] + tensors_of("blk.0.attn_k", lin, 3)
     path, _ = model(tmp_path, 3, tensor_edit=tiny)
-    with pytest.raises(p8x.P8xError, match="no slot type fits"):
+    with pytest.raises(p8x.P8xError, match="exceed every slot size"):
         p8x.VrFile(path)
