@@ -438,10 +438,15 @@ static MmPlan mm_plan(const p8x_tensor *t, int N) {
     p.tiles_n = (N + kMmTok - 1) / kMmTok;
     const long base = (long)p.tiles_m * p.tiles_n, slots = num_cus();
     const double plane_us = 2.0 * 4.0 * N * t->rows / 5e6;
+    // a split's planes stay within what the no-allocation entry point holds next to x', so that it runs the same
+    // plan (and returns the same bits) as p8x_mul_mat wherever it runs at all
+    const size_t xb = ((size_t)N * t->K * sizeof(_Float16) + 255) & ~(size_t)255;
+    const size_t cap = xb < (size_t)P8X_NOALLOC_SCRATCH_BYTES ? (size_t)P8X_NOALLOC_SCRATCH_BYTES - xb : 0;
     double best = -1.0;
     p.nsplit = 1; p.kper = t->nb;
     for (int ns = 1; ns <= std::min(t->nb, 16); ++ns) {
         const int kper = (t->nb + ns - 1) / ns, nsr = (t->nb + kper - 1) / kper;
+        if (nsr > 1 && (size_t)nsr * N * t->rows * 4 > cap) continue;
         const double cost = (double)((base * nsr + slots - 1) / slots) * kper * block_us + ((nsr > 1 || !t->prm_identity) ? nsr * plane_us : 0.0);
         if (best < 0 || cost < best) { best = cost; p.nsplit = nsr; p.kper = kper; }
     }
@@ -469,9 +474,6 @@ static void mm_workspace(const p8x_tensor *t, int N, size_t *x_bytes, size_t *pl
     *plane_bytes = p.nsplit == 1 && t->prm_identity ? 0 : (size_t)p.nsplit * N * t->rows * 4;
 }
 
-// the launches of one prompt GEMM with its workspace given: xr >= N K fp16, wmm >= the plane bytes (unused when the
-// output is written directly)
-
 // k_mm_finish keeps a row of the output (up to 128 KB) in dynamic LDS. The attribute that allows it is per device:
 // set once on each device this process launches on (callers on several threads serialize here).
 static int finish_lds_attribute() {
@@ -489,6 +491,9 @@ static int finish_lds_attribute() {
     done[dev] = 1;
     return P8X_OK;
 }
+
+// the launches of one prompt GEMM with its workspace given: xr >= N K fp16, wmm >= the plane bytes (unused when the
+// output is written directly)
 
 static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, _Float16 *xr,
                              float *wmm, hipStream_t st) {

@@ -264,6 +264,20 @@ class Stream:
     def sync(self):
         hip_check(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
 
+    def release(self):
+        if self.h:
+            hip().hipStreamSynchronize(self.h)
+            hip().hipStreamDestroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        if _finalizing():
+            return
+        try:
+            self.release()
+        except Exception:
+            pass
+
 
 class Graph:
     """A HIP graph of the work `enqueue(stream)` issues on `stream`, captured once (global capture mode: a call
@@ -312,6 +326,19 @@ class Event:
         hip_check(hip().hipEventSynchronize(later.h), "hipEventSynchronize")
         hip_check(hip().hipEventElapsedTime(ctypes.byref(ms), self.h, later.h), "hipEventElapsedTime")
         return ms.value
+
+    def release(self):
+        if self.h:
+            hip().hipEventDestroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        if _finalizing():
+            return
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 # --------------------------------------------------------------------------------------------------- host producers

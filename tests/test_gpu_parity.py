@@ -153,7 +153,9 @@ def test_gemv_deterministic():
 
 
 def test_quantized_4096_config():
-    """4096 x 4096, N(0, 0.02^2) with 0.1% outliers x10, through the class-3 quantizer; CPU dequant vs GPU."""
+    """4096 x 4096, N(0, 0.02^2) with 0.1% outliers x10, through the class-3 quantizer; CPU dequant vs GPU; the GEMV
+    with both activation formats the reference offers for it: 8 bits per 128 columns and ggml's block_q8_1 (blocks
+    bit-exact, integer partials exact, the GEMV within the fp64 bar)."""
     rng = np.random.default_rng(2024)
     W = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
     m = rng.random(W.shape) < 0.001
@@ -165,6 +167,11 @@ def test_quantized_4096_config():
     assert np.array_equal(Wd.view(np.uint32), orc.dequant().view(np.uint32))
     x = rng.standard_normal(4096).astype(np.float32)
     assert rel_l2(t.mul_mat_vec(x)[0], orc.gemv_f64(x)) < 1e-5
+    blk = t.quantize_q8_1(x)[0]
+    assert np.array_equal(blk, orc.quantize_q8_1(x))
+    _, part = t.vec_dot(p8x.ACT_Q8_1, blk[None, :], None, partials=True)
+    assert np.array_equal(part[0], orc.partials_q8_1(blk))
+    assert rel_l2(t.mul_mat_vec(x, act=p8x.ACT_Q8_1)[0], orc.gemv_f64(x, act="q8_1")) < 1e-5
 
 
 def test_encoded_ldlq_slot_all_classes():

@@ -57,6 +57,22 @@ def test_noalloc_matches_mul_mat_two_calls():
     assert rel_l2(Y2, O.dense_f64(orc2.dequant(), X2)) < 1e-3
 
 
+def test_noalloc_runs_the_ffn_down_shape():
+    """the 512-token Llama FFN down-projection (4096 x 14336, class 3, bf16): its K-split plan fits the scratch next
+    to x', and both entry points run that same plan (bitwise equal outputs)"""
+    rng = np.random.default_rng(74)
+    rows, K, N = 4096, 14336, 512
+    slot = p8x.synth_random(74, rows, K, nd=8)
+    t = p8x.Tensor(slot, rows, K)
+    X = bf16(rng.standard_normal((N, K)))
+    Y, R = run_both(t, X, p8x.BF16)
+    assert np.array_equal(Y.view(np.uint32), R.view(np.uint32))
+    orc = O.Oracle(slot, rows, K)
+    sample = [0, 3, 510]
+    Xs = (X[sample].astype(np.uint32) << 16).view(np.float32)
+    assert rel_l2(Y[sample], O.dense_f64(orc.dequant(), Xs)) < 1e-3
+
+
 def test_noalloc_rejects_oversized_request():
     """4096 tokens of a 14336 x 4096 tensor need ~270 MB of workspace: rejected before any launch"""
     rows, K, N = 14336, 4096, 4096
