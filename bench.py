@@ -442,6 +442,77 @@ def measure_dequant(steps):
     return res
 
 
+def measure_grouped(tensors, xs, ybufs, stream, steps, warmup):
+    """One grouped launch (activation prep + fused decode-GEMV + finishing) over every linear per step. A change of
+    load sets off a power-management transient: the first few steps run fast, the next few dozen up to 60% slower,
+    then the step time settles (measured per step on MI355X). The grouped launch therefore runs until its step time is
+    stable (settle steps, reported), then the warmup steps, then K timed steps back to back (the step time), then the
+    same K steps again with each fused decode + GEMV launch carrying a pair of HIP events that the runtime records at
+    that kernel's own start and end (hipExtLaunchKernel): the kernel's duration, the interval rocprofv3's kernel trace
+    reports. The events put about 11 us of queue work around the kernel, so the step time is timed without them.
+    Returns the batch object (still live) and (settle steps, ms per step, ms per step with events, kernel ms, wall s)."""
+    batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ybufs)
+    settle_steps, prev = 0, None
+    while settle_steps < 400:
+        a, b = p8x.Event(), p8x.Event()
+        a.record(stream)
+        for _ in range(10):
+            batch.run(stream)
+        b.record(stream)
+        settle_steps += 10
+        cur = a.elapsed_ms(b)
+        if settle_steps >= 60 and prev is not None and abs(cur - prev) <= 0.02 * prev:
+            break
+        prev = cur
+    for _ in range(warmup):
+        batch.run(stream)
+    stream.sync()
+    e0, e1 = p8x.Event(), p8x.Event()
+    e0.record(stream)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        batch.run(stream)
+    e1.record(stream)
+    stream.sync()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_ms(e1) / steps
+    ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
+    e2, e3 = p8x.Event(), p8x.Event()
+    e2.record(stream)
+    for s_ in range(steps):
+        for stage in range(batch.stages):
+            batch.run_stage(stage, stream, events=ev[s_] if stage == 1 else None)
+    e3.record(stream)
+    stream.sync()
+    ms_per_step_events = e2.elapsed_ms(e3) / steps
+    gemv_ms = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    return batch, settle_steps, ms_per_step, ms_per_step_events, gemv_ms, wall
+
+
+def measure_b4_mix(args, stream):
+    """The same grouped launch over the stack with the released models' class mix (attn_v class 6; ffn_down 78.1%
+    class 3, 12.5% class 4, 9.4% class 2; the rest class 3): the kernels for several class sets."""
+    tensors, kinds, _ = build_stack(args.layers, "b4", 0)
+    step_bytes = sum(t.stream_bytes for t in tensors)
+    rng = np.random.default_rng(0)
+    xs = {K: p8x.DeviceBuffer.from_numpy(rng.standard_normal(K).astype(np.float32)) for K in sorted({t.K for t in tensors})}
+    ybufs = [p8x.DeviceBuffer(4 * t.rows) for t in tensors]
+    batch, settle, ms, ms_ev, gemv_ms, _ = measure_grouped(tensors, xs, ybufs, stream, args.steps, args.warmup)
+    batch.release()
+    for t in tensors:
+        t.release()
+    for b in list(xs.values()) + ybufs:
+        b.free()
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    kgbs = step_bytes / (gemv_ms * 1e-3) / 1e9
+    log(f"b4 mix: {ms * 1e3:.1f} us/step ({gbs:.0f} GB/s), GEMV kernel {gemv_ms * 1e3:.1f} us -> {kgbs:.0f} GB/s")
+    return {"workload": "the headline stack with the released models' class mix (attn_v class 6; ffn_down 78.1% c3, "
+                        "12.5% c4, 9.4% c2); one grouped launch per step", "stream_bytes_per_step": int(step_bytes),
+            "settle_steps": settle, "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel_us": round(gemv_ms * 1e3, 1),
+            "kernel_GB/s": round(kgbs, 1), "kernel_frac": round(kgbs / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -456,6 +527,7 @@ def main():
     ap.add_argument("--no-dependent", action="store_true", help="skip the dependency-respecting decode step")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prompt GEMM and dequantize measurements")
     ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
+    ap.add_argument("--no-mix", action="store_true", help="skip the b4 class-mix line")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replays of the per-linear and dependent steps (the one-launch step still runs)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
@@ -487,54 +559,14 @@ def main():
     gemm = measure_gemm(max(5, args.steps // 2)) if not args.no_gemm else None
     deq = measure_dequant(max(5, args.steps // 2)) if not args.no_gemm else None
 
-    # ---- headline: one grouped launch (activation prep + fused decode-GEMV + finishing) over every linear per step.
-    # A change of load sets off a power-management transient: the first few steps run fast, the next few dozen up to
-    # 60% slower, then the step time settles (measured per step on MI355X). The grouped launch therefore runs until
-    # its step time is stable (settle_steps, reported), then the W warmup steps, then the K timed steps.
-    batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ybufs)
-    settle_steps, prev = 0, None
-    while settle_steps < 400:
-        a, b = p8x.Event(), p8x.Event()
-        a.record(stream)
-        for _ in range(10):
-            batch.run(stream)
-        b.record(stream)
-        settle_steps += 10
-        cur = a.elapsed_ms(b)
-        if settle_steps >= 60 and prev is not None and abs(cur - prev) <= 0.02 * prev:
-            break
-        prev = cur
-    for _ in range(args.warmup):
-        batch.run(stream)
-    stream.sync()
-    # K timed steps back to back, plain launches: the step time (value)
-    e0, e1 = p8x.Event(), p8x.Event()
-    e0.record(stream)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        batch.run(stream)
-    e1.record(stream)
-    stream.sync()
-    wall = time.perf_counter() - t0
-    ms_per_step = e0.elapsed_ms(e1) / args.steps
-    # the same K steps again, each fused decode + GEMV launch carrying a pair of HIP events that the runtime records
-    # at that kernel's own start and end (hipExtLaunchKernel): the kernel's duration, the interval rocprofv3's
-    # kernel trace reports (the roofline of the dominant kernel). The events put about 11 us of queue work around
-    # the kernel, so the step time above is timed without them.
-    ev = [(p8x.Event(), p8x.Event()) for _ in range(args.steps)]
-    e2, e3 = p8x.Event(), p8x.Event()
-    e2.record(stream)
-    for s_ in range(args.steps):
-        for stage in range(batch.stages):
-            batch.run_stage(stage, stream, events=ev[s_] if stage == 1 else None)
-    e3.record(stream)
-    stream.sync()
-    ms_per_step_events = e2.elapsed_ms(e3) / args.steps
-    gemv_ms = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    # ---- headline: one grouped launch over every linear per step (measure_grouped)
+    batch, settle_steps, ms_per_step, ms_per_step_events, gemv_ms, wall = measure_grouped(tensors, xs, ybufs, stream, args.steps,
+                                                                                          args.warmup)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
     log(f"stream: settled after {settle_steps} steps; {ms_per_step * 1e3:.1f} us/step, GEMV kernel {gemv_ms * 1e3:.1f} us "
         f"-> {achieved:.0f} GB/s (steps with kernel events {ms_per_step_events * 1e3:.1f} us)")
+    b4 = measure_b4_mix(args, stream) if args.mix == "c3" and not args.no_mix else None
 
     if args.copy_calib:
         n = args.copy_calib << 20
@@ -581,6 +613,7 @@ def main():
         "qwen3_14b_columns": qwen14b,
         "qwen3_4b_layer": qwen4b,
         "quantized_4096": quant4096,
+        "b4_mix": b4,
         "host_wall_s": round(wall, 3),
     }
     # every handle released here, while the runtime (and a profiler's tool attached to it) is still up; nothing is
