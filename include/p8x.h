@@ -147,6 +147,15 @@ int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *
  * clamp deltas), each row's pair meets through the gate tensor's workspace (calls with one gate tensor are ordered
  * on one stream). */
 int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream);
+/* The two calls above with the activation mode chosen, as p8x_mul_mat_vec_act (the reference's CPU path defaults to
+ * x16, CPU.patch:1157-1160, and prepares the activation once for consecutive mul_mats on the same input and c,
+ * CPU.patch:1142-1143, :1171-1180): P8X_ACT_Q8_128 runs the one-launch forms above; P8X_ACT_Q8_1 and P8X_ACT_X16
+ * prepare x once in tensor 0's (the gate's) workspace and run each tensor's GEMV on it (X16: both planes as two
+ * columns, summed, then the clamp delta), then for the GLU silu(gate) * up. Same values as p8x_mul_mat_vec_act per
+ * tensor. Calls sharing a tensor are ordered on one stream. */
+int p8x_mul_mat_vec_multi_act(const p8x_tensor *const *tensors, int n, int act, const float *x, size_t ldx, float *const *y,
+                              const size_t *ldy, void *stream);
+int p8x_mul_mat_vec_glu_act(const p8x_tensor *gate, const p8x_tensor *up, int act, const float *x, size_t ldx, float *out, void *stream);
 
 /* ---- a decode step's chain of linears in one launch ----
  * The graph-level form of the per-node calls above: where the reference walks the graph's MUL_MAT nodes once
@@ -199,6 +208,11 @@ int p8x_mul_mat_noalloc(const p8x_tensor *t, const void *x, int x_dtype, int N, 
 typedef struct p8x_gemv_batch p8x_gemv_batch;
 int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                           float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out);
+/* the same with the activation mode: P8X_ACT_Q8_128 (as above) or P8X_ACT_X16 (1..4 columns; the prep writes both
+ * planes of each column, the fused launch multiplies them as 2 ncols columns, the finishing launch sums each
+ * column's planes and then adds the clamp delta: p8x_mul_mat_vec_act's x16 values) */
+int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                              float *const *y, const size_t *ldy, int njobs, int ncols, int act, p8x_gemv_batch **out);
 int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
 /* the launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV (sorted-row
  * partials per K-chunk and column), 2 = partials to original rows with the clamp delta */

@@ -98,6 +98,14 @@ __global__ __launch_bounds__(256) void k_x16_combine(const float *__restrict__ y
     y[(size_t)n * ldy + ro] = v;
 }
 
+// out[r] = silu(g[r]) * u[r], silu(g) = g / (1 + e^-g) (ggml's swiglu): the gated input from two finished products
+__global__ __launch_bounds__(256) void k_glu_rows(const float *__restrict__ g, const float *__restrict__ u, int rows, float *__restrict__ out) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const float gate = g[r], up = u[r];
+    out[r] = gate / (1.0f + expf(-gate)) * up;
+}
+
 // block_q8_1 over x' (ggml layout: fp16 d, fp16 s = d * sum q, 32 int8). 8 lanes per 32-column block.
 __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
                                                  uint8_t *__restrict__ blocks) {
@@ -340,6 +348,44 @@ __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restri
     }
 }
 
+// The x16 form of the batch prep (P8X_ACT_X16, the arithmetic of k_act_x16): grid (ceil(total blocks / 4), ncols),
+// column n's two planes written as virtual columns 2n (hi, scale 128 d) and 2n + 1 (lo, scale d) of the broadcast
+// layout, so the grouped kernel multiplies them as 2 ncols columns.
+__global__ __launch_bounds__(256) void k_act_x16_batch(const ActJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int total) {
+    const int gb = 4 * blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = blockIdx.y, lane = threadIdx.x & 63;
+    if (gb >= total) return;
+    const ActJob &J = jobs[as_const(blk_job)[gb]];
+    const int b = gb - J.blk0;
+    BlockLane in;
+    in.load(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane);
+    float v[4];
+    rotate_block_lane(in, lane, v);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = half_wave_max(am, lane);
+    const float dd = div_rn(am, 8191.f);
+    const float id = dd > 0.f ? div_rn(1.f, dd) : 0.f;
+    uint32_t ph = 0, pl = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int q = __float2int_rn(v[e] * id);
+        const int hi = (q + 64) >> 7, lo = q - 128 * hi;
+        ph |= (uint32_t)(uint8_t)hi << (8 * e);
+        pl |= (uint32_t)(uint8_t)lo << (8 * e);
+    }
+    const int hs = lane >> 5, t = lane & 31;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        uint32_t *e = reinterpret_cast<uint32_t *>(J.q + ((size_t)(2 * n + p) * J.nb + b) * kBcastBlockBytes + 256 * hs + 16 * (t & 15));
+        if (t < 16) {
+            e[0] = p ? pl : ph;
+            e[2] = __builtin_bit_cast(uint32_t, p ? dd : 128.f * dd);
+            e[3] = 0u;
+        } else {
+            e[1] = p ? pl : ph;
+        }
+    }
+}
+
 // Finishing launch of a grouped GEMV. Rows that carry clamp-delta entries (bit 15 of prmd) go to the first blocks,
 // one thread per such row: it sums the row's K-chunk partials in chunk order and adds its delta entries (resolved at
 // batch creation, so its loads do not wait on one another beyond the activation gather); these blocks come first so
@@ -358,6 +404,7 @@ struct FinishJob {
     float *y;
     unsigned ldx, ldy;   // column strides of x and y
     int rows, nks, ncol;
+    int planes;          // 1: x16, the partials hold 2 ncol virtual columns (hi 2n, lo 2n + 1) and column n is their sum
 };
 
 // a row with clamp-delta entries, resolved when the batch is created: its sorted row (partials) and original
@@ -373,9 +420,14 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
         const FinDelta d = drows[i];
         const FinishJob &J = jobs[d.job];
         const gptr<const float> wp = as_global(J.wpart);
-        for (int n = 0; n < J.ncol; ++n) {
+        const int ncv = J.planes ? 2 * J.ncol : J.ncol;
+        auto colsum = [&](int c) {
             float v = 0.f;
-            for (int ks = 0; ks < J.nks; ++ks) v += wp[((size_t)ks * J.ncol + n) * J.rows + d.r];
+            for (int ks = 0; ks < J.nks; ++ks) v += wp[((size_t)ks * ncv + c) * J.rows + d.r];
+            return v;
+        };
+        for (int n = 0; n < J.ncol; ++n) {
+            float v = J.planes ? colsum(2 * n) + colsum(2 * n + 1) : colsum(n);   // x16: the two planes, then the delta
             if (J.x) {
                 const gptr<const float> x = as_global(J.x) + (size_t)n * J.ldx;
                 for (int e = d.e0; e < d.e1; ++e) v += as_global(ent)[e].val * x[as_global(ent)[e].col];
@@ -389,6 +441,7 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
     const FinishJob &J = jobs[e & 0xFFFFFFu];
     const int r0 = (int)(e >> 24) * kFinRows + threadIdx.x;
     const gptr<const float> wp = as_global(J.wpart);
+    const int ncv = J.planes ? 2 * J.ncol : J.ncol;
     int r[4];
     uint32_t pd[4];
 #pragma unroll
@@ -396,19 +449,33 @@ __global__ __launch_bounds__(256) void k_gemv_finish(const FinishJob *__restrict
         r[i] = min(r0 + 256 * i, J.rows - 1);
         pd[i] = as_global(J.prmd)[r[i]];
     }
-    for (int n = 0; n < J.ncol; ++n) {
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
+    // virtual column c of the four rows summed over the K-chunks in chunk order (four chunks' loads issued together)
+    auto colsum = [&](int c, float (&v)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = 0.f;
         for (int k0 = 0; k0 < J.nks; k0 += 4) {
             float p[4][4];
 #pragma unroll
             for (int k = 0; k < 4; ++k)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) p[k][i] = k0 + k < J.nks ? wp[((size_t)(k0 + k) * J.ncol + n) * J.rows + r[i]] : 0.f;
+                for (int i = 0; i < 4; ++i) p[k][i] = k0 + k < J.nks ? wp[((size_t)(k0 + k) * ncv + c) * J.rows + r[i]] : 0.f;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (k0 + k < J.nks) v[i] += p[k][i];
+        }
+    };
+    for (int n = 0; n < J.ncol; ++n) {
+        float v[4];
+        if (J.planes) {
+            float lo[4];
+            colsum(2 * n, v);
+            colsum(2 * n + 1, lo);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += lo[i];
+        } else {
+            colsum(n, v);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -437,6 +504,7 @@ int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_
 
 struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
+    int act = P8X_ACT_Q8_128, ncv = 1;   // activation mode; columns the grouped kernel multiplies (x16: 2 ncols planes)
     int split_jobs = 0, small_launch = 0, waves = 0;   // plan facts reported by p8x_gemv_batch_info
     unsigned *ctr = nullptr;       // its unit counters (in work)
     uint32_t *d_ujob = nullptr;    // unit -> job
@@ -472,9 +540,17 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b) {
 
 int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                           float *const *y, const size_t *ldy, int njobs, int ncols, p8x_gemv_batch **out) {
+    return p8x_gemv_batch_create_act(tensors, x, ldx, y, ldy, njobs, ncols, P8X_ACT_Q8_128, out);
+}
+
+int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                              float *const *y, const size_t *ldy, int njobs, int ncols, int act, p8x_gemv_batch **out) {
     if (!tensors || !x || !ldx || !y || !ldy || !out || njobs < 1) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: bad arguments");
     if (njobs >= (1 << 24)) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: %d jobs (at most %d)", njobs, (1 << 24) - 1);
     if (ncols < 1 || ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: ncols %d", ncols);
+    if (act != P8X_ACT_Q8_128 && act != P8X_ACT_X16) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: act %d (P8X_ACT_Q8_128 or P8X_ACT_X16)", act);
+    if (act == P8X_ACT_X16 && 2 * ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: x16 takes at most %d columns", P8X_MAX_COLS / 2);
+    const int ncv = act == P8X_ACT_X16 ? 2 * ncols : ncols;   // the grouped kernel's columns (x16: both planes)
     *out = nullptr;
     size_t hist[8] = {0};
     for (int i = 0; i < njobs; ++i) {
@@ -486,10 +562,10 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
             return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: job %d has a different codebook", i);
         for (int c = 0; c < 8; ++c) hist[c] += t->class_tiles[c];
     }
-    // workspace layout: unit counters | per job: activations [ncols][nb] in the broadcast layout | partials
-    // [nks][ncols][rows]
+    // workspace layout: unit counters | per job: activations [ncv][nb] in the broadcast layout | partials
+    // [nks][ncv][rows]
     std::vector<GemvJob> jobs(njobs);
-    std::vector<ActJob> act(njobs);
+    std::vector<ActJob> ajobs(njobs);
     std::vector<size_t> off_q(njobs), off_p(njobs);
     size_t bytes = 0;
     auto take = [&](size_t n) { const size_t o = bytes; bytes = align16(bytes + n); return o; };
@@ -505,7 +581,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         // Units are handed out longest first, so the launch drains on the units of the last jobs. Those jobs are
         // split along K (units of >= 4 blocks, partial rows summed by the finishing launch) until about two
         // rounds of the launch's waves have short units to finish on.
-        const long need = 2L * wave_wg_per_cu(cm, ncols) * num_cus() * wave_waves(cm, ncols);
+        const long need = 2L * wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
         std::vector<int> order(njobs);
         for (int i = 0; i < njobs; ++i) order[i] = i;
         std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return tensors[a]->nb > tensors[c]->nb; });
@@ -529,15 +605,16 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         const p8x_tensor *t = tensors[i];
         const int kc = kcs[i];
         const int nks = (t->nb + kc - 1) / kc;
-        off_q[i] = take((size_t)ncols * t->nb * kBcastBlockBytes);
-        off_p[i] = take(4 * (size_t)nks * ncols * t->rows);   // partial rows (the finishing launch reads them)
+        off_q[i] = take((size_t)ncv * t->nb * kBcastBlockBytes);
+        off_p[i] = take(4 * (size_t)nks * ncv * t->rows);   // partial rows (the finishing launch reads them)
         fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, 1, 0);
-        act[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, t->nb, nullptr, blk0};
+        ajobs[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, t->nb, nullptr, blk0};
         blk0 += t->nb;
         ablk.insert(ablk.end(), (size_t)t->nb, (uint32_t)i);
     }
     p8x_gemv_batch *b = new p8x_gemv_batch();
     b->njobs = njobs; b->ncols = ncols; b->cm = cm; b->total_blocks = blk0;
+    b->act = act; b->ncv = ncv;
     b->a2 = tensors[0]->a2;
     int rc;
     if (hipMalloc(&b->work, bytes) != hipSuccess || hipMalloc((void **)&b->d_jobs, sizeof(GemvJob) * njobs) != hipSuccess ||
@@ -550,7 +627,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     for (int i = 0; i < njobs; ++i) {
         jobs[i].q = w + off_q[i];
         jobs[i].d = nullptr;
-        act[i].q = (int8_t *)(w + off_q[i]);
+        ajobs[i].q = (int8_t *)(w + off_q[i]);
         jobs[i].wpart = (float *)(w + off_p[i]);
         jobs[i].wcnt = nullptr;
     }
@@ -564,7 +641,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
     b->total_tasks = task0;
     b->small_launch = small_launch;
-    b->waves = wave_wg_per_cu(cm, ncols) * num_cus() * wave_waves(cm, ncols);
+    b->waves = wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
     for (int i = 0; i < njobs; ++i) b->split_jobs += kcs[i] < tensors[i]->nb;
     {
         // unit -> job table
@@ -593,7 +670,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
         for (int i = 0; i < njobs; ++i) {
             const GemvJob &g = jobs[i];
             const p8x_tensor *t = tensor_of[g.M];
-            fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.ldx, g.ldy, g.rows, g.nks, ncols};
+            fin[i] = FinishJob{g.wpart, t->pinv, t->prmd, g.cp, g.cc, g.cv, g.x, g.y, g.ldx, g.ldy, g.rows, g.nks, ncols, act == P8X_ACT_X16 ? 1 : 0};
             if (t->dorig.empty()) continue;
             // the tensor's delta CSR and inverse permutation, read back once (set-up time)
             std::vector<int> cp(t->rows + 1);
@@ -642,7 +719,7 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
     }
     if ((rc = hip_check(hipMemset(b->work, 0, bytes), "p8x_gemv_batch_create: clear")) ||
         (rc = hip_check(hipMemcpy(b->d_jobs, jobs.data(), sizeof(GemvJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: jobs")) ||
-        (rc = hip_check(hipMemcpy(b->d_act, act.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs")) ||
+        (rc = hip_check(hipMemcpy(b->d_act, ajobs.data(), sizeof(ActJob) * njobs, hipMemcpyHostToDevice), "p8x_gemv_batch_create: act jobs")) ||
         (rc = hip_check(hipMemcpy(b->d_ablk, ablk.data(), 4 * ablk.size(), hipMemcpyHostToDevice), "p8x_gemv_batch_create: act blocks"))) {
         p8x_gemv_batch_release(b);
         return rc;
@@ -661,15 +738,15 @@ int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *str
     hipEvent_t e0 = (hipEvent_t)ev_start, e1 = (hipEvent_t)ev_stop;
     if (stage == 0) {
         const dim3 grid((b->total_blocks + 3) / 4, b->ncols);
+        auto kern = b->act == P8X_ACT_X16 ? k_act_x16_batch : k_act_q8_128_batch;
         if (e0 || e1)
-            hipExtLaunchKernelGGL(k_act_q8_128_batch, grid, dim3(256), 0, st, e0, e1, 0, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk,
-                                  b->total_blocks);
+            hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, e0, e1, 0, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
         else
-            hipLaunchKernelGGL(k_act_q8_128_batch, grid, dim3(256), 0, st, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
-        return hip_check(hipGetLastError(), "k_act_q8_128_batch launch");
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
+        return hip_check(hipGetLastError(), "batch activation prep launch");
     }
     if (stage == 1) {
-        return launch_gemv_wave(b->ncols, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
+        return launch_gemv_wave(b->ncv, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
     }
     if (stage == 2) {   // partial rows to original rows with the clamp delta
         // the delta blocks first, padded to a multiple of the XCD count so plain block 8k + x still lands on XCD x
@@ -694,6 +771,58 @@ int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *
     for (int i = 0; i < n; ++i)
         if (!y[i] || ldy[i] < (size_t)tensors[i]->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi: y %d null or short", i);
     return launch_gemv_multi(tensors, n, x, ldx, y, ldy, nullptr, (hipStream_t)stream);
+}
+
+// The shared-input calls with another activation mode: the activations are prepared once (in tensor 0's workspace:
+// every tensor rotates its input the same way) and each tensor multiplies them; Q8_1: block_q8_1 then the Q8_1 GEMV;
+// X16: both planes as two columns into the tensor's plane rows, then its combine (planes summed, then the delta).
+static int multi_act(const p8x_tensor *const *ts, int n, int act, const float *x, size_t ldx, float *const *y, const size_t *ldy, hipStream_t st) {
+    const p8x_tensor *t0 = ts[0];
+    int rc;
+    if (act == P8X_ACT_Q8_1) {
+        if ((rc = launch_act_q8_1(t0, x, 1, ldx, t0->wq81, st))) return rc;
+        for (int i = 0; i < n; ++i)
+            if ((rc = launch_gemv(ts[i], P8X_ACT_Q8_1, t0->wq81, nullptr, 1, x, ldx, y[i], ldy[i], nullptr, st))) return rc;
+        return P8X_OK;
+    }
+    if ((rc = launch_act_x16(t0, x, 1, ldx, t0->wq, t0->wd, nullptr, t0->wq + t0->K, t0->wd + t0->nsl, nullptr, 2 * t0->K, st))) return rc;
+    for (int i = 0; i < n; ++i) {
+        const p8x_tensor *t = ts[i];
+        if ((rc = launch_gemv(t, P8X_ACT_Q8_128, t0->wq, t0->wd, 2, nullptr, 0, t->wy, t->rows, nullptr, st))) return rc;
+        hipLaunchKernelGGL(k_x16_combine, dim3((t->rows + 255) / 256, 1), dim3(256), 0, st, (const float *)t->wy, t->rows, x, ldx,
+                           (const int *)t->cp, (const uint16_t *)t->cc, (const float *)t->cv, y[i], ldy[i]);
+        if ((rc = hip_check(hipGetLastError(), "k_x16_combine launch"))) return rc;
+    }
+    return P8X_OK;
+}
+
+int p8x_mul_mat_vec_multi_act(const p8x_tensor *const *tensors, int n, int act, const float *x, size_t ldx, float *const *y, const size_t *ldy,
+                              void *stream) {
+    if (act == P8X_ACT_Q8_128) return p8x_mul_mat_vec_multi(tensors, n, x, ldx, y, ldy, stream);
+    if (act != P8X_ACT_Q8_1 && act != P8X_ACT_X16) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi_act: act %d", act);
+    if (!tensors || !y || !ldy || n < 1 || n > kRgMaxJobs) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi_act: bad arguments (1..%d tensors)", kRgMaxJobs);
+    int rc;
+    if ((rc = check_shared_input(tensors, n, x, ldx, "p8x_mul_mat_vec_multi_act"))) return rc;
+    for (int i = 0; i < n; ++i)
+        if (!y[i] || ldy[i] < (size_t)tensors[i]->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_multi_act: y %d null or short", i);
+    return multi_act(tensors, n, act, x, ldx, y, ldy, (hipStream_t)stream);
+}
+
+int p8x_mul_mat_vec_glu_act(const p8x_tensor *gate, const p8x_tensor *up, int act, const float *x, size_t ldx, float *out, void *stream) {
+    if (act == P8X_ACT_Q8_128) return p8x_mul_mat_vec_glu(gate, up, x, ldx, out, stream);
+    if (act != P8X_ACT_Q8_1 && act != P8X_ACT_X16) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_glu_act: act %d", act);
+    const p8x_tensor *ts[2] = {gate, up};
+    if (!gate || !up || !out) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_glu_act: null pointer");
+    int rc;
+    if ((rc = check_shared_input(ts, 2, x, ldx, "p8x_mul_mat_vec_glu_act"))) return rc;
+    if (gate->rows != up->rows) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec_glu_act: gate has %d rows, up %d", gate->rows, up->rows);
+    // the two products in original rows in each tensor's plane rows past the x16 planes (row block 2), then the gate
+    hipStream_t st = (hipStream_t)stream;
+    float *const ys[2] = {gate->wy + 2 * (size_t)gate->rows, up->wy + 2 * (size_t)up->rows};
+    const size_t ldys[2] = {(size_t)gate->rows, (size_t)up->rows};
+    if ((rc = multi_act(ts, 2, act, x, ldx, ys, ldys, st))) return rc;
+    hipLaunchKernelGGL(k_glu_rows, dim3((gate->rows + 255) / 256), dim3(256), 0, st, (const float *)ys[0], (const float *)ys[1], gate->rows, out);
+    return hip_check(hipGetLastError(), "k_glu_rows launch");
 }
 
 int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream) {

@@ -27,7 +27,8 @@ EXPORTS = [
     "p8x_gemv_batch_run_stage_timed",
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
-    "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_decode_tiles",
+    "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_mul_mat_vec_multi_act",
+    "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_decode_tiles",
     "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
     "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_run", "p8x_step_check", "p8x_step_info",
     "p8x_step_release",
@@ -100,10 +101,12 @@ def lib():
     L.p8x_quantize_q8_1.argtypes = [vp, vp, i, sz, vp, vp]
     L.p8x_quantize_x16.argtypes = [vp, vp, i, sz, vp, vp, vp, vp, vp, vp, vp]
     L.p8x_mul_mat_vec_multi.argtypes = [vp, i, vp, sz, vp, vp, vp]
+    L.p8x_mul_mat_vec_multi_act.argtypes = [vp, i, i, vp, sz, vp, vp, vp]
     L.p8x_decode_tiles.argtypes = [vp, i, i, i, i, i, vp, sz, vp]
     L.p8x_dequantize_rows.argtypes = [vp, i, i, i, vp, sz, vp]
     L.p8x_vec_dot_rows.argtypes = [vp, i, vp, vp, i, i, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec_glu.argtypes = [vp, vp, vp, sz, vp, vp]
+    L.p8x_mul_mat_vec_glu_act.argtypes = [vp, vp, i, vp, sz, vp, vp]
     L.p8x_vec_dot.argtypes = [vp, i, vp, vp, i, vp, sz, vp, sz, vp, vp]
     L.p8x_mul_mat_vec.argtypes = [vp, vp, i, sz, vp, sz, vp]
     L.p8x_mul_mat_vec_act.argtypes = [vp, i, vp, i, sz, vp, sz, vp]
@@ -132,6 +135,7 @@ def lib():
     L.p8x_step_info.argtypes = [vp, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)]
     L.p8x_step_release.argtypes = [vp]; L.p8x_step_release.restype = None
     L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
+    L.p8x_gemv_batch_create_act.argtypes = [vp, vp, vp, vp, vp, i, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
     L.p8x_gemv_batch_run_stage_timed.argtypes = [vp, i, vp, vp, vp]
@@ -718,32 +722,40 @@ class Tensor:
         return y.to_numpy(np.float32, (N, self.rows))
 
 
-def mul_mat_vec_multi_dev(tensors, x, ys, stream=None):
-    """y_i = W_i x for tensors sharing K and input rotation, one launch (device buffers)"""
+def mul_mat_vec_multi_dev(tensors, x, ys, stream=None, act=ACT_Q8_128):
+    """y_i = W_i x for tensors sharing K and input rotation, the activation prepared once (device buffers)"""
     n = len(tensors)
     T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
     Y = (ctypes.c_void_p * n)(*[y.addr for y in ys])
     LY = (ctypes.c_size_t * n)(*[t.rows for t in tensors])
-    check(lib().p8x_mul_mat_vec_multi(T, n, _vp(x), tensors[0].K, Y, LY, stream.h if stream else None), "p8x_mul_mat_vec_multi")
+    st = stream.h if stream else None
+    if act == ACT_Q8_128:
+        check(lib().p8x_mul_mat_vec_multi(T, n, _vp(x), tensors[0].K, Y, LY, st), "p8x_mul_mat_vec_multi")
+    else:
+        check(lib().p8x_mul_mat_vec_multi_act(T, n, act, _vp(x), tensors[0].K, Y, LY, st), "p8x_mul_mat_vec_multi_act")
 
 
-def mul_mat_vec_multi(tensors, x):
+def mul_mat_vec_multi(tensors, x, act=ACT_Q8_128):
     xd = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
     ys = [DeviceBuffer(4 * t.rows) for t in tensors]
-    mul_mat_vec_multi_dev(tensors, xd, ys)
+    mul_mat_vec_multi_dev(tensors, xd, ys, act=act)
     synchronize()
     return [y.to_numpy(np.float32, (t.rows,)) for y, t in zip(ys, tensors)]
 
 
-def mul_mat_vec_glu_dev(gate, up, x, out, stream=None):
-    check(lib().p8x_mul_mat_vec_glu(gate.h, up.h, _vp(x), gate.K, _vp(out), stream.h if stream else None), "p8x_mul_mat_vec_glu")
+def mul_mat_vec_glu_dev(gate, up, x, out, stream=None, act=ACT_Q8_128):
+    st = stream.h if stream else None
+    if act == ACT_Q8_128:
+        check(lib().p8x_mul_mat_vec_glu(gate.h, up.h, _vp(x), gate.K, _vp(out), st), "p8x_mul_mat_vec_glu")
+    else:
+        check(lib().p8x_mul_mat_vec_glu_act(gate.h, up.h, act, _vp(x), gate.K, _vp(out), st), "p8x_mul_mat_vec_glu_act")
 
 
-def mul_mat_vec_glu(gate, up, x):
-    """silu(gate x) * (up x), one launch"""
+def mul_mat_vec_glu(gate, up, x, act=ACT_Q8_128):
+    """silu(gate x) * (up x)"""
     xd = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
     out = DeviceBuffer(4 * gate.rows)
-    mul_mat_vec_glu_dev(gate, up, xd, out)
+    mul_mat_vec_glu_dev(gate, up, xd, out, act=act)
     synchronize()
     return out.to_numpy(np.float32, (gate.rows,))
 
@@ -802,7 +814,7 @@ class GemvBatch:
 
     stages = 3   # activation prep, fused decode + GEMV, finishing (original rows, clamp delta)
 
-    def __init__(self, tensors, xs, ys, ncols=1):
+    def __init__(self, tensors, xs, ys, ncols=1, act=ACT_Q8_128):
         n = len(tensors)
         T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
         X = (ctypes.c_void_p * n)(*[x.addr for x in xs])
@@ -810,7 +822,7 @@ class GemvBatch:
         LX = (ctypes.c_size_t * n)(*[t.K for t in tensors])
         LY = (ctypes.c_size_t * n)(*[t.rows for t in tensors])
         self.h = ctypes.c_void_p()
-        check(lib().p8x_gemv_batch_create(T, X, LX, Y, LY, n, ncols, ctypes.byref(self.h)), "p8x_gemv_batch_create")
+        check(lib().p8x_gemv_batch_create_act(T, X, LX, Y, LY, n, ncols, act, ctypes.byref(self.h)), "p8x_gemv_batch_create")
         self._keep = (tensors, xs, ys)
 
     def info(self):

@@ -1,6 +1,8 @@
 """Several linears on one activation vector in one launch (p8x_mul_mat_vec_multi: q/k/v, gate/up) and the gated
 FFN input silu(gate x) * (up x) (p8x_mul_mat_vec_glu), against the fp64 oracle of each tensor on the same 8-bit
-activations (bar 1e-3 relative L2, asserted at 1e-5), and the rejections of tensors that cannot share an input."""
+activations (bar 1e-3 relative L2, asserted at 1e-5), and the rejections of tensors that cannot share an input.
+The same calls with the other activation modes (p8x_mul_mat_vec_multi_act / _glu_act: x16, the reference CPU path's
+default, and block_q8_1) against the oracle's GEMV in that mode, and the grouped launch with x16 activations."""
 import numpy as np
 import pytest
 
@@ -69,6 +71,70 @@ def test_glu_matches_oracle(rows, K, cp, nd):
             first = out
         else:
             assert np.array_equal(out.view(np.uint32), first.view(np.uint32)), rep
+
+
+ACTS = [(p8x.ACT_X16, "x16"), (p8x.ACT_Q8_1, "q8_1")]
+
+
+@pytest.mark.parametrize("act,name", ACTS, ids=[a[1] for a in ACTS])
+@pytest.mark.parametrize("specs", [
+    [(4096, 4096, C3, 3), (1024, 4096, C3, 1), (1024, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 2)],   # Llama q / k / v
+    [(512, 14336, MIX, 5), (256, 14336, MIX, 3)],                                           # long K: the K-split path
+], ids=["llama_qkv", "ksplit"])
+def test_multi_act_matches_oracle(specs, act, name):
+    slots = shared_input(specs, 62)
+    ts = [p8x.Tensor(s, r, K) for s, (r, K, _, _) in zip(slots, specs)]
+    x = np.random.default_rng(63).standard_normal(specs[0][1]).astype(np.float32)
+    for rep in range(2):
+        ys = p8x.mul_mat_vec_multi(ts, x, act=act)
+        for i, (s, (r, K, _, _)) in enumerate(zip(slots, specs)):
+            orc = O.Oracle(s, r, K)
+            assert rel_l2(ys[i], orc.gemv_f64(x, act=name)) < 1e-5, (rep, i)
+            # the same values as the single call in that mode
+            assert np.array_equal(ys[i].view(np.uint32), ts[i].mul_mat_vec(x, act=act)[0].view(np.uint32)), (rep, i)
+
+
+@pytest.mark.parametrize("act,name", ACTS, ids=[a[1] for a in ACTS])
+@pytest.mark.parametrize("rows,K,cp,nd", [(14336, 4096, C3, 6), (1024, 14336, MIX, 4)], ids=["llama_ffn", "ksplit"])
+def test_glu_act_matches_oracle(rows, K, cp, nd, act, name):
+    slots = shared_input([(rows, K, cp, nd), (rows, K, cp, nd + 1)], 72)
+    gate, up = p8x.Tensor(slots[0], rows, K), p8x.Tensor(slots[1], rows, K)
+    x = np.random.default_rng(73).standard_normal(K).astype(np.float32)
+    ref = silu_up(O.Oracle(slots[0], rows, K).gemv_f64(x, act=name), O.Oracle(slots[1], rows, K).gemv_f64(x, act=name))
+    first = None
+    for rep in range(2):
+        out = p8x.mul_mat_vec_glu(gate, up, x, act=act)
+        assert rel_l2(out, ref) < 1e-5, rep
+        if first is None:
+            first = out
+        else:
+            assert np.array_equal(out.view(np.uint32), first.view(np.uint32)), rep
+
+
+@pytest.mark.parametrize("ncols", [1, 2, 4])
+def test_batch_x16_matches_oracle(ncols):
+    """the grouped launch with x16 activations: a q/k/v group (one input), a long-K job (split along K by the plan)
+    and a mixed-class job, ncols columns each; every column against the oracle's x16 GEMV"""
+    specs = [(4096, 4096, C3, 3), (1024, 4096, C3, 1), (1024, 4096, (0, 0, 0, 0, 0, 0, 1, 0), 2)]
+    slots = shared_input(specs, 64) + [p8x.synth_random(66, 512, 14336, class_p=MIX, nd=4), p8x.synth_random(67, 96, 1024, class_p=(1, 1, 1, 1, 1, 1, 1, 1), nd=2)]
+    shapes = [(r, K) for r, K, _, _ in specs] + [(512, 14336), (96, 1024)]
+    ts = [p8x.Tensor(s, r, K) for s, (r, K) in zip(slots, shapes)]
+    rng = np.random.default_rng(65)
+    xh = [rng.standard_normal((ncols, K)).astype(np.float32) for _, K in shapes]
+    xs = [p8x.DeviceBuffer.from_numpy(x) for x in xh]
+    ys = [p8x.DeviceBuffer(4 * ncols * r) for r, _ in shapes]
+    b = p8x.GemvBatch(ts, xs, ys, ncols=ncols, act=p8x.ACT_X16)
+    for rep in range(2):
+        for y in ys:
+            y.fill(0xFF)
+        b.run()
+        p8x.synchronize()
+        for i, ((r, K), s) in enumerate(zip(shapes, slots)):
+            got = ys[i].to_numpy(np.float32, (ncols, r))
+            orc = O.Oracle(s, r, K)
+            for n in range(ncols):
+                assert rel_l2(got[n], orc.gemv_f64(xh[i][n], act="x16")) < 1e-5, (rep, i, n)
+    b.release()
 
 
 def test_multi_and_glu_reject_unshared_inputs():
