@@ -417,27 +417,34 @@ def measured_traffic(step_bytes, layers, mix):
     return int(prof["traffic_bytes_per_launch"]), "profiles/k_gemv_wave_llama8b_stream.json"
 
 
-def measure_dequant(steps):
+def measure_dequant(steps, copies=20):
     """dequantize-to-fp16 (original rows, Hadamard applied) of one Llama FFN weight, 14336 x 4096: a write-bound
-    kernel; bytes = packed stream read + fp16 output written"""
+    kernel; bytes = packed stream read + fp16 output written. The calls rotate over 20 device copies of the tensor
+    (303 MB, more than the 256 MB MALL) and two output buffers, so every call reads its packed weights from HBM."""
     rows, K = 14336, 4096
-    t = p8x.Tensor(p8x.synth_random(99, rows, K, nd=8), rows, K)
-    out = p8x.DeviceBuffer(2 * rows * K)
+    slot = p8x.synth_random(99, rows, K, nd=8)
+    ts = [p8x.Tensor(slot, rows, K) for _ in range(copies)]
+    outs = [p8x.DeviceBuffer(2 * rows * K) for _ in range(2)]
     stream = p8x.Stream()
-    for _ in range(40):
-        t.dequantize_dev(p8x.F16, out, stream=stream)
+    for i in range(40):
+        ts[i % copies].dequantize_dev(p8x.F16, outs[i % 2], stream=stream)
     stream.sync()
     ev = [(p8x.Event(), p8x.Event()) for _ in range(steps)]
-    for a, b in ev:
+    for i, (a, b) in enumerate(ev):
         a.record(stream)
-        t.dequantize_dev(p8x.F16, out, stream=stream)
+        ts[i % copies].dequantize_dev(p8x.F16, outs[i % 2], stream=stream)
         b.record(stream)
     stream.sync()
     ms = float(np.median([a.elapsed_ms(b) for a, b in ev]))
-    nbytes = t.stream_bytes + 2 * rows * K
-    res = {"tensor": f"{rows} x {K} -> fp16", "us_per_call": round(ms * 1e3, 1), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-           "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(nbytes)}
-    t.release()
+    nbytes = ts[0].stream_bytes + 2 * rows * K
+    res = {"tensor": f"{rows} x {K} -> fp16, {copies} copies in rotation", "us_per_call": round(ms * 1e3, 1),
+           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes": int(nbytes)}
+    for t in ts:
+        t.release()
+    for o in outs:
+        o.free()
+    stream.release()
     log("dequantize to fp16:", json.dumps(res))
     return res
 

@@ -445,9 +445,8 @@ __device__ __forceinline__ void lo_stage64(uint32_t (&P)[32], s16x2 sg) {
     }
 }
 
-struct LoNext {   // the next tile: class, flagged row and scale (its payload is in the wave's LDS copy)
-    int c, ro;
-    uint32_t s;
+struct LoNext {   // the next tile's class (its payload is in the wave's LDS copy)
+    int c;
 };
 constexpr int kLoTileWords = 512;   // a tile of classes 0-3 (nw <= 8): at most 2 KB
 
@@ -458,10 +457,7 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
     __shared__ __align__(16) float icw[kLoWaves][256];
     __shared__ __align__(16) uint32_t stg[kLoWaves][32 * kLoBandWords];   // one 32-row x 128-byte band per wave
     __shared__ __align__(16) uint32_t pay[kLoWaves][kLoTileWords];         // the next tile's payload, per wave
-    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 31, p = lane >> 5, p16 = 16 * p;
-    const int d = p16;
-    const s16x2 sg = {(short)(p ? -1 : 1), (short)(p ? -1 : 1)};
+    const int tid = threadIdx.x, lane_in = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (int i = tid; i < 512; i += kLoThreads) tab4[i] = fwht4_entry(a.a2[(i & 1) * 256 + (i >> 1)]);
     __syncthreads();
     size_t first, last;
@@ -469,13 +465,16 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
     first += w;
     if (first >= last) return;
     LoNext nx;
-    // The next tile's payload is copied into the wave's LDS buffer (direct-to-LDS loads, no registers held) and its
-    // scale and row into registers, all before this tile's output stores: stores count in vmcnt like loads, so data
-    // requested after them could only be waited for together with them.
-    auto issue = [&](size_t q) {
+    // The next tile's payload is copied into the wave's LDS buffer (direct-to-LDS loads, no registers held) before
+    // this tile's output stores, and its tile word comes through the scalar cache: stores count in vmcnt like loads,
+    // so data requested after them could only be waited for together with them. A tile's row scale and row are
+    // loaded at the start of its own iteration and first used after its decode.
+    auto issue = [&](size_t q, int lane) {
         int g, b;
         tile_of(a, q, g, b);
-        const uint32_t mt = a.M[(size_t)g * a.nb + b];
+        g = __builtin_amdgcn_readfirstlane(g);
+        b = __builtin_amdgcn_readfirstlane(b);
+        const uint32_t mt = as_const(a.M)[(size_t)g * a.nb + b];
         nx.c = (int)(mt >> 29);
         const int chunks = 16 * nw_of(nx.c);   // 16-byte pieces of the tile (both half-slices)
         if (chunks) {
@@ -484,19 +483,29 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
             for (int i = 0; i < kLoTileWords / 256; ++i)   // lanes past the tile repeat its last piece
                 __builtin_amdgcn_global_load_lds(base + 4 * min(64 * i + lane, chunks - 1), pay[w] + 256 * i, 16, 0, 0);
         }
-        nx.s = a.S[(size_t)b * a.rows + 32 * g + j];
-        nx.ro = a.prmd[32 * g + j];
     };
     int icb = -1;
-    issue(first);
+    issue(first, lane_in);
     for (size_t q = first; q < last; q += kLoWaves) {
-        const int c = nx.c, rof = nx.ro, ro = rof & 0x7FFF;
-        const float S = half_to_float((uint16_t)nx.s);
+        // lane-derived values formed per tile: held across the loop they would be spilled, and a spill reload waits
+        // for every memory operation in flight (this tile's stores included)
+        int lane = lane_in;
+        __asm__ volatile("" : "+v"(lane));
+        const int j = lane & 31, p = lane >> 5, p16 = 16 * p;
+        const int d = p16;
+        const s16x2 sg = {(short)(p ? -1 : 1), (short)(p ? -1 : 1)};
+        const int c = nx.c;
         uint32_t w0[8], w1[8];
         lo_read_any<CM>(c, w0, pay[w], j, d);
         lo_read_any<CM>(c, w1, pay[w] + nw_of(c) * 32, j, d);
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read before the next tile's copy overwrites it
-        if (q + kLoWaves < last) issue(q + kLoWaves);
+        int g, b;
+        tile_of(a, q, g, b);
+        g = __builtin_amdgcn_readfirstlane(g);
+        b = __builtin_amdgcn_readfirstlane(b);
+        const uint16_t s16 = a.S[(size_t)b * a.rows + 32 * g + j];
+        const int rof = a.prmd[32 * g + j], ro = rof & 0x7FFF;
+        if (q + kLoWaves < last) issue(q + kLoWaves, lane);
         // one half-slice at a time through its integer stages (only its 32 packed registers are being built)
         uint32_t P0[32], P1[32];
         lo_decode_any<CM>(c, w0, d, p16, tab4, P0);
@@ -507,8 +516,7 @@ __global__ __launch_bounds__(kLoThreads) __attribute__((amdgpu_waves_per_eu(4, 4
         lo_stages(P1);
         lo_stage64(P1, sg);
         __asm__ volatile("" ::: "memory");
-        int g, b;
-        tile_of(a, q, g, b);
+        const float S = half_to_float(s16);
         if (b != icb) {   // this block's ic / 16 into the wave's row (wave-local)
             const float4 c4 = reinterpret_cast<const float4 *>(a.ic + 256 * b)[lane];
             reinterpret_cast<float4 *>(icw[w])[lane] = make_float4(c4.x * 0.0625f, c4.y * 0.0625f, c4.z * 0.0625f, c4.w * 0.0625f);
