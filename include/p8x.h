@@ -196,7 +196,7 @@ int p8x_mul_mat_reserve(const p8x_tensor *t, int n_max);
  * synchronizes; rejects (P8X_ERR_UNSUPPORTED) a call whose workspace exceeds the array (512 tokens of the Llama-3.1-8B
  * FFN shapes fit). Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other
  * threads) race; calls ordered on one stream do not. Results equal p8x_mul_mat's. */
-#define P8X_NOALLOC_SCRATCH_BYTES (64 << 20)
+#define P8X_NOALLOC_SCRATCH_BYTES (96 << 20)
 int p8x_mul_mat_noalloc(const p8x_tensor *t, const void *x, int x_dtype, int N, size_t ldx, float *y, size_t ldy, void *stream);
 
 /* ---- grouped GEMV ------------------------------------------------------------------------------------- */

@@ -35,7 +35,7 @@ constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles 
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the
-// lane, 4 .. 128 across lanes (DPP row moves for distances 1-8, ds_bpermute for 16 and 32). One wave per block,
+// lane, 4 .. 128 across lanes (DPP row moves for distances 1-8, lane swaps for 16 and 32). One wave per block,
 // kMmActWaves blocks of one token per workgroup.
 constexpr int kMmActWaves = 4;
 template <typename XT>
