@@ -135,6 +135,14 @@ int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, 
 /* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1, or P8X_ACT_X16 (1..4
  * columns: both planes of each column through one GEMV, summed, then the clamp delta; the reference's CPU default) */
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
+/* Marks the start of a graph evaluation (ggml_vr_cpu_graph_begin, CPU.patch:1148). After the first call, a
+ * p8x_mul_mat_vec_act call in P8X_ACT_X16 or P8X_ACT_Q8_1 mode reuses the activation that the previous such call on
+ * the same device prepared when the input pointer, stride, column count, mode, K, input rotation and stream are the
+ * same and no p8x_graph_begin came between them (the reference's cache across consecutive mul_mats on one input,
+ * CPU.patch:1142-1143, :1171-1180). The caller keeps x unchanged between such calls, as within one graph evaluation;
+ * with reuse on, calls in these modes on one device are ordered on one stream (they share a per-GPU buffer, a fixed
+ * device array: nothing is allocated). Without any p8x_graph_begin call nothing is reused. */
+void p8x_graph_begin(void);
 /* Several linears on the same activation vector in one launch, batch 1 (the q/k/v or gate/up of a layer; ggml issues
  * one mul_mat per linear): y_i = W_i x for n = 1..4 tensors with the same K, codebook and input rotation (column
  * scales c and signs; a file encodes the linears that share an input with one c). Same arithmetic and results as n

@@ -16,8 +16,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <vector>
 
 #include "p8x_gemv.h"
@@ -866,12 +868,71 @@ int launch_act_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, i
 // virtual columns (hi of column n at 2n, lo at 2n + 1), one 8-bit-per-128 GEMV over them into the plane rows, then
 // the combine pass
 int launch_gemv_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, hipStream_t st) {
+    return launch_gemv_x16_on(t, x, ncols, ldx, y, ldy, t->wq, t->wd, false, st);
+}
+
+// the same with the planes' buffers given (q [2 ncols][K], d [2 ncols][nsl]); have: they already hold x's planes
+int launch_gemv_x16_on(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, int8_t *q, float *d, bool have,
+                       hipStream_t st) {
     int rc;
-    if ((rc = launch_act_x16(t, x, ncols, ldx, t->wq, t->wd, nullptr, t->wq + t->K, t->wd + t->nsl, nullptr, 2 * t->K, st))) return rc;
-    if ((rc = launch_gemv(t, P8X_ACT_Q8_128, t->wq, t->wd, 2 * ncols, nullptr, 0, t->wy, t->rows, nullptr, st))) return rc;
+    if (!have && (rc = launch_act_x16(t, x, ncols, ldx, q, d, nullptr, q + t->K, d + t->nsl, nullptr, 2 * t->K, st))) return rc;
+    if ((rc = launch_gemv(t, P8X_ACT_Q8_128, q, d, 2 * ncols, nullptr, 0, t->wy, t->rows, nullptr, st))) return rc;
     hipLaunchKernelGGL(k_x16_combine, dim3((t->rows + 255) / 256, ncols), dim3(256), 0, st, (const float *)t->wy, t->rows, x, ldx,
                        (const int *)t->cp, (const uint16_t *)t->cc, (const float *)t->cv, y, ldy);
     return hip_check(hipGetLastError(), "k_x16_combine launch");
+}
+
+// ---------------------------------------------------------------------------------------- prepared-activation reuse
+// The activation most recently prepared by a call in x16 or block_q8_1 mode, kept for later calls on the same input
+// within one graph evaluation (p8x_graph_begin): one file-scope device array per GPU (no allocation; its address
+// from hipGetSymbolAddress, resolved at prepare), a host-side key per device.
+static __device__ __align__(256) uint8_t act_cache[kActCacheBytes];
+
+struct ActKey {
+    unsigned epoch = 0;
+    const float *x = nullptr;
+    size_t ldx = 0;
+    int ncols = 0, act = -1, K = 0;
+    uint64_t ic_hash = 0;
+    const void *stream = nullptr;
+    bool operator==(const ActKey &o) const {
+        return epoch == o.epoch && x == o.x && ldx == o.ldx && ncols == o.ncols && act == o.act && K == o.K && ic_hash == o.ic_hash &&
+               stream == o.stream;
+    }
+};
+static std::mutex g_act_mu;
+static void *g_act_buf[kMaxActDevices];
+static ActKey g_act_key[kMaxActDevices];
+static std::atomic<unsigned> g_epoch{0};
+
+int act_cache_resolve(int device) {
+    if (device < 0 || device >= kMaxActDevices) return set_error(P8X_ERR_UNSUPPORTED, "activation cache: device %d beyond %d", device, kMaxActDevices);
+    std::lock_guard<std::mutex> lk(g_act_mu);
+    if (g_act_buf[device]) return P8X_OK;
+    int cur = 0, rc;
+    if ((rc = hip_check(hipGetDevice(&cur), "activation cache: hipGetDevice"))) return rc;
+    if (cur != device && (rc = hip_check(hipSetDevice(device), "activation cache: hipSetDevice"))) return rc;
+    void *ptr = nullptr;
+    rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(act_cache)), "activation cache: hipGetSymbolAddress");
+    if (cur != device) (void)hipSetDevice(cur);
+    if (rc) return rc;
+    g_act_buf[device] = ptr;
+    return P8X_OK;
+}
+
+void act_epoch_advance() { g_epoch.fetch_add(1u, std::memory_order_relaxed); }
+
+uint8_t *act_reuse(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, size_t bytes, hipStream_t st, bool *have) {
+    *have = false;
+    const unsigned ep = g_epoch.load(std::memory_order_relaxed);
+    if (ep == 0 || bytes > kActCacheBytes || t->device < 0 || t->device >= kMaxActDevices) return nullptr;
+    ActKey k;
+    k.epoch = ep; k.x = x; k.ldx = ldx; k.ncols = ncols; k.act = act; k.K = t->K; k.ic_hash = t->ic_hash; k.stream = st;
+    std::lock_guard<std::mutex> lk(g_act_mu);
+    if (!g_act_buf[t->device]) return nullptr;
+    *have = g_act_key[t->device] == k;
+    g_act_key[t->device] = k;
+    return static_cast<uint8_t *>(g_act_buf[t->device]);
 }
 
 int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, void *blocks, hipStream_t st) {

@@ -252,6 +252,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     memcpy(t->a2_host, a2.data(), sizeof t->a2_host);
     (void)hipGetDevice(&t->device);
     if ((rc = scratch_resolve(t->device))) { delete t; return rc; }   // set-up of the no-allocation entry point
+    if ((rc = act_cache_resolve(t->device))) { delete t; return rc; }   // and of the prepared-activation reuse
     auto fail = [&](int code) { p8x_release(t); return code; };
     auto alloc = [&](void **p, size_t bytes, const char *what) -> int {
         if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return set_error(P8X_ERR_NOMEM, "p8x_prepare: hipMalloc %s (%zu B)", what, bytes);
@@ -455,16 +456,26 @@ int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols,
     int rc;
     if (act == P8X_ACT_Q8_128)   // one launch: every task quantizes its chunk of x itself (same arithmetic as the prep)
         return launch_gemv(t, act, nullptr, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
+    // x16 and block_q8_1 prepare x in a launch of their own; within a graph evaluation (p8x_graph_begin) a later call on
+    // the same input and rotation reuses the activation the previous call prepared (CPU.patch:1171-1180)
+    bool have = false;
     if (act == P8X_ACT_Q8_1) {
-        if ((rc = launch_act_q8_1(t, x, ncols, ldx, t->wq81, st))) return rc;
-        return launch_gemv(t, act, t->wq81, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
+        uint8_t *blk = act_reuse(t, act, x, ncols, ldx, (size_t)36 * ncols * (t->K / 32), st, &have);
+        if (!blk) blk = t->wq81;
+        if (!have && (rc = launch_act_q8_1(t, x, ncols, ldx, blk, st))) return rc;
+        return launch_gemv(t, act, blk, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
     }
     if (act == P8X_ACT_X16) {
         if (2 * ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: x16 takes at most %d columns", P8X_MAX_COLS / 2);
-        return launch_gemv_x16(t, x, ncols, ldx, y, ldy, st);
+        const size_t qb = ((size_t)2 * ncols * t->K + 255) & ~(size_t)255;
+        uint8_t *c = act_reuse(t, act, x, ncols, ldx, qb + (size_t)8 * ncols * t->nsl, st, &have);
+        if (!c) return launch_gemv_x16(t, x, ncols, ldx, y, ldy, st);
+        return launch_gemv_x16_on(t, x, ncols, ldx, y, ldy, reinterpret_cast<int8_t *>(c), reinterpret_cast<float *>(c + qb), have, st);
     }
     return set_error(P8X_ERR_ARG, "p8x_mul_mat_vec: act %d", act);
 }
+
+void p8x_graph_begin(void) { act_epoch_advance(); }
 
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream) {
     return p8x_mul_mat_vec_act(t, P8X_ACT_Q8_128, x, ncols, ldx, y, ldy, stream);

@@ -81,6 +81,17 @@ int launch_act_q8_1(const p8x_tensor *t, const float *x, int ncols, size_t ldx, 
 int launch_act_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, int8_t *qh, float *dh, int32_t *sh, int8_t *ql, float *dl,
                    int32_t *sl, int qstride, hipStream_t st);
 int launch_gemv_x16(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, hipStream_t st);
+int launch_gemv_x16_on(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, int8_t *q, float *d, bool have,
+                       hipStream_t st);
+// Prepared-activation reuse within one graph evaluation (p8x_graph_begin): a device array of kActCacheBytes per GPU
+// holds the activation the last x16 / block_q8_1 call prepared; act_reuse returns it (nullptr: no reuse, use the
+// tensor's workspace) and whether it already holds this call's activation (same evaluation, input, stride, columns,
+// mode, K, rotation and stream), and records this call's key.
+constexpr size_t kActCacheBytes = 320 << 10;   // x16 and block_q8_1 activations of up to 4 / 8 columns of K <= 32768
+constexpr int kMaxActDevices = 64;
+int act_cache_resolve(int device);
+void act_epoch_advance();
+uint8_t *act_reuse(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, size_t bytes, hipStream_t st, bool *have);
 int launch_gemv_multi(const p8x_tensor *const *ts, int n, const float *x, size_t ldx, float *const *y, const size_t *ldy, float *out,
                       hipStream_t st);
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,

@@ -28,7 +28,7 @@ EXPORTS = [
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_mul_mat_vec_multi_act",
-    "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_decode_tiles",
+    "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_graph_begin", "p8x_decode_tiles",
     "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
     "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_run", "p8x_step_check", "p8x_step_info",
     "p8x_step_release",
@@ -102,6 +102,7 @@ def lib():
     L.p8x_quantize_x16.argtypes = [vp, vp, i, sz, vp, vp, vp, vp, vp, vp, vp]
     L.p8x_mul_mat_vec_multi.argtypes = [vp, i, vp, sz, vp, vp, vp]
     L.p8x_mul_mat_vec_multi_act.argtypes = [vp, i, i, vp, sz, vp, vp, vp]
+    L.p8x_graph_begin.argtypes = []; L.p8x_graph_begin.restype = None
     L.p8x_decode_tiles.argtypes = [vp, i, i, i, i, i, vp, sz, vp]
     L.p8x_dequantize_rows.argtypes = [vp, i, i, i, vp, sz, vp]
     L.p8x_vec_dot_rows.argtypes = [vp, i, vp, vp, i, i, i, vp, sz, vp, sz, vp, vp]
@@ -720,6 +721,11 @@ class Tensor:
         self.mul_mat_dev(xd, dtype, N, y)
         synchronize()
         return y.to_numpy(np.float32, (N, self.rows))
+
+
+def graph_begin():
+    """start of a graph evaluation: later x16 / block_q8_1 calls on the same input reuse its prepared activation"""
+    lib().p8x_graph_begin()
 
 
 def mul_mat_vec_multi_dev(tensors, x, ys, stream=None, act=ACT_Q8_128):

@@ -151,3 +151,45 @@ def test_multi_and_glu_reject_unshared_inputs():
     s = shared_input([(256, 1024, C3, 0), (128, 1024, C3, 0)], 83)
     with pytest.raises(p8x.P8xError, match="rows"):
         p8x.mul_mat_vec_glu(p8x.Tensor(s[0], 256, 1024), p8x.Tensor(s[1], 128, 1024), x)
+
+
+@pytest.mark.parametrize("act,name", ACTS, ids=[a[1] for a in ACTS])
+def test_prepared_activation_reuse(act, name):
+    """p8x_graph_begin: within one evaluation a call on the same input and rotation reuses the activation the previous
+    call prepared (shown by changing x in place: the next call still sees the old x), a tensor with another rotation
+    prepares its own, and the next p8x_graph_begin starts over. Every result equals the oracle on the x it used."""
+    # no clamp deltas: those read the live x (as the reference's do), and the reuse shows in the rest of the row sum
+    slots = shared_input([(1024, 4096, C3, 0), (512, 4096, C3, 0)], 90)
+    ta, tb = p8x.Tensor(slots[0], 1024, 4096), p8x.Tensor(slots[1], 512, 4096)
+    other = p8x.synth_random(92, 256, 4096, nd=1)   # its own column scales and signs
+    tc = p8x.Tensor(other, 256, 4096)
+    oa, ob, oc = O.Oracle(slots[0], 1024, 4096), O.Oracle(slots[1], 512, 4096), O.Oracle(other, 256, 4096)
+    rng = np.random.default_rng(91)
+    x1 = rng.standard_normal(4096).astype(np.float32)
+    x2 = rng.standard_normal(4096).astype(np.float32)
+    xd = p8x.DeviceBuffer.from_numpy(x1)
+    ya, yb, yc = p8x.DeviceBuffer(4 * 1024), p8x.DeviceBuffer(4 * 512), p8x.DeviceBuffer(4 * 256)
+
+    def run(t, y, n):
+        t.mul_mat_vec_dev(xd, y, act=act)
+        p8x.synchronize()
+        return y.to_numpy(np.float32, (n,)).copy()
+
+    p8x.graph_begin()
+    a1 = run(ta, ya, 1024)
+    b1 = run(tb, yb, 512)                      # reuses ta's prepared x1
+    assert rel_l2(a1, oa.gemv_f64(x1, act=name)) < 1e-5
+    assert rel_l2(b1, ob.gemv_f64(x1, act=name)) < 1e-5
+    xd.copy_from(p8x.DeviceBuffer.from_numpy(x2))   # x changed in place, no new evaluation
+    b2 = run(tb, yb, 512)
+    assert np.array_equal(b2.view(np.uint32), b1.view(np.uint32))   # still x1's activation: reused
+    c2 = run(tc, yc, 256)                      # another rotation: prepares x2 itself
+    assert rel_l2(c2, oc.gemv_f64(x2, act=name)) < 1e-5
+    p8x.graph_begin()
+    b3 = run(tb, yb, 512)                      # a new evaluation: x2
+    assert rel_l2(b3, ob.gemv_f64(x2, act=name)) < 1e-5
+    # the reused result equals a call that prepares for itself
+    p8x.graph_begin()
+    xd.copy_from(p8x.DeviceBuffer.from_numpy(x1))
+    b4 = run(tb, yb, 512)
+    assert np.array_equal(b4.view(np.uint32), b1.view(np.uint32))
