@@ -4,14 +4,16 @@
 //   W[prm[r], 256b + c] = (FWHT(v[r, 256b + :] S[b][r]) / 16)[c] ic[256b + c]   (+ clamp delta)
 // so  Y[n, prm[r]] = sum_b S[b][r] sum_i v[r, 256b + i] x'[n, 256b + i] + delta terms, with
 //   x' = FWHT(x ic) / 16 per 256-block (the GEMV's activation prep, CPU.patch:559-571, kept in fp16 here).
-// Pass 1 (k_mm_act) writes x' as fp16 [N][K]. Pass 2 (k_mm) gives each wave two 32-row tiles of a 256-row
-// workgroup tile: per 256-block it decodes the tiles in chunk order (rotated loads, p8x_lane.h) through a
-// 4 KB fp16 LDS copy of the coset table straight into MFMA operands (v S, one rounding), and multiplies them
-// with the block's x' (staged by direct-to-LDS loads) by v_mfma_f32_32x32x16_f16 with fp32 accumulation.
-// Tokens are the MFMA rows and weight rows its columns, so each lane's outputs run along 32 consecutive sorted
-// rows (coalesced stores). Sorted-row planes (one per K split) are then summed in a fixed order, un-permuted
-// and given the sparse clamp delta (CPU.patch:1193) on the original activations by k_mm_finish; a tensor
-// with identity rows and one K range writes y directly and only adds the delta.
+// Pass 1 (k_mm_act) writes x' as fp16 [N][K]. Pass 2 (k_mm): one workgroup of four waves per CU, one wave per
+// SIMD; a wave holds NTI x 2 MFMA tiles (32 NTI tokens x 64 weight rows; NTI = 8 or 4 for class-3 tensors, the
+// plan's choice, 4 for the every-class kernel). Per 256-block it decodes its two row tiles in chunk order (rotated
+// loads, p8x_lane.h) through the LDS coset table straight into MFMA operands (v S, one rounding), each B operand
+// feeding NTI v_mfma_f32_32x32x16_f16 with fp32 accumulation, software-pipelined two steps deep with counted LDS
+// waits; the block's x' goes through registers into two LDS half-block buffers, written while the other half is
+// multiplied. Tokens are the MFMA rows and weight rows its columns, so each lane's outputs run along 32 consecutive
+// sorted rows (coalesced buffer stores). Sorted-row planes (one per K split) are then summed in a fixed order,
+// un-permuted and given the sparse clamp delta (CPU.patch:1193) on the original activations by k_mm_finish; a
+// tensor with identity rows and one K range writes y directly and only adds the delta.
 //
 // Reference role: ggml_cuda_f44_mul_mat_q8 (CPU.patch:2303-2343), which instead dequantizes the tensor to a
 // Q8_0 slab (k_r51_k1, CPU.patch:2138-2235) and calls the stock integer MMQ.
@@ -31,7 +33,6 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int kMmTok = 128;      // tokens per workgroup tile (4 MFMA row tiles of 32)
 
 // ------------------------------------------------------------------------------------------------ pass 1
 // x' = FWHT(x ic) / 16 per 256-block, fp16. Lane holds 4 consecutive elements; butterflies h = 1, 2 in the
@@ -81,6 +82,9 @@ struct MmJob {
     const uint32_t *a2;     // [2][256] coset table words (A[f] + h c), h-major
     int N, rows, K, nb, ng;
     int tiles_m, tiles_n, nsplit, kper, direct;
+#ifdef P8X_TIMELINE
+    unsigned long long *tl;
+#endif
 };
 
 // offset-binary int8x4 (v + 128 per byte) -> two fp16 pairs holding 1152 + v exactly
@@ -133,10 +137,23 @@ __device__ __forceinline__ half8v decode_pair(const AnySlice<NWMAX> &ls, const u
 constexpr int kMmCmC3 = 1 << 3, kMmCmAll = 0xFE;
 constexpr int kMmMain = 3;   // the class with a branch-free path in every instantiation (the 2-bit bulk)
 __host__ __device__ constexpr int mm_nwmax(int cm) { return cm == kMmCmC3 ? 8 : 24; }
-// Waves per workgroup (each: 64 weight rows x 128 tokens, 128 accumulator registers): the class-3 kernel fits in 256
-// registers per wave and runs two waves per SIMD (one's decode overlaps the other's MFMAs) in 8-wave workgroups of
-// 512 rows that share the x' tile and the table; the every-class kernel needs more and runs one wave per SIMD.
-__host__ __device__ constexpr int mm_waves(int cm) { return cm == kMmCmC3 ? 8 : 4; }
+// Tile shape (one wave per SIMD, four per workgroup): a wave holds NTI x NTJ MFMA tiles of 32 tokens x 32 weight
+// rows, 16 NTI NTJ fp32 accumulators per lane, for all the workgroup's tokens and its own 32 NTJ rows. Each decoded
+// B operand feeds NTI MFMAs, so the decode work per MFMA falls as 1 / NTI: the class-3 kernel takes 8 x 2 (256
+// tokens x 64 rows, 256 registers, held in the accumulation registers); the every-class kernel, whose decode needs
+// more registers, 4 x 2.
+// The class-3 kernel comes in two tile shapes, 8 x 2 and 4 x 2 (256 x 256 and 128 x 256 workgroup tiles); the plan
+// picks the one with the lower modelled time (the smaller tile halves the K-split planes a shape may need).
+__host__ __device__ constexpr int mm_waves() { return 4; }
+__host__ __device__ constexpr int mm_ntj() { return 2; }
+__host__ __device__ constexpr int mm_rows() { return 32 * mm_ntj() * mm_waves(); }
+__host__ __device__ constexpr int mm_tok(int nti) { return 32 * nti; }
+// Coset table copies in LDS: the every-class kernel's decode reads 32, one per lane of a half-wave (conflict-free);
+// the class-3 kernels keep 16 (lane j reads copy j & 15: word f 32 + h 16 + (j & 15), the 32-copy byte address with
+// the lane field doubled, halved), half the table to build per workgroup, and room next to the 8 x 2 shape's two
+// 64 KB x' buffers (160 KB of LDS in all).
+__host__ __device__ constexpr int mm_tab_words(int cm) { return cm == kMmCmC3 ? kTabWords / 2 : kTabWords; }
+__host__ __device__ constexpr int mm_tab_shift(int cm) { return cm == kMmCmC3 ? 1 : 0; }
 
 template <int CM, int NWMAX>
 __device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
@@ -155,30 +172,46 @@ __device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, c
 
 // x' half-block tile in LDS: half sh of block b holds, per token, columns 128 kh + 64 sh + 8 c8 + (0..7) as
 // chunk c = 8 kh + c8 at position c ^ (t & 15) of the token's 256-byte row, so the 16-byte operand reads of
-// 16 consecutive tokens cover all 64 banks once.
-constexpr int kMmXsHalfs = kMmTok * 128;
+// 16 consecutive tokens cover all 64 banks once. TOK tokens: TOK x 128 halves per buffer.
 
-// Stage half sh of block b: with IPW = 128 / (4 NWAVES) instructions per wave, instruction i of wave w fills token
-// rows 4 (IPW w + i) + (0..3); lane l lands at the instruction's LDS base + 16 l (direct-to-LDS), i.e. row + (l >> 4),
-// position l & 15.
-template <int NWAVES>
-__device__ __forceinline__ void mm_stage(const MmJob &J, _Float16 *xb, int tok0, int b, int sh, int w, int lane) {
-    constexpr int IPW = kMmTok / (4 * NWAVES);   // instructions per wave
+// Stage half sh of block b in two parts: mm_fetch loads it into registers, mm_put writes it to LDS. With IPW =
+// TOK / (4 NWAVES) rows of four tokens per wave, row i of wave w holds token rows 4 (IPW w + i) + (0..3); lane l
+// carries token row + (l >> 4), position l & 15 and writes it at the row's LDS base + 16 l bytes. (Direct-to-LDS loads
+// would save the registers, but while one may be in flight the compiler waits for every LDS read to finish
+// before using any, which serializes the operand reads of consecutive MFMA steps.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int NWAVES, int TOK>
+struct XStage {
+    static constexpr int IPW = TOK / (4 * NWAVES);
+    u32x4 v[IPW];   // a native vector type: kept in registers (HIP's uint4 struct made the array a stack object)
+};
+
+template <int NWAVES, int TOK>
+__device__ __forceinline__ void mm_fetch(const MmJob &J, XStage<NWAVES, TOK> &xs, int tok0, int b, int sh, int w, int lane) {
+    constexpr int IPW = XStage<NWAVES, TOK>::IPW;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
         const int row = 4 * (IPW * w + i), t = row + (lane >> 4);
         const int ts = min(tok0 + t, J.N - 1);   // rows past N repeat the last token (never written out)
         const int c = (lane & 15) ^ (t & 15);
-        const _Float16 *src = J.xr + (size_t)ts * J.K + 256 * b + 128 * (c >> 3) + 64 * sh + 8 * (c & 7);
-        __builtin_amdgcn_global_load_lds(src, xb + row * 128, 16, 0, 0);
+        xs.v[i] = *reinterpret_cast<const u32x4 *>(J.xr + (size_t)ts * J.K + 256 * b + 128 * (c >> 3) + 64 * sh + 8 * (c & 7));
     }
+    __asm__ volatile("" ::: "memory");   // issued here, ahead of the products they overlap
 }
 
-// issue the raw payload loads of the wave's two tiles at block b
-template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_issue(const MmJob &J, AnyRaw<NWMAX> (&raw)[2], int (&cl)[2], const int (&g)[2], int b, int j, int kh) {
+// rows I0 .. I1 - 1 of the wave's share
+template <int NWAVES, int TOK, int I0 = 0, int I1 = XStage<NWAVES, TOK>::IPW>
+__device__ __forceinline__ void mm_put(const XStage<NWAVES, TOK> &xs, _Float16 *xb, int w, int lane) {
+    constexpr int IPW = XStage<NWAVES, TOK>::IPW;
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
+    for (int i = I0; i < I1; ++i) *reinterpret_cast<u32x4 *>(xb + 4 * (IPW * w + i) * 128 + 8 * lane) = xs.v[i];
+}
+
+// issue the raw payload loads of the wave's NTJ tiles at block b
+template <int CM, int NWMAX, int NTJ>
+__device__ __forceinline__ void mm_issue(const MmJob &J, AnyRaw<NWMAX> (&raw)[NTJ], int (&cl)[NTJ], const int (&g)[NTJ], int b, int j, int kh) {
+#pragma unroll
+    for (int tj = 0; tj < NTJ; ++tj) {
         cl[tj] = 0;
         if constexpr (CM == kMmCmC3) {   // the class-3-only path decodes every tile; zero weights through S = 0
 #pragma unroll
@@ -194,99 +227,148 @@ __device__ __forceinline__ void mm_issue(const MmJob &J, AnyRaw<NWMAX> (&raw)[2]
 }
 
 // decode the raw words into the slices the products read (after the loads have landed)
-template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const AnyRaw<NWMAX> (&raw)[2]) {
+template <int CM, int NWMAX, int NTJ>
+__device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[NTJ], const int (&cl)[NTJ], const AnyRaw<NWMAX> (&raw)[NTJ]) {
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
+    for (int tj = 0; tj < NTJ; ++tj) {
         if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj]);   // zero raw words, S = 0: zero weights
         else prepare_any<CM>(ls[tj], cl[tj], raw[tj]);
     }
 }
 
-// The 8 MFMA steps of one half-block (steps s = 8 sh .. 8 sh + 7) from x' buffer xb.
-template <int CM, int NWMAX>
-__device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const AnySlice<NWMAX> (&ls)[2], const int (&cl)[2], const uint32_t *tab,
-                                        uint32_t bankbytes, int sh, int j, int kh, float16v (&acc)[4][2]) {
-    auto read_a = [&](int s8, half8v (&A)[4]) {
+// The 8 MFMA steps of one half-block (steps s = 8 sh .. 8 sh + 7) from x' buffer xb; the staged x' of the next
+// half-block goes to the other buffer xn during them (no wave reads xn between the barriers around this call).
+template <int CM, int NWMAX, int NTI, int NTJ, int NWAVES, int TOK>
+__device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const AnySlice<NWMAX> (&ls)[NTJ], const int (&cl)[NTJ], const uint32_t *tab,
+                                        uint32_t bankbytes, int sh, int j, int kh, float16v (&acc)[NTI][NTJ],
+                                        const XStage<NWAVES, TOK> &xq, _Float16 *xn, int w, int lane) {
+    constexpr int IPW = XStage<NWAVES, TOK>::IPW, PPS = IPW / 4;   // x' rows written per step, in the last 4 steps
+    static_assert(IPW % 4 == 0, "x' rows per wave split over 4 steps");
+    auto read_a = [&](int s8, half8v (&A)[NTI]) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
+        for (int ti = 0; ti < NTI; ++ti)
             A[ti] = *reinterpret_cast<const half8v *>(xb + (32 * ti + j) * 128 + 8 * ((8 * kh + s8) ^ (j & 15)));
     };
-    if (CM == kMmCmC3 || (cl[0] == kMmMain && cl[1] == kMmMain)) {
-        // software-pipelined by one step: x' operands and table words of step s + 1 are read before the 8 MFMAs of
-        // step s, which then wait only for the fp16 conversion of their B operands
-        const half2v s2[2] = {{__builtin_bit_cast(_Float16, (uint16_t)ls[0].s), __builtin_bit_cast(_Float16, (uint16_t)ls[0].s)},
-                              {__builtin_bit_cast(_Float16, (uint16_t)ls[1].s), __builtin_bit_cast(_Float16, (uint16_t)ls[1].s)}};
-        auto lookups = [&](int s, uint32_t (&W)[2][2][3]) {
+    bool main_only = true;
+    if constexpr (CM != kMmCmC3) {
 #pragma unroll
-            for (int tj = 0; tj < 2; ++tj) {
+        for (int tj = 0; tj < NTJ; ++tj) main_only = main_only && cl[tj] == kMmMain;
+    }
+    if (main_only) {
+        // Software-pipelined in two depths. While the NTI NTJ MFMAs of step s run, the first half of them interleaved
+        // with the decode of step s + 1's B operands (table words read one step earlier), the second half with the
+        // x' reads of step s + 1 and the table reads of step s + 2. At most NTI + 2 NTJ = 12 LDS reads are in
+        // flight, within what the wait counter tracks, so each wait is counted: the MFMAs wait only for their own
+        // x' operands.
+        half2v s2[NTJ];
+#pragma unroll
+        for (int tj = 0; tj < NTJ; ++tj) s2[tj] = half2v{__builtin_bit_cast(_Float16, (uint16_t)ls[tj].s), __builtin_bit_cast(_Float16, (uint16_t)ls[tj].s)};
+        auto lookups = [&](int s, uint32_t (&W)[NTJ][2][3]) {
+#pragma unroll
+            for (int tj = 0; tj < NTJ; ++tj) {
                 const uint32_t hq = coset_bytes(ls[tj].H, bankbytes, s >> 1);
-                lookup_chunk<kMmMain>(ls[tj], tab, 2 * s, hq, W[tj][0]);
-                lookup_chunk<kMmMain>(ls[tj], tab, 2 * s + 1, hq, W[tj][1]);
+                W[tj][0][0] = lds_word(tab, ls[tj].template addr<kMmMain, 0>(2 * s, hq) >> mm_tab_shift(CM));
+                W[tj][1][0] = lds_word(tab, ls[tj].template addr<kMmMain, 0>(2 * s + 1, hq) >> mm_tab_shift(CM));
             }
         };
-        half8v A[4];
-        uint32_t W[2][2][3];
-        read_a(0, A);
-        lookups(8 * sh, W);
+        auto decode = [&](const uint32_t (&W)[NTJ][2][3], half8v (&B)[NTJ]) {
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-            half8v An[4];
-            uint32_t Wn[2][2][3];
-            if (s8 < 7) { read_a(s8 + 1, An); lookups(8 * sh + s8 + 1, Wn); }
-            half8v B[2];
-#pragma unroll
-            for (int tj = 0; tj < 2; ++tj) {
+            for (int tj = 0; tj < NTJ; ++tj) {
                 half2v a, b, c, d;
                 weights_chunk<kMmMain>(W[tj][0], s2[tj], a, b);
                 weights_chunk<kMmMain>(W[tj][1], s2[tj], c, d);
                 B[tj][0] = a.x; B[tj][1] = a.y; B[tj][2] = b.x; B[tj][3] = b.y;
                 B[tj][4] = c.x; B[tj][5] = c.y; B[tj][6] = d.x; B[tj][7] = d.y;
             }
+        };
+        static_assert(nstage_of(kMmMain) == 1, "the main path reads one table word per chunk");
+        half8v A[NTI], B[NTJ];
+        uint32_t W[NTJ][2][3];
+        lookups(8 * sh, W);
+        decode(W, B);
+        read_a(0, A);
+        lookups(8 * sh + 1, W);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ti = 0; ti < 4; ++ti)
+        for (int s8 = 0; s8 < 8; ++s8) {
+            half8v An[NTI], Bn[NTJ];
+            uint32_t Wn[NTJ][2][3];
+            if (s8 < 7) decode(W, Bn);
+            if (s8 < 7) read_a(s8 + 1, An);
+            if (s8 < 6) lookups(8 * sh + s8 + 2, Wn);
 #pragma unroll
-                for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
+            for (int tj = 0; tj < NTJ; ++tj)
+#pragma unroll
+                for (int ti = 0; ti < NTI; ++ti) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
+            if (s8 >= 4) {
+                // the next half-block's x' rows (loaded since the start of this half-block) go to the other buffer
+#pragma unroll
+                for (int i = 0; i < PPS; ++i)
+                    *reinterpret_cast<u32x4 *>(xn + 4 * (IPW * w + (s8 - 4) * PPS + i) * 128 + 8 * lane) = xq.v[(s8 - 4) * PPS + i];
+            }
             if (s8 < 7) {
+                constexpr int HM = NTI * NTJ / 2;                          // MFMAs per half of the step
+                constexpr int DV = (12 * NTJ + HM - 1) / HM;               // decode VALU per MFMA
+                constexpr int RD = (NTI + 2 * NTJ + HM - 1) / HM;          // LDS reads per MFMA
 #pragma unroll
-                for (int ti = 0; ti < 4; ++ti) A[ti] = An[ti];
+                for (int i = 0; i < HM; ++i) {   // decode
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, DV, 0);
+                }
 #pragma unroll
-                for (int tj = 0; tj < 2; ++tj)
+                for (int i = 0; i < HM; ++i) {   // x' and table reads, table addresses, x' writes
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    if (s8 >= 4 && i < PPS) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                }
+#pragma unroll
+                for (int ti = 0; ti < NTI; ++ti) A[ti] = An[ti];
+#pragma unroll
+                for (int tj = 0; tj < NTJ; ++tj) {
+                    B[tj] = Bn[tj];
 #pragma unroll
                     for (int u = 0; u < 2; ++u)
 #pragma unroll
                         for (int q = 0; q < 3; ++q) W[tj][u][q] = Wn[tj][u][q];
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) {
-            half8v A[4], B[2];
+            half8v A[NTI], B[NTJ];
             read_a(s8, A);
 #pragma unroll
-            for (int tj = 0; tj < 2; ++tj) B[tj] = decode_any<CM>(ls[tj], cl[tj], tab, bankbytes, 8 * sh + s8);
+            for (int tj = 0; tj < NTJ; ++tj) B[tj] = decode_any<CM>(ls[tj], cl[tj], tab, bankbytes, 8 * sh + s8);
 #pragma unroll
-            for (int ti = 0; ti < 4; ++ti)
+            for (int ti = 0; ti < NTI; ++ti)
 #pragma unroll
-                for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
+                for (int tj = 0; tj < NTJ; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
         }
+        mm_put<NWAVES, TOK>(xq, xn, w, lane);
     }
 }
 
-// One workgroup per CU of mm_waves(CM) waves (each: 64 weight rows x 128 tokens, 128 accumulator registers). K
-// advances by half-blocks; the x' of the next half-block and the next block's payload are in flight while the current
-// half-block is multiplied.
-template <int CM>
-__global__ __launch_bounds__(64 * mm_waves(CM)) __attribute__((amdgpu_waves_per_eu(mm_waves(CM) / 4, mm_waves(CM) / 4)))
+// One workgroup per CU of mm_waves() waves, one per SIMD (each: 32 NTJ weight rows x all 32 NTI tokens of the
+// workgroup tile). K advances by half-blocks; the x' of the next half-block and the next block's payload are in flight
+// while the current half-block is multiplied.
+template <int CM, int NTI>
+__global__ __launch_bounds__(64 * mm_waves()) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_mm(MmJob J) {
-    constexpr int NWMAX = mm_nwmax(CM), NWAVES = mm_waves(CM), kMmThreads = 64 * NWAVES, kMmRows = 64 * NWAVES;
-    __shared__ uint32_t tab[kTabWords];   // first: LDS address 0, replicated coset table (bytes offset by 128)
-    __shared__ __attribute__((aligned(16))) _Float16 xs0[kMmXsHalfs];   // half 0 of a block
-    __shared__ __attribute__((aligned(16))) _Float16 xs1[kMmXsHalfs];   // half 1
+    constexpr int NWMAX = mm_nwmax(CM), NWAVES = mm_waves(), NTJ = mm_ntj(), kMmThreads = 64 * NWAVES;
+    constexpr int kMmRows = mm_rows(), TOK = mm_tok(NTI), TABW = mm_tab_words(CM);
+    __shared__ uint32_t tab[TABW];   // first: LDS address 0, replicated coset table (bytes offset by 128)
+    __shared__ __attribute__((aligned(16))) _Float16 xs0[TOK * 128];   // half 0 of a block
+    __shared__ __attribute__((aligned(16))) _Float16 xs1[TOK * 128];   // half 1
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, kh = lane >> 5;
-    const uint32_t bankbytes = (uint32_t)(j << 2) * 0x01010101u;
+    // lane field of the table byte addresses: the lane's copy, at the 32-copy spacing (halved on read for 16 copies)
+    const uint32_t bankbytes = (uint32_t)((TABW == kTabWords ? j : (j & 15) << 1) << 2) * 0x01010101u;
+#ifdef P8X_TIMELINE
+    const unsigned long long tl_start = __builtin_amdgcn_s_memrealtime();
+#endif
     // Workgroups are dealt to the 8 XCDs round-robin (XCD = blockIdx % 8). Linear tile order is x'-slice-major
     // (slice = token tile x K split, then row tile), and each XCD takes one contiguous run of it, so the
     // workgroups that read one x' slice share an L2.
@@ -295,66 +377,123 @@ void k_mm(MmJob J) {
     if (lin >= J.tiles_m * J.tiles_n * J.nsplit) return;
     const int tm = lin % J.tiles_m, slice = lin / J.tiles_m;
     const int ks = slice % J.nsplit, tn = slice / J.nsplit;
+    const int tok0 = tn * TOK;
+    const int b0 = ks * J.kper, b1 = min(J.nb, b0 + J.kper);
+    int g[NTJ];
+#pragma unroll
+    for (int tj = 0; tj < NTJ; ++tj) g[tj] = (tm * kMmRows) / 32 + NTJ * w + tj;
+    float16v acc[NTI][NTJ];
+#pragma unroll
+    for (int ti = 0; ti < NTI; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < NTJ; ++tj) acc[ti][tj] = float16v{};
+    AnySlice<NWMAX> ls[NTJ];
+    AnyRaw<NWMAX> raw[NTJ];
+    int cl[NTJ], ncl[NTJ];
+    // the first half-block and payload loads go out first; the table is built while they are in flight
+    XStage<NWAVES, TOK> xq;
+    mm_fetch<NWAVES, TOK>(J, xq, tok0, b0, 0, w, lane);
+    mm_issue<CM>(J, raw, cl, g, b0, j, kh);
     {
+        // word (f, h, c) = A[f] + h c bytes (offset by 128) at f (TABW / 256) + h (TABW / 512) + c, c < TABW / 512
+        constexpr int CPS = TABW / 512;   // copies
         uint4 *t4 = reinterpret_cast<uint4 *>(tab);
-        for (int i = tid; i < kTabWords / 4; i += kMmThreads) {
-            const int f = i >> 4, h = (i >> 3) & 1;
+        for (int i = tid; i < TABW / 4; i += kMmThreads) {
+            const int f = (4 * i) / (2 * CPS), h = ((4 * i) / CPS) & 1;
             const uint32_t v = J.a2[h * 256 + f] ^ 0x80808080u;
             t4[i] = make_uint4(v, v, v, v);
         }
     }
-    const int tok0 = tn * kMmTok;
-    const int b0 = ks * J.kper, b1 = min(J.nb, b0 + J.kper);
-    int g[2];
-    g[0] = (tm * kMmRows) / 32 + 2 * w;
-    g[1] = g[0] + 1;
-    float16v acc[4][2];
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = float16v{};
-    AnySlice<NWMAX> ls[2];
-    AnyRaw<NWMAX> raw[2];
-    int cl[2], ncl[2];
-    mm_stage<NWAVES>(J, xs0, tok0, b0, 0, w, lane);
-    mm_issue<CM>(J, raw, cl, g, b0, j, kh);
-    __builtin_amdgcn_s_waitcnt(0);
+    mm_put<NWAVES, TOK>(xq, xs0, w, lane);
     mm_prepare<CM>(ls, cl, raw);
     __syncthreads();   // table and the first half-block's x' are in LDS
-    // The two x' buffers are separate LDS objects named statically (half 0 always in xs0, half 1 in xs1), so
-    // the compiler can tell the operand reads from the in-flight direct-to-LDS writes and does not wait for them.
+#ifdef P8X_TIMELINE
+    // Timeline build: s_memrealtime (100 MHz) per wave at its start, after the prologue, summed over the
+    // half-blocks (products; x' write and barrier), at the loop's end and after its stores have completed:
+    // record [8] = {lin << 32 | wave << 16 | blocks, start, prologue, products, barriers, loop end, end, grid}
+    unsigned long long tl_t = __builtin_amdgcn_s_memrealtime(), tl_cmp = 0, tl_bar = 0;
+    const unsigned long long tl_pro = tl_t;
+#define P8X_MM_LAP(sum) do { const unsigned long long t_ = __builtin_amdgcn_s_memrealtime(); sum += t_ - tl_t; tl_t = t_; } while (0)
+#else
+#define P8X_MM_LAP(sum) do {} while (0)
+#endif
+    // Half h + 1 is fetched into registers while half h is multiplied, then written to the other buffer (which no
+    // wave reads since the last barrier); the next block's payload stays in flight through the second half.
+    // The loads are unconditional (the last block's successor is the last block again, never used), so the wait
+    // counts the compiler derives for the x' writes inside mm_half are exact.
     for (int b = b0; b < b1; ++b) {
-        mm_stage<NWAVES>(J, xs1, tok0, b, 1, w, lane);
-        if (b + 1 < b1) mm_issue<CM>(J, raw, ncl, g, b + 1, j, kh);
-        mm_half<CM>(xs0, ls, cl, tab, bankbytes, 0, j, kh, acc);
-        __builtin_amdgcn_s_waitcnt(0);   // half 1 of b landed (and the next block's payload)
+        const int bn = min(b + 1, b1 - 1);
+        mm_fetch<NWAVES, TOK>(J, xq, tok0, b, 1, w, lane);
+        mm_issue<CM>(J, raw, ncl, g, bn, j, kh);
+        mm_half<CM>(xs0, ls, cl, tab, bankbytes, 0, j, kh, acc, xq, xs1, w, lane);
+        P8X_MM_LAP(tl_cmp);
         __syncthreads();
-        if (b + 1 < b1) mm_stage<NWAVES>(J, xs0, tok0, b + 1, 0, w, lane);
-        mm_half<CM>(xs1, ls, cl, tab, bankbytes, 1, j, kh, acc);
-        __builtin_amdgcn_s_waitcnt(0);   // half 0 of b + 1 landed
-        if (b + 1 < b1) {
-            cl[0] = ncl[0]; cl[1] = ncl[1];
-            mm_prepare<CM>(ls, cl, raw);
-        }
+        P8X_MM_LAP(tl_bar);
+        mm_fetch<NWAVES, TOK>(J, xq, tok0, bn, 0, w, lane);
+        mm_half<CM>(xs1, ls, cl, tab, bankbytes, 1, j, kh, acc, xq, xs0, w, lane);
+        P8X_MM_LAP(tl_cmp);
+#pragma unroll
+        for (int tj = 0; tj < NTJ; ++tj) cl[tj] = ncl[tj];
+        mm_prepare<CM>(ls, cl, raw);
         __syncthreads();
+        P8X_MM_LAP(tl_bar);
     }
+#ifdef P8X_TIMELINE
+    const unsigned long long tl_loop = tl_t;
+#endif
     // acc[ti][tj] lane l, reg q: token 32 ti + 8 (q >> 2) + 4 kh + (q & 3), sorted row 32 g[tj] + j: 32 lanes
-    // store 32 consecutive rows of one token
+    // store 32 consecutive rows of one token (planes, or y with identity rows; scattered 4-byte stores to the
+    // original rows measured 5x slower than a plane and k_mm_finish)
     float *dst = J.direct ? J.y : J.ws + (size_t)ks * J.N * J.rows;
     const size_t ld = J.direct ? (size_t)J.ldy : (size_t)J.rows;
+    if ((size_t)J.N * ld * 4 < 0xFFFFFFFFull) {
+        // Buffer stores with 32-bit offsets, no branches. In a tile that runs past N, a token at or past N is
+        // stored to token N - 1, whose value it holds bit for bit (its x' row repeats row N - 1, and each MFMA
+        // output element is computed alike), so every store stays inside the N ld floats of the resource.
+        const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(dst, (uint32_t)((size_t)J.N * ld * 4));
+        const uint32_t ld4 = (uint32_t)ld * 4u;
+        const bool whole = tok0 + TOK <= J.N;
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
-        if (g[tj] >= J.ng) continue;
-        const int r = 32 * g[tj] + j;
+        for (int tj = 0; tj < NTJ; ++tj) {
+            if (g[tj] >= J.ng) continue;
+            const uint32_t r4 = (uint32_t)(32 * g[tj] + j) * 4u;
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
+            for (int ti = 0; ti < NTI; ++ti)
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int tok = tok0 + 32 * ti + 8 * (q >> 2) + 4 * kh + (q & 3);
-                if (tok < J.N) dst[(size_t)tok * ld + r] = acc[ti][tj][q];
-            }
+                for (int q = 0; q < 16; ++q) {
+                    const int tok = tok0 + 32 * ti + 8 * (q >> 2) + 4 * kh + (q & 3);
+                    const uint32_t off = (uint32_t)(whole ? tok : min(tok, J.N - 1)) * ld4 + r4;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[ti][tj][q]), rd, off, 0, 0);
+                }
+        }
+    } else {
+#pragma unroll
+        for (int tj = 0; tj < NTJ; ++tj) {
+            if (g[tj] >= J.ng) continue;
+            const int r = 32 * g[tj] + j;
+#pragma unroll
+            for (int ti = 0; ti < NTI; ++ti)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int tok = tok0 + 32 * ti + 8 * (q >> 2) + 4 * kh + (q & 3);
+                    if (tok < J.N) dst[(size_t)tok * ld + r] = acc[ti][tj][q];
+                }
+        }
     }
+#ifdef P8X_TIMELINE
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const unsigned long long tl_end = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && (unsigned)(4 * blockIdx.x + w) < kTimelineRecords) {
+        const unsigned slot = __hip_atomic_fetch_add((unsigned *)(J.tl + kTimelineRecords * 8), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (slot < kTimelineRecords) {
+            unsigned long long *o = J.tl + (size_t)slot * 8;
+            o[0] = ((unsigned long long)lin << 32) | ((unsigned)w << 16) | (unsigned)(b1 - b0);
+            o[1] = tl_start; o[2] = tl_pro; o[3] = tl_cmp; o[4] = tl_bar; o[5] = tl_loop; o[6] = tl_end; o[7] = gridDim.x;
+        }
+    }
+#endif
 }
+#undef P8X_MM_LAP
 
 // y[n][ro] = sum over K splits (split order) of the sorted planes at row pinv[ro], plus the clamp delta on the
 // original activations. One workgroup per token: the planes are read coalesced into LDS (sorted order), the
@@ -417,40 +556,44 @@ static int grow(void **p, size_t *have, size_t need, const char *what) {
 }
 
 struct MmPlan {
+    int nti;   // token tiles per wave: the workgroup tile is 256 rows x 32 nti tokens
     int tiles_m, tiles_n, nsplit, kper;
 };
 
-// One workgroup per CU. Estimated time = rounds of workgroups x blocks per workgroup x the time of one block of a
-// workgroup tile (a relative model: 256 x 128 for the every-class kernel, 512 x 128 at two waves per SIMD for the
-// class-3 one) + the sorted-plane traffic of k_mm_finish (written once, read once, ~5 TB/s) when planes are used (K
-// split, or rows to un-permute).
+// One workgroup per CU. Estimated time = rounds of workgroups x (the measured prologue + blocks per workgroup x the
+// measured time of one K block of a workgroup tile of the shape) + when planes are used (K split, or rows to
+// un-permute) their traffic (written by k_mm, read by k_mm_finish at ~5 TB/s) and k_mm_finish's launch.
 static bool mm_only_c3(const p8x_tensor *t) {
     for (int c = 1; c < 8; ++c) if (c != 3 && t->class_tiles[c]) return false;
     return true;
 }
 
 static MmPlan mm_plan(const p8x_tensor *t, int N) {
-    MmPlan p;
     const bool c3 = mm_only_c3(t);
-    const int rows_tile = 64 * mm_waves(c3 ? kMmCmC3 : kMmCmAll);
-    const double block_us = c3 ? 4.9 : 3.4;   // one K block of one workgroup tile
-    p.tiles_m = (t->rows + rows_tile - 1) / rows_tile;
-    p.tiles_n = (N + kMmTok - 1) / kMmTok;
-    const long base = (long)p.tiles_m * p.tiles_n, slots = num_cus();
-    const double plane_us = 2.0 * 4.0 * N * t->rows / 5e6;
+    const long slots = num_cus();
+    const double plane_us = 2.0 * 4.0 * N * t->rows / 5e6, finish_us = 3.0;
     // a split's planes stay within what the no-allocation entry point holds next to x', so that it runs the same
     // plan (and returns the same bits) as p8x_mul_mat wherever it runs at all
     const size_t xb = ((size_t)N * t->K * sizeof(_Float16) + 255) & ~(size_t)255;
     const size_t cap = xb < (size_t)P8X_NOALLOC_SCRATCH_BYTES ? (size_t)P8X_NOALLOC_SCRATCH_BYTES - xb : 0;
-    double best = -1.0;
-    p.nsplit = 1; p.kper = t->nb;
-    for (int ns = 1; ns <= std::min(t->nb, 16); ++ns) {
-        const int kper = (t->nb + ns - 1) / ns, nsr = (t->nb + kper - 1) / kper;
-        if (nsr > 1 && (size_t)nsr * N * t->rows * 4 > cap) continue;
-        const double cost = (double)((base * nsr + slots - 1) / slots) * kper * block_us + ((nsr > 1 || !t->prm_identity) ? nsr * plane_us : 0.0);
-        if (best < 0 || cost < best) { best = cost; p.nsplit = nsr; p.kper = kper; }
+    MmPlan best{4, 0, 0, 1, t->nb};
+    double best_cost = -1.0;
+    for (int nti = 8; nti >= 4; nti -= 4) {
+        if (nti == 8 && !c3) continue;   // the every-class decode needs the registers of the 4 x 2 shape
+        // one K block of one workgroup tile and the prologue, us (class 3: 256 x 256 and 256 x 128 measured; every
+        // class: 256 x 128)
+        const double block_us = nti == 8 ? 7.5 : c3 ? 3.9 : 4.4, pro_us = c3 ? 3.7 : 5.0;
+        const int tiles_m = (t->rows + mm_rows() - 1) / mm_rows(), tiles_n = (N + mm_tok(nti) - 1) / mm_tok(nti);
+        const long base = (long)tiles_m * tiles_n;
+        for (int ns = 1; ns <= std::min(t->nb, 16); ++ns) {
+            const int kper = (t->nb + ns - 1) / ns, nsr = (t->nb + kper - 1) / kper;
+            if (nsr > 1 && (size_t)nsr * N * t->rows * 4 > cap) continue;
+            const bool planes = nsr > 1 || !t->prm_identity;
+            const double cost = (double)((base * nsr + slots - 1) / slots) * (pro_us + kper * block_us) + (planes ? nsr * plane_us + finish_us : 0.0);
+            if (best_cost < 0 || cost < best_cost) { best_cost = cost; best = MmPlan{nti, tiles_m, tiles_n, nsr, kper}; }
+        }
     }
-    return p;
+    return best;
 }
 
 int reserve_mul_mat(const p8x_tensor *t, int n_max) {
@@ -509,9 +652,13 @@ static int launch_mul_mat_ws(const p8x_tensor *t, const void *x, int x_dtype, in
     J.y = y; J.ldy = (unsigned)ldy; J.ws = wmm; J.a2 = t->a2;
     J.N = N; J.rows = t->rows; J.K = t->K; J.nb = t->nb; J.ng = t->ng;
     J.tiles_m = p.tiles_m; J.tiles_n = p.tiles_n; J.nsplit = p.nsplit; J.kper = p.kper; J.direct = direct;
+#ifdef P8X_TIMELINE
+    J.tl = timeline_buf();
+#endif
     const int grid = ((p.tiles_m * p.tiles_n * p.nsplit + kXcds - 1) / kXcds) * kXcds;
-    if (mm_only_c3(t)) hipLaunchKernelGGL(k_mm<kMmCmC3>, dim3(grid), dim3(64 * mm_waves(kMmCmC3)), 0, st, J);
-    else hipLaunchKernelGGL(k_mm<kMmCmAll>, dim3(grid), dim3(64 * mm_waves(kMmCmAll)), 0, st, J);
+    if (!mm_only_c3(t)) hipLaunchKernelGGL((k_mm<kMmCmAll, 4>), dim3(grid), dim3(64 * mm_waves()), 0, st, J);
+    else if (p.nti == 8) hipLaunchKernelGGL((k_mm<kMmCmC3, 8>), dim3(grid), dim3(64 * mm_waves()), 0, st, J);
+    else hipLaunchKernelGGL((k_mm<kMmCmC3, 4>), dim3(grid), dim3(64 * mm_waves()), 0, st, J);
     if ((rc = hip_check(hipGetLastError(), "k_mm launch"))) return rc;
     if (!direct) {
         const size_t lds = 4 * (size_t)t->rows;   // rows < 32768: at most 128 KB

@@ -585,8 +585,6 @@ __device__ __forceinline__ void rg_quantize(int nbk, RgSmem<NCOL> &sm, const Blo
 // (it waits for them there, which the product kernel does not), after the table and the quantization, after the
 // barrier, after its tiles and at its end, into records [kTimelineRecords][8] = {block << 32 | grid, 7 stamps}.
 #ifdef P8X_TIMELINE
-constexpr unsigned kTimelineRecords = 65536;
-unsigned long long *timeline_buf();   // device: the records, then the record counter
 #define P8X_STAMP(k) do { if (threadIdx.x == 0) stamp[k] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define P8X_STAMP(k) do {} while (0)

@@ -114,4 +114,11 @@ int num_cus();
 // delta, c16, prm, pinv, signs, trailer
 void side_offsets(size_t n, size_t rows, size_t K, size_t nd, size_t off[6]);
 
+#ifdef P8X_TIMELINE
+// Timeline build only (make timeline): per-workgroup / per-wave s_memrealtime records written by the instrumented
+// kernels, [kTimelineRecords][8] words followed by the record counter.
+constexpr unsigned kTimelineRecords = 65536;
+unsigned long long *timeline_buf();
+#endif
+
 }  // namespace p8x

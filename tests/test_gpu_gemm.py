@@ -98,6 +98,20 @@ def test_gemm_ffn_512(rows, K):
     assert np.isfinite(Y).all()
 
 
+def test_gemm_wide_tile_2000_tokens():
+    """2000 tokens of the 14336 x 4096 shape: the plan takes the 256-token workgroup tile (8 MFMA token tiles per
+    wave), whose last tile runs past N; fp64 check on tokens of the first, a middle and the last tile"""
+    rows, K, N = 14336, 4096, 2000
+    slot = p8x.synth_random(2000, rows, K, nd=5)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    Xb = to_bf16(np.random.default_rng(2000).standard_normal((N, K)))
+    Y = t.mul_mat(Xb, p8x.BF16)
+    tok = np.array([0, 1, 255, 256, 1000, 1791, 1792, 1900, 1998, 1999])
+    assert rel_l2(Y[tok], reference(orc, bf16_to_f32(Xb), tok)) < REL_L2
+    assert np.isfinite(Y).all()
+
+
 def test_gemm_reserve_then_smaller_calls():
     """workspace reserved for 300 tokens serves calls with 300 and fewer tokens, results unchanged"""
     rows, K = 512, 4096

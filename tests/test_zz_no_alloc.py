@@ -74,8 +74,8 @@ def test_noalloc_runs_the_ffn_down_shape():
 
 
 def test_noalloc_rejects_oversized_request():
-    """4096 tokens of a 14336 x 4096 tensor need ~270 MB of workspace: rejected before any launch"""
-    rows, K, N = 14336, 4096, 4096
+    """4096 tokens of a 4096 x 14336 tensor need 117 MB of rotated activations alone: rejected before any launch"""
+    rows, K, N = 4096, 14336, 4096
     t = p8x.Tensor(p8x.synth_random(73, rows, K, nd=1), rows, K)
     xd = p8x.DeviceBuffer(2 * N * K)
     yd = p8x.DeviceBuffer(4 * N * rows)
