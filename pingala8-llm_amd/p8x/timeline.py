@@ -23,6 +23,14 @@ activation loads are in (the timeline build waits for them there), when its tile
 quantization is done, and, for its first round of row groups, when its tiles are done, the partial rows exchanged
 and the epilogue done. Per stage: the median / maximum over workgroups of each phase, and the stage's span (the
 previous stage's last release to this stage's last release).
+
+    python -m p8x.timeline --gemm [--tokens 512]
+
+times one p8x_mul_mat call per Llama-3.1-8B FFN shape (bf16 tokens, after warm-up calls): lane 0 of every k_mm wave
+records s_memrealtime at its start, after its prologue (first x' half-block, payload and coset table in, first
+barrier), summed over the half-blocks the time of its products (the x' writes of the next half-block included) and of
+its barrier waits, at the end of its K loop and when its output stores have completed. Prints the median and maximum
+over waves of each phase.
 """
 import argparse
 import ctypes
@@ -127,12 +135,45 @@ def step_timeline(args, L):
     barrier_timeline(buf.astype(np.int64), info, nl)
 
 
+def gemm_timeline(args, L):
+    rng = np.random.default_rng(3)
+    N = args.tokens
+    for name, rows, K in (("ffn_up 4096->14336", 14336, 4096), ("ffn_down 14336->4096", 4096, 14336)):
+        t = p8x.Tensor(p8x.synth_random(rows + K, rows, K, nd=8), rows, K)
+        u = rng.standard_normal((N, K)).astype(np.float32).view(np.uint32).astype(np.uint64)
+        xb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        xd, yd = p8x.DeviceBuffer.from_numpy(xb), p8x.DeviceBuffer(4 * N * rows)
+        st = p8x.Stream()
+        for _ in range(args.replays):
+            t.mul_mat_dev(xd, p8x.BF16, N, yd, stream=st)
+        st.sync()
+        p8x.check(L.p8x_timeline_reset(), "p8x_timeline_reset")
+        t.mul_mat_dev(xd, p8x.BF16, N, yd, stream=st)
+        st.sync()
+        buf = np.zeros((65536, 8), np.uint64)
+        n = ctypes.c_uint()
+        p8x.check(L.p8x_timeline_read(buf.ctypes.data, buf.nbytes, ctypes.byref(n)), "p8x_timeline_read")
+        r = buf[:min(n.value, 65536)].astype(np.int64)
+        blocks = r[:, 0] & 0xFFFF
+        us = lambda v: v / 100.0
+        phases = [("prologue", r[:, 2] - r[:, 1]), ("products", r[:, 3]), ("barrier waits", r[:, 4]),
+                  ("stores", r[:, 6] - r[:, 5]), ("wave total", r[:, 6] - r[:, 1])]
+        print(f"{name}, {N} tokens: {len(r)} waves, {int(r[0, 7])} workgroups, {sorted(set(blocks.tolist()))} K blocks each; "
+              f"kernel span {us(r[:, 6].max() - r[:, 1].min()):.2f} us")
+        for label, v in phases:
+            print(f"  {label:14s} median {us(np.median(v)):7.2f} us   max {us(v.max()):7.2f} us")
+        print(f"  products per half-block (median) {us(np.median(r[:, 3] / (2 * blocks))):.3f} us")
+        xd.free(); yd.free(); st.release(); t.release()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--replays", type=int, default=20, help="untimed graph replays before the recorded one")
     ap.add_argument("--step", action="store_true", help="the one-launch step kernel instead of the graph of launches")
     ap.add_argument("--dump", default=None, help="with --step: save the raw records [stage][workgroup][8] to this .npy file")
+    ap.add_argument("--gemm", action="store_true", help="the prompt GEMM's k_mm waves instead of the decode step")
+    ap.add_argument("--tokens", type=int, default=512, help="with --gemm: tokens per call")
     args = ap.parse_args()
     p8x.LIB_PATH = os.path.join(p8x.HERE, "libp8x_timeline.so")
     L = p8x.lib()
@@ -142,6 +183,9 @@ def main():
     p8x.check(L.p8x_timeline_reset(), "p8x_timeline_reset")   # allocates the record buffer before any capture
     if args.step:
         step_timeline(args, L)
+        return
+    if args.gemm:
+        gemm_timeline(args, L)
         return
     root = os.path.dirname(os.path.dirname(p8x.HERE))
     sys.path.insert(0, root)
