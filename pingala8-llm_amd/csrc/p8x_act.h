@@ -52,14 +52,17 @@ __device__ __forceinline__ T lane_xor(T v, int lane) {
     return __builtin_bit_cast(T, r);
 }
 
-// one butterfly stage across lanes: the lower index gets a + b, the upper a - b, with a the lower operand
+// one butterfly stage across lanes: the lower index gets a + b, the upper a - b, with a the lower operand. Computed
+// as p + s v with s = -1 for the upper lanes and +1 for the lower: s v is exact and the one rounding of the add gives
+// p - v and v + p bit for bit (IEEE defines x - y as x + (-y)); the partner's value p reaches the add through its DPP
+// operand, so a stage costs a multiply and an add instead of an add, a move, a subtract and a select.
 template <int M>
 __device__ __forceinline__ void fwht_lane_stage(float (&v)[4], int lane) {
-    const bool upper = (lane & M) != 0;
+    const float s = (lane & M) ? -1.f : 1.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float p = lane_xor<M>(v[e], lane);
-        v[e] = upper ? p - v[e] : v[e] + p;
+        const float sv = s * v[e];
+        v[e] = lane_xor<M>(v[e], lane) + sv;
     }
 }
 
