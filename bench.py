@@ -374,11 +374,13 @@ def measure_dependent_step(tensors, kinds, stream, steps, graph_replay=True):
 
 
 def measure_gemm(steps, N=512):
-    """prompt GEMM on the Llama-3.1-8B FFN shapes: N bf16 tokens ~ N(0, 1), whole p8x_mul_mat calls timed"""
+    """prompt GEMM on the Llama-3.1-8B FFN shapes: N bf16 tokens ~ N(0, 1), whole p8x_mul_mat calls timed; class-3
+    tensors, and ffn_down with the released models' class mix (the every-class kernel)"""
     out = {}
     rng = np.random.default_rng(3)
-    for name, rows, K in (("ffn_up 4096->14336", 14336, 4096), ("ffn_down 14336->4096", 4096, 14336)):
-        t = p8x.Tensor(p8x.synth_random(rows + K, rows, K, nd=8), rows, K)
+    for name, rows, K, cp in (("ffn_up 4096->14336", 14336, 4096, CLASS_C3), ("ffn_down 14336->4096", 4096, 14336, CLASS_C3),
+                              ("ffn_down 14336->4096, b4 class mix", 4096, 14336, CLASS_B4["ffn_down"])):
+        t = p8x.Tensor(p8x.synth_random(rows + K, rows, K, class_p=cp, nd=8), rows, K)
         u = rng.standard_normal((N, K)).astype(np.float32).view(np.uint32).astype(np.uint64)
         xb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
         xd = p8x.DeviceBuffer.from_numpy(xb)

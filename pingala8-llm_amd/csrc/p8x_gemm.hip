@@ -118,21 +118,6 @@ __device__ __forceinline__ void weights_chunk(const uint32_t (&w)[3], half2v s2,
     hi = vh * s2;
 }
 
-template <int C, int NWMAX>
-__device__ __forceinline__ half8v decode_pair(const AnySlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes, int s) {
-    const half2v s2 = {__builtin_bit_cast(_Float16, (uint16_t)ls.s), __builtin_bit_cast(_Float16, (uint16_t)ls.s)};
-    const uint32_t hq = coset_bytes(ls.H, bankbytes, s >> 1);
-    uint32_t w0[3], w1[3];
-    lookup_chunk<C>(ls, tab, 2 * s, hq, w0);
-    lookup_chunk<C>(ls, tab, 2 * s + 1, hq, w1);
-    half2v a, b, c, d;
-    weights_chunk<C>(w0, s2, a, b);
-    weights_chunk<C>(w1, s2, c, d);
-    half8v o;
-    o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y; o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
-    return o;
-}
-
 // classes decoded by an instantiation: the tensor's class set (class 0 decodes as zeros in all of them)
 constexpr int kMmCmC3 = 1 << 3, kMmCmAll = 0xFE;
 constexpr int kMmMain = 3;   // the class with a branch-free path in every instantiation (the 2-bit bulk)
@@ -155,20 +140,6 @@ __host__ __device__ constexpr int mm_tok(int nti) { return 32 * nti; }
 __host__ __device__ constexpr int mm_tab_words(int cm) { return cm == kMmCmC3 ? kTabWords / 2 : kTabWords; }
 __host__ __device__ constexpr int mm_tab_shift(int cm) { return cm == kMmCmC3 ? 1 : 0; }
 
-template <int CM, int NWMAX>
-__device__ __forceinline__ half8v decode_any(const AnySlice<NWMAX> &ls, int c, const uint32_t *tab, uint32_t bankbytes, int s) {
-    switch (c) {
-        case 1: if constexpr ((CM >> 1) & 1) return decode_pair<1>(ls, tab, bankbytes, s); break;
-        case 2: if constexpr ((CM >> 2) & 1) return decode_pair<2>(ls, tab, bankbytes, s); break;
-        case 3: if constexpr ((CM >> 3) & 1) return decode_pair<3>(ls, tab, bankbytes, s); break;
-        case 4: if constexpr ((CM >> 4) & 1) return decode_pair<4>(ls, tab, bankbytes, s); break;
-        case 5: if constexpr ((CM >> 5) & 1) return decode_pair<5>(ls, tab, bankbytes, s); break;
-        case 6: if constexpr ((CM >> 6) & 1) return decode_pair<6>(ls, tab, bankbytes, s); break;
-        case 7: if constexpr ((CM >> 7) & 1) return decode_pair<7>(ls, tab, bankbytes, s); break;
-        default: break;
-    }
-    return half8v{};
-}
 
 // x' half-block tile in LDS: half sh of block b holds, per token, columns 128 kh + 64 sh + 8 c8 + (0..7) as
 // chunk c = 8 kh + c8 at position c ^ (t & 15) of the token's 256-byte row, so the 16-byte operand reads of
@@ -233,6 +204,73 @@ __device__ __forceinline__ void mm_prepare(AnySlice<NWMAX> (&ls)[NTJ], const int
     for (int tj = 0; tj < NTJ; ++tj) {
         if constexpr (CM == kMmCmC3) ls[tj].template from_raw<3>(raw[tj]);   // zero raw words, S = 0: zero weights
         else prepare_any<CM>(ls[tj], cl[tj], raw[tj]);
+    }
+}
+
+// The 8 steps of one half-block for row tile TJ alone, its class C fixed: the same two-deep pipeline as the both-tiles
+// path of mm_half (table words two steps ahead, B one step ahead), NTI MFMAs per step. Every-class kernel, for a
+// half-block whose two tiles are not both class 3: one compact loop per (class, tile) instead of a class switch in
+// every step (whose code for all classes exceeded the instruction cache).
+template <int C, int TJ, int NWMAX, int NTI, int NTJ>
+__device__ __forceinline__ void mm_tile_pass(const _Float16 *__restrict__ xb, const AnySlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes,
+                                             int sh, int j, int kh, float16v (&acc)[NTI][NTJ]) {
+    const half2v s2 = {__builtin_bit_cast(_Float16, (uint16_t)ls.s), __builtin_bit_cast(_Float16, (uint16_t)ls.s)};
+    auto read_a = [&](int s8, half8v (&A)[NTI]) {
+#pragma unroll
+        for (int ti = 0; ti < NTI; ++ti)
+            A[ti] = *reinterpret_cast<const half8v *>(xb + (32 * ti + j) * 128 + 8 * ((8 * kh + s8) ^ (j & 15)));
+    };
+    auto lookups = [&](int s, uint32_t (&W)[2][3]) {
+        const uint32_t hq = coset_bytes(ls.H, bankbytes, s >> 1);
+        lookup_chunk<C>(ls, tab, 2 * s, hq, W[0]);
+        lookup_chunk<C>(ls, tab, 2 * s + 1, hq, W[1]);
+    };
+    auto decode = [&](const uint32_t (&W)[2][3]) {
+        half2v a, b, c, d;
+        weights_chunk<C>(W[0], s2, a, b);
+        weights_chunk<C>(W[1], s2, c, d);
+        half8v o;
+        o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y; o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
+        return o;
+    };
+    uint32_t W[2][3];
+    lookups(8 * sh, W);
+    half8v B = decode(W), A[NTI];
+    read_a(0, A);
+    lookups(8 * sh + 1, W);
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+        half8v An[NTI], Bn;
+        uint32_t Wn[2][3];
+        if (s8 < 7) { Bn = decode(W); read_a(s8 + 1, An); }
+        if (s8 < 6) lookups(8 * sh + s8 + 2, Wn);
+#pragma unroll
+        for (int ti = 0; ti < NTI; ++ti) acc[ti][TJ] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B, acc[ti][TJ], 0, 0, 0);
+        if (s8 < 7) {
+            B = Bn;
+#pragma unroll
+            for (int ti = 0; ti < NTI; ++ti) A[ti] = An[ti];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int q = 0; q < 3; ++q) W[u][q] = Wn[u][q];
+        }
+    }
+}
+
+// row tile TJ's half-block in the pass for its class (class 0: zero weights, nothing to add)
+template <int CM, int TJ, int NWMAX, int NTI, int NTJ>
+__device__ __forceinline__ void mm_tile_any(int c, const _Float16 *__restrict__ xb, const AnySlice<NWMAX> &ls, const uint32_t *tab, uint32_t bankbytes,
+                                            int sh, int j, int kh, float16v (&acc)[NTI][NTJ]) {
+    switch (c) {
+        case 1: if constexpr ((CM >> 1) & 1) mm_tile_pass<1, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 2: if constexpr ((CM >> 2) & 1) mm_tile_pass<2, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 3: if constexpr ((CM >> 3) & 1) mm_tile_pass<3, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 4: if constexpr ((CM >> 4) & 1) mm_tile_pass<4, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 5: if constexpr ((CM >> 5) & 1) mm_tile_pass<5, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 6: if constexpr ((CM >> 6) & 1) mm_tile_pass<6, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        case 7: if constexpr ((CM >> 7) & 1) mm_tile_pass<7, TJ>(xb, ls, tab, bankbytes, sh, j, kh, acc); break;
+        default: break;
     }
 }
 
@@ -335,18 +373,10 @@ __device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const A
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-    } else {
-#pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-            half8v A[NTI], B[NTJ];
-            read_a(s8, A);
-#pragma unroll
-            for (int tj = 0; tj < NTJ; ++tj) B[tj] = decode_any<CM>(ls[tj], cl[tj], tab, bankbytes, 8 * sh + s8);
-#pragma unroll
-            for (int ti = 0; ti < NTI; ++ti)
-#pragma unroll
-                for (int tj = 0; tj < NTJ; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ti], B[tj], acc[ti][tj], 0, 0, 0);
-        }
+    } else if constexpr (CM != kMmCmC3) {
+        static_assert(NTJ == 2, "one pass per row tile");
+        mm_tile_any<CM, 0>(cl[0], xb, ls[0], tab, bankbytes, sh, j, kh, acc);
+        mm_tile_any<CM, 1>(cl[1], xb, ls[1], tab, bankbytes, sh, j, kh, acc);
         mm_put<NWAVES, TOK>(xq, xn, w, lane);
     }
 }
