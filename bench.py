@@ -577,13 +577,32 @@ def main():
         f"-> {achieved:.0f} GB/s (steps with kernel events {ms_per_step_events * 1e3:.1f} us)")
     b4 = measure_b4_mix(args, stream) if args.mix == "c3" and not args.no_mix else None
 
+    device_bw = None
     if args.copy_calib:
+        # also the practical ceilings of a write-only and a read + write stream on this card: the runtime's own fill
+        # and device-to-device copy of the same size, median of 5 (events around each synchronous call)
         n = args.copy_calib << 20
         src, dst = p8x.DeviceBuffer(n), p8x.DeviceBuffer(n)
         src.fill(1)
         p8x.synchronize()
         dst.copy_from(src)
         p8x.synchronize()
+        e0, e1 = p8x.Event(), p8x.Event()
+
+        def timed(fn):
+            ts = []
+            for _ in range(5):
+                e0.record(None)
+                fn()
+                e1.record(None)
+                p8x.synchronize()
+                ts.append(e0.elapsed_ms(e1))
+            return float(np.median(ts))
+        fill_ms, copy_ms = timed(lambda: src.fill(7)), timed(lambda: dst.copy_from(src))
+        device_bw = {"bytes": n, "fill_TB/s": round(n / (fill_ms * 1e-3) / 1e12, 3),
+                     "copy_TB/s (read + write)": round(2 * n / (copy_ms * 1e-3) / 1e12, 3)}
+        log("device fill / copy:", json.dumps(device_bw))
+        e0.release(); e1.release()
         src.free(); dst.free()
         log(f"copy calibration: {n} bytes device to device")
 
@@ -623,6 +642,7 @@ def main():
         "qwen3_4b_layer": qwen4b,
         "quantized_4096": quant4096,
         "b4_mix": b4,
+        "device_bandwidth": device_bw,
         "host_wall_s": round(wall, 3),
     }
     # every handle released here, while the runtime (and a profiler's tool attached to it) is still up; nothing is
