@@ -112,6 +112,20 @@ def test_gemm_wide_tile_2000_tokens():
     assert np.isfinite(Y).all()
 
 
+def test_gemm_identity_rows_direct_output():
+    """identity row order and one K range: k_mm writes y itself (no planes) and a separate launch adds the clamp
+    delta; 250 tokens, so the last token tile runs past N"""
+    rows, K, N = 14336, 1024, 250
+    slot = p8x.synth_random(77, rows, K, nd=6, permute=False)
+    t = p8x.Tensor(slot, rows, K)
+    orc = O.Oracle(slot, rows, K)
+    X = np.random.default_rng(77).standard_normal((N, K)).astype(np.float32)
+    Y = t.mul_mat(X, p8x.F32)
+    tok = np.array([0, 1, 127, 128, 200, 248, 249])
+    assert rel_l2(Y[tok], reference(orc, X, tok)) < REL_L2
+    assert np.isfinite(Y).all()
+
+
 def test_gemm_reserve_then_smaller_calls():
     """workspace reserved for 300 tokens serves calls with 300 and fewer tokens, results unchanged"""
     rows, K = 512, 4096
