@@ -7,7 +7,7 @@ the workgroup barrier, after its tiles, and at its end. The chain replayed from 
 dependent_step measures: per layer {q,k,v} -> o -> {gate,up}+swiglu -> down, then the head shards, each launch reading
 its producer's output (Llama-3.1-8B shapes, class-3 tensors).
 
-    python -m p8x.timeline [--layers 32]
+    python -m p8x.timeline [--layers 32] [--eager]
 
 prints, per kind of launch, the median and maximum over workgroups of each stamp (us from the launch's first
 workgroup start), averaged over the launches of that kind, and the gap from the previous launch's last workgroup end
@@ -171,6 +171,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--replays", type=int, default=20, help="untimed graph replays before the recorded one")
     ap.add_argument("--step", action="store_true", help="the one-launch step kernel instead of the graph of launches")
+    ap.add_argument("--eager", action="store_true", help="the launches enqueued one by one instead of replayed from a graph")
     ap.add_argument("--dump", default=None, help="with --step: save the raw records [stage][workgroup][8] to this .npy file")
     ap.add_argument("--gemm", action="store_true", help="the prompt GEMM's k_mm waves instead of the decode step")
     ap.add_argument("--tokens", type=int, default=512, help="with --gemm: tokens per call")
@@ -212,18 +213,19 @@ def main():
         p8x.mul_mat_vec_multi_dev(head, cur, yh, stream=s)
 
     st = p8x.Stream()
-    graph = p8x.Graph(enqueue, st)
+    graph = None if args.eager else p8x.Graph(enqueue, st)
     for _ in range(args.replays):
-        graph.launch(st)
+        enqueue(st) if args.eager else graph.launch(st)
     st.sync()
     p8x.check(L.p8x_timeline_reset(), "p8x_timeline_reset")
-    graph.launch(st)
+    enqueue(st) if args.eager else graph.launch(st)
     st.sync()
     nrec = 65536
     buf = np.zeros((nrec, 8), np.uint64)
     n = ctypes.c_uint()
     p8x.check(L.p8x_timeline_read(buf.ctypes.data, buf.nbytes, ctypes.byref(n)), "p8x_timeline_read")
-    graph.release()
+    if graph:
+        graph.release()
     rec = buf[:min(n.value, nrec)].astype(np.int64)
     # records in arrival order; launches on one stream do not overlap, so consecutive runs of `grid` records are
     # one launch each
@@ -244,13 +246,21 @@ def main():
         prev_end = t[:, 6].max()
         rows.setdefault(kind, []).append(med + mx + [gap, len(t)])
     print(f"{len(launches)} launches, {len(rec)} workgroup records; us from the launch's first workgroup start")
-    print("| launch | workgroups | " + " | ".join(STAMPS[1:]) + " | gap before |")
-    print("|---|---|" + "---|" * 7)
+    print("| launch | workgroups | " + " | ".join(STAMPS) + " | gap before |")
+    print("|---|---|" + "---|" * 8)
     for kind, v in rows.items():
         m = np.nanmean(np.array(v, np.float64), axis=0)
-        cells = [f"{m[j]:.2f} / {m[7 + j]:.2f}" for j in range(1, 7)]
+        cells = [f"{m[j]:.2f} / {m[7 + j]:.2f}" for j in range(0, 7)]
         print(f"| {kind} | {int(m[15])} | " + " | ".join(cells) + f" | {m[14]:.2f} |")
-    print("(each cell: median / maximum over the workgroups, averaged over the launches of that kind)")
+    print("(each cell: median / maximum over the workgroups, averaged over the launches of that kind; start: when the "
+          "workgroup began, the dispatch ramp of the launch)")
+    # per workgroup, from its own start: how long its kernel-argument fields took (args in - start)
+    own = {}
+    for li, t in enumerate(launches):
+        kind = names[li % 4] if li < 4 * nl else "head"
+        own.setdefault(kind, []).append(np.median((t[:, 1] - t[:, 0]) / 100.0))
+    print("kernel-argument fields in, from each workgroup's own start (median over workgroups, mean over launches): " +
+          ", ".join(f"{k} {np.mean(v):.2f} us" for k, v in own.items()))
 
 
 if __name__ == "__main__":
