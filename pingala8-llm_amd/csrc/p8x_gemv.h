@@ -629,6 +629,11 @@ __device__ __forceinline__ void glu_meet(const RgJobs &R, int jb, int r, float v
 template <int CM, bool SPLIT, int NCOL, bool TEAMS, bool MULTI>
 __global__ __launch_bounds__(64 * rg_waves(NCOL)) __attribute__((amdgpu_waves_per_eu(rg_waves(NCOL) / 4, rg_waves(NCOL) / 4)))
 void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
+#ifdef P8X_TIMELINE
+    unsigned long long stamp[7] = {0, 0, 0, 0, 0, 0, 0};
+    stamp[0] = __builtin_amdgcn_s_memrealtime();   // before any kernel-argument load
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
     const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
@@ -648,14 +653,6 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     }
     const GemvJob &J = JL;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-#ifdef P8X_TIMELINE
-    unsigned long long stamp[7] = {0, 0, 0, 0, 0, 0, 0};
-    unsigned slot = 0;
-    if (tid == 0) {
-        stamp[0] = __builtin_amdgcn_s_memrealtime();
-        slot = __hip_atomic_fetch_add((unsigned *)(jobs.tl + kTimelineRecords * 8), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-#endif
     TaskCtx<NCOL, P8X_ACT_Q8_128> c;
     c.J = &J;
     c.hs = lane >> 5; c.j = lane & 31;
@@ -809,6 +806,10 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     if (tid == 0) {
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         stamp[6] = __builtin_amdgcn_s_memrealtime();
+        // the record slot is taken last: a returning atomic on one counter that every workgroup hits would
+        // otherwise sit inside the first stamped interval
+        const unsigned slot = __hip_atomic_fetch_add((unsigned *)(jobs.tl + kTimelineRecords * 8), 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         if (slot < kTimelineRecords) {
             unsigned long long *o = jobs.tl + (size_t)slot * 8;
             o[0] = ((unsigned long long)blockIdx.x << 32) | gridDim.x;
