@@ -637,6 +637,14 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
     const int gc = TEAMS ? gc_ : 1;   // without teams: one row group at a time, all waves on it
     constexpr int WAVES = rg_waves(NCOL), RQ = kRgMaxBlocks / WAVES;
     __shared__ RgSmem<NCOL> sm;
+    // the argument fields the x loads need, requested in the first round of scalar loads with the job ranges
+    // (left to the scheduler, some land in a second round behind the job selection's branches)
+    if constexpr (MULTI)
+        __asm__ volatile("" ::"s"(jobs.j0.x), "s"(jobs.j0.ic), "s"(jobs.j0.ldx), "s"(jobs.j0.kchunk), "s"(jobs.j0.nks), "s"(jobs.j0.nb),
+                         "s"(jobs.wgbase[1]), "s"(jobs.wgbase[2]), "s"(jobs.wgbase[3]), "s"(jobs.wgbase[4]), "s"(jobs.jt[0]),
+                         "s"(jobs.jt[1]), "s"(jobs.jt[2]), "s"(jobs.jt[3]));
+    else
+        __asm__ volatile("" ::"s"(jobs.j0.x), "s"(jobs.j0.ic), "s"(jobs.j0.ldx), "s"(jobs.j0.kchunk), "s"(jobs.j0.nks), "s"(jobs.j0.nb));
     // this workgroup's job, its index among the job's workgroups and their count
     int jb = 0, wgl = (int)blockIdx.x, nwg = (int)gridDim.x;
     GemvJob JL = jobs.j0;
@@ -647,7 +655,10 @@ void k_gemv_rg(RgJobs jobs, const uint32_t *__restrict__ a2, int gc_) {
         wgl = bi - wb;
         nwg = pick(jb, jobs.wgbase[1], jobs.wgbase[2], jobs.wgbase[3], jobs.wgbase[4]) - wb;
         JL = *(const GemvJob *)pick(jb, jobs.jt[0], jobs.jt[1], jobs.jt[2], jobs.jt[3]);
+        // the x loads take only argument fields (the jobs share K and the rotation ic bit for bit, which the host
+        // checks), so they are issued before the job's tensor record arrives
         JL.x = jobs.j0.x; JL.ldx = jobs.j0.ldx; JL.nks = jobs.j0.nks; JL.kchunk = jobs.j0.kchunk;
+        JL.ic = jobs.j0.ic; JL.nb = jobs.j0.nb;
         JL.y = pick(jb, jobs.y[0], jobs.y[1], jobs.y[2], jobs.y[3]);
         JL.ldy = pick(jb, jobs.ldy[0], jobs.ldy[1], jobs.ldy[2], jobs.ldy[3]);
     }

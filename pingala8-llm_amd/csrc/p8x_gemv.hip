@@ -494,7 +494,8 @@ int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_
         if (ts[i]->K != ts[0]->K) return set_error(P8X_ERR_ARG, "%s: tensor %d has K %d, tensor 0 has %d", what, i, ts[i]->K, ts[0]->K);
         if (memcmp(ts[i]->a2_host, ts[0]->a2_host, sizeof ts[0]->a2_host))
             return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d has a different codebook", what, i);
-        if (ts[i]->ic_hash != ts[0]->ic_hash)
+        if (ts[i]->ic_hash != ts[0]->ic_hash || ts[i]->ic_host.size() != ts[0]->ic_host.size() ||
+            memcmp(ts[i]->ic_host.data(), ts[0]->ic_host.data(), 4 * ts[0]->ic_host.size()))
             return set_error(P8X_ERR_UNSUPPORTED, "%s: tensor %d rotates its input differently (column scales c or signs); call it alone", what, i);
     }
     if (!x || ldx < (size_t)ts[0]->K || ldx % 4 || ((uintptr_t)x & 15))

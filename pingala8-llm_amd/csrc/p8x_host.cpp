@@ -242,6 +242,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     t->n = n; t->nt = nt; t->kbytes = kbytes;
     t->stream_bytes = 4 * nt + 64 * nt + 4 * words;
     t->ic_hash = ic_hash;
+    t->ic_host = ic;
     for (int c = 0; c < 8; ++c) t->class_tiles[c] = hist[c];
     for (int c = 1; c < 8; ++c)
         if (hist[c] == nt) {   // one class: are the tiles in order (tile i at word i * 64 nw)?

@@ -48,6 +48,7 @@ struct p8x_tensor {
     unsigned long long *wglu = nullptr;   // gate / up meeting slots (this tensor as the gate) [rows], 0 between calls
     unsigned long long *wslot = nullptr;  // K-half meeting slots of one-column two-chunk plans [rows], 0 between calls
     uint64_t ic_hash = 0;            // hash of the rotation sg / c (tensors with equal hashes share quantized inputs)
+    std::vector<float> ic_host;      // the rotation sg / c on the host (several-tensor launches compare it bit for bit)
     p8x::GemvJob *djob = nullptr;    // the tensor's metadata as a device-side GEMV job (launches over several tensors)
     float *wpart = nullptr;          // K-chunk partial rows [nks][ncols][rows], sized for the largest plan
     size_t wpart_floats = 0;

@@ -94,6 +94,7 @@ __device__ __forceinline__ void step_stage(kptr<const StepStage> sp, int v, RgSm
     const int nwg = pick(jb, sp->R.wgbase[1], sp->R.wgbase[2], sp->R.wgbase[3], sp->R.wgbase[4]) - wb;
     GemvJob JL = *(const GemvJob *)pick(jb, sp->R.jt[0], sp->R.jt[1], sp->R.jt[2], sp->R.jt[3]);
     JL.x = sp->R.j0.x; JL.ldx = sp->R.j0.ldx; JL.nks = sp->R.j0.nks; JL.kchunk = sp->R.j0.kchunk;
+    JL.ic = sp->R.j0.ic; JL.nb = sp->R.j0.nb;   // shared by the stage's jobs (checked on the host): no tensor record wait
     JL.y = pick(jb, sp->R.y[0], sp->R.y[1], sp->R.y[2], sp->R.y[3]);
     const GemvJob &J = JL;
     const int glu = sp->R.glu;
