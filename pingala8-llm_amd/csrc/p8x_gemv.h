@@ -1167,6 +1167,221 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int uni
     return hip_check(hipGetLastError(), "k_gemv_wave launch");
 }
 
+// ------------------------------------------------------------------------------------------------ matrix-core GEMV
+// 2..8 columns of class-3 tiles in grouped launches. A tile's integer products form a small matrix product,
+// (32 rows x 128 K) x (128 K x columns) per 128-column half, which v_mfma_i32_32x32x32_i8 computes with the
+// looked-up codewords as the B operand (n = row = lane & 31) and the activations as A (m = column; rows of A past
+// the batch read a zero line): per tile 8 MFMAs replace 32 v_dot4 per column and lane. Lane (row j, half hs) looks up
+// its 32 codewords as the broadcast kernel does; one v_permlane32_swap per pair (chunk k, chunk k + 16) turns the
+// two halves' words into per-half operands (words 0..15: half 0, lanes 0..31 chunks 0..15 and lanes 32..63 chunks
+// 16..31; words 16..31 the same of half 1), so that MFMA i of half h reads words 16 h + 4 i .. + 3: K bytes
+// 16 i .. + 15 of the half in lanes 0..31 and 64 + 16 i .. in lanes 32..63. The activations come in a layout to
+// match (k_act_q8_128_mx_batch): per 256-block and column a 256-byte record (half 0, then half 1), the halves'
+// scales [block][column][2] after the records. A wave loads its next tile's records and scales with one to three
+// 16-byte loads per lane and, when it reaches that tile, copies them into its own LDS slot, from which lane
+// (column m, group g) reads its A operands (64 bytes at 64 g of each half) and lane (row j, group g) the scales of
+// columns 4 g .. 4 g + 3; so only 12 registers per tile in flight hold activations. The output lane (row j, group
+// g) holds columns 4 g .. 4 g + 3, accumulated per half as the broadcast kernel does (y_h += ((float)isum d) S tile
+// by tile, then half 0 + half 1): the same bits.
+constexpr uint32_t kMxRecBytes = 256;   // activation record per 256-block and column
+__host__ __device__ constexpr int mx_waves() { return 16; }
+__host__ __device__ constexpr int mx_per_eu() { return 4; }
+__host__ __device__ constexpr int mx_wg_per_cu() { return 4 * mx_per_eu() / mx_waves(); }
+// activation bytes of a job: the records, then the scales
+__host__ __device__ constexpr size_t mx_act_bytes(int ncols, int nb) { return (size_t)ncols * nb * (kMxRecBytes + 8); }
+// a wave's LDS slot: the tile's records, its scales (8 columns' worth) and a zero line for the rows of A past the batch
+template <int NCOL>
+struct MxSlot {
+    static constexpr int kRecWords = NCOL * kMxRecBytes / 4;
+    uint32_t w[kRecWords + 16 + 4];   // records | scales [8][2] | zero line
+    static constexpr int kScaleWord = kRecWords, kZeroWord = kRecWords + 16;
+};
+template <int NCOL>
+struct MxSmem {
+    uint32_t tab[kTabWords];   // LDS address 0
+    MxSlot<NCOL> slot[mx_waves()];
+};
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+
+template <int NCOL>
+struct MxSlice {
+    static constexpr int NREC = (16 * NCOL + 63) / 64;   // 16-byte record pieces per lane
+    QuadSlice<3> p;
+    u32x4_t r[NREC];   // record piece l (and l + 64) of the tile's NCOL records
+    u32x4_t d;         // scale piece l (lanes l < NCOL / 2, rounded up)
+};
+
+template <int NCOL>
+__device__ __forceinline__ void mx_tile(const uint32_t *tab, MxSlot<NCOL> &slot, int lane, const MxSlice<NCOL> &r_, float (&ya)[2][4]) {
+    constexpr int SH1 = sh1_of(3), NREC = MxSlice<NCOL>::NREC;
+    static_assert(nstage_of(3) == 1, "one codeword per chunk");
+    const int j = lane & 31, g = lane >> 5;
+    MxSlice<NCOL> r = r_;
+    pin(r.p.w);
+    pin(r.p.s);
+    // the tile's activations into the wave's slot (program order keeps the wave's own LDS accesses in order)
+    u32x4_t *sv = reinterpret_cast<u32x4_t *>(slot.w);
+#pragma unroll
+    for (int q = 0; q < NREC; ++q)
+        if (lane + 64 * q < 16 * NCOL) sv[lane + 64 * q] = r.r[q];
+    if (lane < (NCOL + 1) / 2) sv[MxSlot<NCOL>::kScaleWord / 4 + lane] = r.d;
+    const uint32_t H = r.p.coset_bits(), bankbytes = (uint32_t)(j << 2) * 0x01010101u;
+    uint32_t w[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const uint32_t hq = coset_bytes(H, bankbytes, q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * q + e] = lds_word(tab, r.p.template addr<0>(4 * q + e, hq));
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(w[k], w[k + 16], false, false);
+        w[k] = sw[0];
+        w[k + 16] = sw[1];
+    }
+    const int m = j;   // A row (column of the batch) of this lane
+    const u32x4_t *arow = sv + (m * (int)kMxRecBytes + 64 * g) / 16;
+    // lanes of rows past the batch keep zero operands and read nothing (their loads are masked off)
+    u32x4_t xa[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xa[i] = u32x4_t{0u, 0u, 0u, 0u};
+    if (m < NCOL) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xa[i] = arow[8 * (i >> 2) + (i & 3)];   // half i / 4, 16-byte piece i % 4
+    }
+    const u32x4_t dv0 = sv[MxSlot<NCOL>::kScaleWord / 4 + 2 * g], dv1 = sv[MxSlot<NCOL>::kScaleWord / 4 + 2 * g + 1];
+    const float sc = half_to_float(r.p.s);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        i32x16_t acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4_t xv = xa[4 * h + i];
+            const i32x4_t a = {(int)xv[0], (int)xv[1], (int)xv[2], (int)xv[3]};
+            const i32x4_t bw = {(int)w[16 * h + 4 * i], (int)w[16 * h + 4 * i + 1], (int)w[16 * h + 4 * i + 2], (int)w[16 * h + 4 * i + 3]};
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4_t dd = c < 2 ? dv0 : dv1;
+            const float dsc = __uint_as_float(dd[2 * (c & 1) + h]);
+            ya[h][c] += ((float)(acc[c] * (1 << SH1)) * dsc) * sc;
+        }
+    }
+}
+
+// a run of consecutive class-3 tiles of row group g, MX_NBUF - 1 ahead of the one multiplied (the wave_run scheme)
+#ifndef MX_NBUF
+#define MX_NBUF 2
+#endif
+template <int NCOL>
+__device__ __forceinline__ int mx_run(const GemvJob &J, const uint32_t *tab, MxSlot<NCOL> &slot, int g, int b, int bend, int lane,
+                                      float (&ya)[2][4]) {
+    constexpr int NREC = MxSlice<NCOL>::NREC;
+    const int hs = lane >> 5, j = lane & 31;
+    const kptr<const uint32_t> mrow = as_const(J.M) + (size_t)g * J.nb;
+    const int e = bend;
+    const uint32_t sbytes = (uint32_t)J.nb * J.rows * 2u;
+    const uint32_t qbytes = (uint32_t)(NCOL * J.nb) * kMxRecBytes, dbytes = (uint32_t)(NCOL * J.nb) * 8u;
+    const uint32_t vo = QuadSlice<3>::quad_offset(hs, j), vp = QuadSlice<3>::pair_offset(hs, j);
+    const uint32_t vs = 2u * (uint32_t)j;
+    const uint8_t *dbase = reinterpret_cast<const uint8_t *>(J.q) + qbytes;
+    uint32_t wn = mrow[b];
+    auto issue = [&](MxSlice<NCOL> &r, int ta) {
+        const bool ok = ta < e;
+        const int tc = ok ? ta : b;
+        const uint32_t toff = (wn & 0x1FFFFFFFu) * 4u;
+        const uint32_t soff = ((uint32_t)g * (uint32_t)J.nb + (uint32_t)tc) * 64u;
+        __builtin_amdgcn_s_setprio(2);
+        r.p.load(buffer_rsrc(J.D, ok ? J.dbytes : 0u), toff, vo, vp, buffer_rsrc(J.S, ok ? sbytes : 0u), soff, vs);
+        // the tile's NCOL records (16 NCOL pieces) and scales; pieces past them read zeros without traffic
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(J.q, ok ? qbytes : 0u), rdd = buffer_rsrc(dbase, ok ? dbytes : 0u);
+        const uint32_t rec0 = (uint32_t)(tc * NCOL) * kMxRecBytes;
+#pragma unroll
+        for (int q = 0; q < NREC; ++q) {
+            const int piece = lane + 64 * q;
+            r.r[q] = __builtin_amdgcn_raw_buffer_load_b128(rq, piece < 16 * NCOL ? rec0 + 16u * (uint32_t)piece : 0x7FFFFF00u, 0, 0);
+        }
+        r.d = __builtin_amdgcn_raw_buffer_load_b128(rdd, lane < (NCOL + 1) / 2 ? (uint32_t)(tc * NCOL) * 8u + 16u * (uint32_t)lane : 0x7FFFFF00u, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+        wn = mrow[min(ta + 1, e - 1)];
+    };
+    MxSlice<NCOL> buf[MX_NBUF];
+#pragma unroll
+    for (int i = 0; i < MX_NBUF - 1; ++i) issue(buf[i], b + i);
+    int base = b;
+    for (; base + MX_NBUF <= e; base += MX_NBUF) {
+#pragma unroll
+        for (int i = 0; i < MX_NBUF; ++i) {
+            issue(buf[(i + MX_NBUF - 1) % MX_NBUF], base + i + MX_NBUF - 1);
+            mx_tile<NCOL>(tab, slot, lane, buf[i], ya);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MX_NBUF - 1; ++i)
+        if (base + i < e) mx_tile<NCOL>(tab, slot, lane, buf[i], ya);
+    return e;
+}
+
+// Grouped launch of class-3 jobs with 2..8 columns (the unit scheduling of k_gemv_wave); lane (row j, group g)
+// stores columns 4 g .. 4 g + 3 of its row's K-chunk partial
+template <int NCOL>
+__global__ __launch_bounds__(64 * mx_waves()) __attribute__((amdgpu_waves_per_eu(mx_per_eu(), mx_per_eu())))
+void k_gemv_wave_mx(const GemvJob *__restrict__ jobs, const uint32_t *__restrict__ ujob, int total_units, unsigned *ctr,
+                    const uint32_t *__restrict__ a2) {
+    static_assert(NCOL >= 1 && NCOL <= 8, "1..8 columns");
+    constexpr int WAVES = mx_waves();
+    __shared__ MxSmem<NCOL> sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    build_coset_table<64 * WAVES>(sm.tab, a2, tid);
+    MxSlot<NCOL> &slot = sm.slot[w];
+    if (lane < 4) slot.w[MxSlot<NCOL>::kZeroWord + lane] = 0u;
+    __syncthreads();
+    const int np = min(kWaveParts, (int)gridDim.x), part = blockIdx.x % np;
+    const int nwp = (((int)gridDim.x - 1 - part) / np + 1) * WAVES;
+    unsigned *pc = ctr + part * kWaveCtrStride;
+    int k = (blockIdx.x / np) * WAVES + w;
+    const int j = lane & 31, cg = lane >> 5;
+    for (int u = part + np * k; u < total_units; u = part + np * k) {
+        const int jc = (int)as_const(ujob)[u];
+        const GemvJob &J = jobs[jc];
+        const int local = u - J.task0, g = local / J.nks, ks = local % J.nks;
+        const int b0 = ks * J.kchunk, bend = min(b0 + J.kchunk, J.nb);
+        float ya[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ya[h][c] = 0.f;
+        if (b0 < bend) mx_run<NCOL>(J, sm.tab, slot, g, b0, bend, lane, ya);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = 4 * cg + c;
+            if (col < NCOL) as_global_rw(J.wpart)[((size_t)ks * NCOL + col) * J.rows + 32 * g + j] = ya[0][c] + ya[1][c];
+        }
+        k = nwp + (int)wave_atomic_add(pc, lane);
+    }
+    const unsigned left = wave_atomic_add(pc + 1, lane);
+    if (lane == 0 && left == (unsigned)nwp - 1) {
+        __hip_atomic_store(pc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pc + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int NCOL>
+static int launch_gemv_wave_mx_t(const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
+                                 hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
+    const int grid = mx_wg_per_cu() * num_cus();
+    if (e0 || e1)
+        hipExtLaunchKernelGGL((k_gemv_wave_mx<NCOL>), dim3(grid), dim3(64 * mx_waves()), 0, st, e0, e1, 0, jobs, ujob, units, ctr, a2);
+    else
+        hipLaunchKernelGGL((k_gemv_wave_mx<NCOL>), dim3(grid), dim3(64 * mx_waves()), 0, st, jobs, ujob, units, ctr, a2);
+    return hip_check(hipGetLastError(), "k_gemv_wave_mx launch");
+}
+
 // defined in the instantiation units
 int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
@@ -1180,5 +1395,13 @@ int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_
 int class_set(const size_t hist[8], bool in_order = true);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
                      hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// the matrix-core grouped launch (class 3, q8/128 activations in the k_act_q8_128_mx_batch layout), 2..8 columns
+int launch_gemv_wave_mx(int ncols, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
+                        hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// batches the matrix-core kernel can run (class set, activation mode, columns), and from how many columns the plan
+// takes it (on the Qwen3-14B stack it is slower at 2 columns, even at 3, and faster from 4: 0.84 / 0.96 ms against
+// 0.92 / 1.43 ms per step at 4 / 8 columns)
+__host__ __device__ constexpr bool wave_mx(int cm, int act, int ncols) { return cm == kCmC3 && act == P8X_ACT_Q8_128 && ncols >= 2 && ncols <= 8; }
+constexpr int kMxMinCols = 4;
 
 }  // namespace p8x

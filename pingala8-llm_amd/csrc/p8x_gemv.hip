@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -350,6 +351,23 @@ __global__ __launch_bounds__(256) void k_act_q8_128_batch(const ActJob *__restri
     }
 }
 
+// The same prep in the matrix-core kernel's layout (k_gemv_wave_mx): column n's block b as the 256-byte record
+// (b ncols + n) (the int8 of half 0, then half 1), the halves' scales after all records at [b][n][2].
+__global__ __launch_bounds__(256) void k_act_q8_128_mx_batch(const ActJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int total) {
+    const int gb = 4 * blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = blockIdx.y, lane = threadIdx.x & 63;
+    if (gb >= total) return;
+    const ActJob &J = jobs[as_const(blk_job)[gb]];
+    const int b = gb - J.blk0, ncols = (int)gridDim.y;
+    uint32_t packed;
+    float dd;
+    int s;
+    quantize_block_q8_128(J.x + (size_t)n * J.ldx + 256 * b, J.ic + 256 * b, lane, packed, dd, s);
+    const int hs = lane >> 5, t = lane & 31;
+    const size_t rec = (size_t)b * ncols + n;
+    reinterpret_cast<uint32_t *>(J.q + rec * kMxRecBytes + 128 * hs)[t] = packed;
+    if (t == 0) reinterpret_cast<float *>(J.q + (size_t)ncols * J.nb * kMxRecBytes)[2 * rec + hs] = dd;
+}
+
 // The x16 form of the batch prep (P8X_ACT_X16, the arithmetic of k_act_x16): grid (ceil(total blocks / 4), ncols),
 // column n's two planes written as virtual columns 2n (hi, scale 128 d) and 2n + 1 (lo, scale d) of the broadcast
 // layout, so the grouped kernel multiplies them as 2 ncols columns.
@@ -509,6 +527,7 @@ struct p8x_gemv_batch {
     int njobs = 0, ncols = 1, cm = 0, total_tasks = 0, total_blocks = 0;
     int act = P8X_ACT_Q8_128, ncv = 1;   // activation mode; columns the grouped kernel multiplies (x16: 2 ncols planes)
     int split_jobs = 0, small_launch = 0, waves = 0;   // plan facts reported by p8x_gemv_batch_info
+    bool mx = false;               // the matrix-core kernel (and its activation layout)
     unsigned *ctr = nullptr;       // its unit counters (in work)
     uint32_t *d_ujob = nullptr;    // unit -> job
     p8x::FinishJob *d_fin = nullptr;   // finishing launch (one column)
@@ -576,6 +595,11 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
     int blk0 = 0;
     std::vector<uint32_t> ablk;   // activation prep: 256-block -> job
     const int cm = class_set(hist);
+    // class-3 batches of kMxMinCols..8 columns run on the matrix cores; P8X_GEMV_MX in the environment overrides
+    // the choice for 2..8 columns (0: the v_dot4 kernel, 1: the matrix cores; the same bits either way)
+    const char *mx_env = getenv("P8X_GEMV_MX");
+    const bool mx = wave_mx(cm, act, ncols) && (mx_env && (mx_env[0] == '0' || mx_env[0] == '1') ? mx_env[0] == '1' : ncols >= kMxMinCols);
+    const int launch_waves = mx ? mx_wg_per_cu() * num_cus() * mx_waves() : wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
     // wave-independent units: (row group, whole K)
     std::vector<int> kcs(njobs);
     bool small_launch = false;
@@ -584,7 +608,7 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
         // Units are handed out longest first, so the launch drains on the units of the last jobs. Those jobs are
         // split along K (units of >= 4 blocks, partial rows summed by the finishing launch) until about two
         // rounds of the launch's waves have short units to finish on.
-        const long need = 2L * wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
+        const long need = 2L * launch_waves;
         std::vector<int> order(njobs);
         for (int i = 0; i < njobs; ++i) order[i] = i;
         std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return tensors[a]->nb > tensors[c]->nb; });
@@ -608,7 +632,7 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
         const p8x_tensor *t = tensors[i];
         const int kc = kcs[i];
         const int nks = (t->nb + kc - 1) / kc;
-        off_q[i] = take((size_t)ncv * t->nb * kBcastBlockBytes);
+        off_q[i] = take((size_t)ncv * t->nb * kBcastBlockBytes);   // also holds the matrix-core layout (mx_act_bytes)
         off_p[i] = take(4 * (size_t)nks * ncv * t->rows);   // partial rows (the finishing launch reads them)
         fill_job(jobs[i], t, nullptr, nullptr, x[i], ldx[i], y[i], ldy[i], nullptr, nks, kc, 1, 0);
         ajobs[i] = ActJob{x[i], (unsigned)ldx[i], t->ic, t->K, t->nb, nullptr, blk0};
@@ -644,7 +668,8 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
     for (auto &j : jobs) { j.task0 = task0; task0 += j.ntasks; }
     b->total_tasks = task0;
     b->small_launch = small_launch;
-    b->waves = wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
+    b->waves = launch_waves;
+    b->mx = mx;
     for (int i = 0; i < njobs; ++i) b->split_jobs += kcs[i] < tensors[i]->nb;
     {
         // unit -> job table
@@ -741,7 +766,7 @@ int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *str
     hipEvent_t e0 = (hipEvent_t)ev_start, e1 = (hipEvent_t)ev_stop;
     if (stage == 0) {
         const dim3 grid((b->total_blocks + 3) / 4, b->ncols);
-        auto kern = b->act == P8X_ACT_X16 ? k_act_x16_batch : k_act_q8_128_batch;
+        auto kern = b->act == P8X_ACT_X16 ? k_act_x16_batch : b->mx ? k_act_q8_128_mx_batch : k_act_q8_128_batch;
         if (e0 || e1)
             hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, e0, e1, 0, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
         else
@@ -749,6 +774,7 @@ int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *str
         return hip_check(hipGetLastError(), "batch activation prep launch");
     }
     if (stage == 1) {
+        if (b->mx) return launch_gemv_wave_mx(b->ncols, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
         return launch_gemv_wave(b->ncv, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
     }
     if (stage == 2) {   // partial rows to original rows with the clamp delta
@@ -840,7 +866,7 @@ int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const floa
 int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out) {
     if (!b || !out) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_info: null pointer");
     out->njobs = b->njobs; out->ncols = b->ncols; out->class_set = b->cm; out->units = b->total_tasks;
-    out->split_jobs = b->split_jobs; out->small_launch = b->small_launch; out->waves = b->waves;
+    out->split_jobs = b->split_jobs; out->small_launch = b->small_launch; out->waves = b->waves; out->matrix_cores = b->mx ? 1 : 0;
     return P8X_OK;
 }
 

@@ -58,7 +58,8 @@ class VrDesc(ctypes.Structure):
 
 
 class BatchInfo(ctypes.Structure):
-    _fields_ = [(f, ctypes.c_int) for f in ("njobs", "ncols", "class_set", "units", "split_jobs", "small_launch", "waves")]
+    _fields_ = [(f, ctypes.c_int) for f in ("njobs", "ncols", "class_set", "units", "split_jobs", "small_launch", "waves",
+                                            "matrix_cores")]
 
 
 class EncodeParams(ctypes.Structure):
