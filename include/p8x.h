@@ -233,9 +233,9 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b);
 /* The launch plan of a batch: work units (a 32-row group over a K-chunk), jobs cut along K, waves of the launch,
  * class_set (bit c: tile class c is decoded), small_launch = 1 when the batch had fewer whole-K units than two
  * rounds of the launch's waves and every job was cut into units of two or more blocks, matrix_cores = 1 when the
- * fused launch computes the tile products on the matrix cores (class-3 batches of 4..8 q8/128 columns; the same
- * bits as the v_dot4 kernel; the environment variable P8X_GEMV_MX, read at creation, overrides the choice for 2..8
- * columns: 0 the v_dot4 kernel, 1 the matrix cores). */
+ * fused launch computes the tile products on the matrix cores (class-3 batches of 4..8 q8/128 columns or 2..4 x16
+ * columns, whose planes count as two; the same bits as the v_dot4 kernel; the environment variable P8X_GEMV_MX, read
+ * at creation, overrides the choice from 2 multiplied columns: 0 the v_dot4 kernel, 1 the matrix cores). */
 typedef struct p8x_batch_info { int njobs, ncols, class_set, units, split_jobs, small_launch, waves, matrix_cores; } p8x_batch_info;
 int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out);
 

@@ -1176,11 +1176,11 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int uni
 // two halves' words into per-half operands (words 0..15: half 0, lanes 0..31 chunks 0..15 and lanes 32..63 chunks
 // 16..31; words 16..31 the same of half 1), so that MFMA i of half h reads words 16 h + 4 i .. + 3: K bytes
 // 16 i .. + 15 of the half in lanes 0..31 and 64 + 16 i .. in lanes 32..63. The activations come in a layout to
-// match (k_act_q8_128_mx_batch): per 256-block and column a 256-byte record (half 0, then half 1), the halves'
-// scales [block][column][2] after the records. A wave loads its next tile's records and scales with one to three
-// 16-byte loads per lane and, when it reaches that tile, copies them into its own LDS slot, from which lane
-// (column m, group g) reads its A operands (64 bytes at 64 g of each half) and lane (row j, group g) the scales of
-// columns 4 g .. 4 g + 3; so only 12 registers per tile in flight hold activations. The output lane (row j, group
+// match (k_act_q8_128_mx_batch, k_act_x16_batch<true>): per 256-block and column a 256-byte record (half 0, then half
+// 1), the halves' scales [block][column][2] after the records. A wave loads its next tile's records and scales with
+// one to three 16-byte loads per lane and, when it reaches that tile, copies them into its own LDS slot, from which
+// lane (column m, group g) reads its A operands (64 bytes at 64 g of each half) and lane (row j, group g) the scales
+// of columns 4 g .. 4 g + 3; so only 12 registers per tile in flight hold activations. The output lane (row j, group
 // g) holds columns 4 g .. 4 g + 3, accumulated per half as the broadcast kernel does (y_h += ((float)isum d) S tile
 // by tile, then half 0 + half 1): the same bits.
 constexpr uint32_t kMxRecBytes = 256;   // activation record per 256-block and column
@@ -1395,13 +1395,14 @@ int check_shared_input(const p8x_tensor *const *ts, int n, const float *x, size_
 int class_set(const size_t hist[8], bool in_order = true);
 int launch_gemv_wave(int ncols, int cm, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
                      hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
-// the matrix-core grouped launch (class 3, q8/128 activations in the k_act_q8_128_mx_batch layout), 2..8 columns
+// the matrix-core grouped launch (class 3, activations in the k_act_q8_128_mx_batch / k_act_x16_batch<true>
+// layout), 2..8 columns
 int launch_gemv_wave_mx(int ncols, const GemvJob *jobs, const uint32_t *ujob, int units, unsigned *ctr, const uint32_t *a2, hipStream_t st,
                         hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
-// batches the matrix-core kernel can run (class set, activation mode, columns), and from how many columns the plan
-// takes it (on the Qwen3-14B stack it is slower at 2 columns, even at 3, and faster from 4: 0.84 / 0.96 ms against
-// 0.92 / 1.43 ms per step at 4 / 8 columns)
-__host__ __device__ constexpr bool wave_mx(int cm, int act, int ncols) { return cm == kCmC3 && act == P8X_ACT_Q8_128 && ncols >= 2 && ncols <= 8; }
+// batches the matrix-core kernel can run (class set, columns it multiplies: x16 batches two per column), and from how
+// many columns the plan takes it (on the Qwen3-14B stack it is slower at 2 columns, even at 3, and faster from 4:
+// 0.84 / 0.96 ms against 0.92 / 1.43 ms per step at 4 / 8 columns)
+__host__ __device__ constexpr bool wave_mx(int cm, int ncv) { return cm == kCmC3 && ncv >= 2 && ncv <= 8; }
 constexpr int kMxMinCols = 4;
 
 }  // namespace p8x

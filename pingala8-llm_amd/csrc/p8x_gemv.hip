@@ -370,7 +370,9 @@ __global__ __launch_bounds__(256) void k_act_q8_128_mx_batch(const ActJob *__res
 
 // The x16 form of the batch prep (P8X_ACT_X16, the arithmetic of k_act_x16): grid (ceil(total blocks / 4), ncols),
 // column n's two planes written as virtual columns 2n (hi, scale 128 d) and 2n + 1 (lo, scale d) of the broadcast
-// layout, so the grouped kernel multiplies them as 2 ncols columns.
+// layout (MX false) or of the matrix-core kernel's records (MX true, 2 ncols virtual columns), so the grouped kernel
+// multiplies them as 2 ncols columns.
+template <bool MX>
 __global__ __launch_bounds__(256) void k_act_x16_batch(const ActJob *__restrict__ jobs, const uint32_t *__restrict__ blk_job, int total) {
     const int gb = 4 * blockIdx.x + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), n = blockIdx.y, lane = threadIdx.x & 63;
     if (gb >= total) return;
@@ -395,13 +397,20 @@ __global__ __launch_bounds__(256) void k_act_x16_batch(const ActJob *__restrict_
     const int hs = lane >> 5, t = lane & 31;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-        uint32_t *e = reinterpret_cast<uint32_t *>(J.q + ((size_t)(2 * n + p) * J.nb + b) * kBcastBlockBytes + 256 * hs + 16 * (t & 15));
-        if (t < 16) {
-            e[0] = p ? pl : ph;
-            e[2] = __builtin_bit_cast(uint32_t, p ? dd : 128.f * dd);
-            e[3] = 0u;
+        if constexpr (MX) {
+            const int ncv = 2 * (int)gridDim.y;
+            const size_t rec = (size_t)b * ncv + 2 * n + p;
+            reinterpret_cast<uint32_t *>(J.q + rec * kMxRecBytes + 128 * hs)[t] = p ? pl : ph;
+            if (t == 0) reinterpret_cast<float *>(J.q + (size_t)ncv * J.nb * kMxRecBytes)[2 * rec + hs] = p ? dd : 128.f * dd;
         } else {
-            e[1] = p ? pl : ph;
+            uint32_t *e = reinterpret_cast<uint32_t *>(J.q + ((size_t)(2 * n + p) * J.nb + b) * kBcastBlockBytes + 256 * hs + 16 * (t & 15));
+            if (t < 16) {
+                e[0] = p ? pl : ph;
+                e[2] = __builtin_bit_cast(uint32_t, p ? dd : 128.f * dd);
+                e[3] = 0u;
+            } else {
+                e[1] = p ? pl : ph;
+            }
         }
     }
 }
@@ -595,10 +604,11 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
     int blk0 = 0;
     std::vector<uint32_t> ablk;   // activation prep: 256-block -> job
     const int cm = class_set(hist);
-    // class-3 batches of kMxMinCols..8 columns run on the matrix cores; P8X_GEMV_MX in the environment overrides
-    // the choice for 2..8 columns (0: the v_dot4 kernel, 1: the matrix cores; the same bits either way)
+    // class-3 batches of kMxMinCols..8 columns (x16: virtual columns, two per column) run on the matrix cores;
+    // P8X_GEMV_MX in the environment overrides the choice for 2..8 columns (0: the v_dot4 kernel, 1: the matrix
+    // cores; the same bits either way)
     const char *mx_env = getenv("P8X_GEMV_MX");
-    const bool mx = wave_mx(cm, act, ncols) && (mx_env && (mx_env[0] == '0' || mx_env[0] == '1') ? mx_env[0] == '1' : ncols >= kMxMinCols);
+    const bool mx = wave_mx(cm, ncv) && (mx_env && (mx_env[0] == '0' || mx_env[0] == '1') ? mx_env[0] == '1' : ncv >= kMxMinCols);
     const int launch_waves = mx ? mx_wg_per_cu() * num_cus() * mx_waves() : wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
     // wave-independent units: (row group, whole K)
     std::vector<int> kcs(njobs);
@@ -766,7 +776,8 @@ int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *str
     hipEvent_t e0 = (hipEvent_t)ev_start, e1 = (hipEvent_t)ev_stop;
     if (stage == 0) {
         const dim3 grid((b->total_blocks + 3) / 4, b->ncols);
-        auto kern = b->act == P8X_ACT_X16 ? k_act_x16_batch : b->mx ? k_act_q8_128_mx_batch : k_act_q8_128_batch;
+        auto kern = b->act == P8X_ACT_X16 ? (b->mx ? k_act_x16_batch<true> : k_act_x16_batch<false>)
+                                          : b->mx ? k_act_q8_128_mx_batch : k_act_q8_128_batch;
         if (e0 || e1)
             hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, e0, e1, 0, (const ActJob *)b->d_act, (const uint32_t *)b->d_ablk, b->total_blocks);
         else
@@ -774,7 +785,7 @@ int p8x_gemv_batch_run_stage_timed(const p8x_gemv_batch *b, int stage, void *str
         return hip_check(hipGetLastError(), "batch activation prep launch");
     }
     if (stage == 1) {
-        if (b->mx) return launch_gemv_wave_mx(b->ncols, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
+        if (b->mx) return launch_gemv_wave_mx(b->ncv, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
         return launch_gemv_wave(b->ncv, b->cm, b->d_jobs, b->d_ujob, b->total_tasks, b->ctr, b->a2, st, e0, e1);
     }
     if (stage == 2) {   // partial rows to original rows with the clamp delta

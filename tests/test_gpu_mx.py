@@ -19,13 +19,13 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
 
 
-def run_batch(tensors, xs, rows, ncols, mx):
+def run_batch(tensors, xs, rows, ncols, mx, act=p8x.ACT_Q8_128):
     """one grouped launch with P8X_GEMV_MX set to 1 (mx) or 0 (the v_dot4 kernel) while the batch is created"""
     ys = [p8x.DeviceBuffer(4 * ncols * r) for r in rows]
     old = os.environ.get("P8X_GEMV_MX")
     os.environ["P8X_GEMV_MX"] = "1" if mx else "0"
     try:
-        batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols)
+        batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols, act=act)
     finally:
         if old is None:
             os.environ.pop("P8X_GEMV_MX", None)
@@ -73,9 +73,37 @@ def test_mx_batch_matches_dot4_and_oracle(ncols):
         x.free()
 
 
+@pytest.mark.parametrize("ncols", [1, 2, 3, 4])
+def test_mx_batch_x16_matches_dot4_and_oracle(ncols):
+    """x16 activations (both planes as virtual columns): the matrix-core launch gives the v_dot4 launch's bits, and
+    each column is within 1e-5 of the oracle's x16 GEMV"""
+    shapes = [(1024, 4096), (512, 14336), (32, 256)]
+    rng = np.random.default_rng(700 + ncols)
+    tensors, orcs, xs, hx = [], [], [], []
+    for i, (rows, K) in enumerate(shapes):
+        slot = p8x.synth_random(950 + 5 * ncols + i, rows, K, class_p=C3, nd=2)
+        tensors.append(p8x.Tensor(slot, rows, K))
+        orcs.append(O.Oracle(slot, rows, K))
+        X = rng.standard_normal((ncols, K)).astype(np.float32)
+        hx.append(X)
+        xs.append(p8x.DeviceBuffer.from_numpy(X))
+    rows = [r for r, _ in shapes]
+    info_mx, y_mx = run_batch(tensors, xs, rows, ncols, True, act=p8x.ACT_X16)
+    info_d4, y_d4 = run_batch(tensors, xs, rows, ncols, False, act=p8x.ACT_X16)
+    assert info_mx["matrix_cores"] == 1 and info_d4["matrix_cores"] == 0
+    for i in range(len(shapes)):
+        assert np.array_equal(y_mx[i].view(np.uint32), y_d4[i].view(np.uint32)), i
+        for n in range(ncols):
+            assert rel_l2(y_mx[i][n], orcs[i].gemv_f64(hx[i][n], act="x16")) < 1e-5, (i, n)
+    for t in tensors:
+        t.release()
+    for x in xs:
+        x.free()
+
+
 def test_mx_plan_choice():
-    """by default the matrix cores take class-3 q8/128 batches of 4..8 columns; one column, 2 or 3 columns, a
-    non-class-3 set and x16 activations stay on the v_dot4 kernel"""
+    """by default the matrix cores take class-3 batches of 4..8 multiplied columns (q8/128 columns, or x16 columns
+    with their two planes); one to three, and non-class-3 sets, stay on the v_dot4 kernel"""
     saved = os.environ.pop("P8X_GEMV_MX", None)
     rows, K = 256, 2048
     t3 = p8x.Tensor(p8x.synth_random(31, rows, K, class_p=C3, nd=1), rows, K)
@@ -83,8 +111,8 @@ def test_mx_plan_choice():
     x8 = p8x.DeviceBuffer.from_numpy(np.ones((8, K), np.float32))
     y8 = p8x.DeviceBuffer(4 * 8 * rows)
     for ts, ncols, act, want in (([t3], 1, p8x.ACT_Q8_128, 0), ([t3], 2, p8x.ACT_Q8_128, 0), ([t3], 3, p8x.ACT_Q8_128, 0),
-                                 ([t6], 4, p8x.ACT_Q8_128, 0), ([t3], 4, p8x.ACT_X16, 0), ([t3], 4, p8x.ACT_Q8_128, 1),
-                                 ([t3], 8, p8x.ACT_Q8_128, 1)):
+                                 ([t6], 4, p8x.ACT_Q8_128, 0), ([t3], 4, p8x.ACT_Q8_128, 1), ([t3], 8, p8x.ACT_Q8_128, 1),
+                                 ([t3], 1, p8x.ACT_X16, 0), ([t3], 2, p8x.ACT_X16, 1), ([t3], 4, p8x.ACT_X16, 1)):
         b = p8x.GemvBatch(ts, [x8], [y8], ncols=ncols, act=act)
         assert b.info()["matrix_cores"] == want, (ncols, act)
         b.release()
