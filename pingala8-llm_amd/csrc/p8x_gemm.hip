@@ -139,6 +139,13 @@ __host__ __device__ constexpr int mm_tok(int nti) { return 32 * nti; }
 // 64 KB x' buffers (160 KB of LDS in all).
 __host__ __device__ constexpr int mm_tab_words(int cm) { return cm == kMmCmC3 ? kTabWords / 2 : kTabWords; }
 __host__ __device__ constexpr int mm_tab_shift(int cm) { return cm == kMmCmC3 ? 1 : 0; }
+// The class-3 kernel of the 128-token tile keeps its 16 copies as fp16 instead: entry (f, h, c) = the four weights
+// A[f] + h c as fp16 (8 bytes) at byte f 256 + h 128 + 8 c, the 32-copy byte address with the lane field doubled,
+// so a lookup is one 8-byte read and the decode of a 4-weight chunk two packed multiplies by S (the offset-binary
+// conversion moves into the table build). 64 KB, beside the 128-token tile's two 32 KB x' buffers; the 256-token
+// tile's 64 KB buffers leave no room for it.
+__host__ __device__ constexpr bool mm_f16_tab(int cm, int nti) { return cm == kMmCmC3 && nti == 4; }
+__host__ __device__ constexpr int mm_tab_words(int cm, int nti) { return mm_f16_tab(cm, nti) ? kTabWords : mm_tab_words(cm); }
 
 
 // x' half-block tile in LDS: half sh of block b holds, per token, columns 128 kh + 64 sh + 8 c8 + (0..7) as
@@ -301,20 +308,37 @@ __device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const A
         half2v s2[NTJ];
 #pragma unroll
         for (int tj = 0; tj < NTJ; ++tj) s2[tj] = half2v{__builtin_bit_cast(_Float16, (uint16_t)ls[tj].s), __builtin_bit_cast(_Float16, (uint16_t)ls[tj].s)};
+        constexpr bool F16T = mm_f16_tab(CM, NTI);
         auto lookups = [&](int s, uint32_t (&W)[NTJ][2][3]) {
 #pragma unroll
             for (int tj = 0; tj < NTJ; ++tj) {
                 const uint32_t hq = coset_bytes(ls[tj].H, bankbytes, s >> 1);
-                W[tj][0][0] = lds_word(tab, ls[tj].template addr<kMmMain, 0>(2 * s, hq) >> mm_tab_shift(CM));
-                W[tj][1][0] = lds_word(tab, ls[tj].template addr<kMmMain, 0>(2 * s + 1, hq) >> mm_tab_shift(CM));
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint32_t a = ls[tj].template addr<kMmMain, 0>(2 * s + u, hq);
+                    if constexpr (F16T) {   // the chunk's four fp16 weights
+                        const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(tab) + a);
+                        W[tj][u][0] = v.x;
+                        W[tj][u][1] = v.y;
+                    } else {
+                        W[tj][u][0] = lds_word(tab, a >> mm_tab_shift(CM));
+                    }
+                }
             }
         };
         auto decode = [&](const uint32_t (&W)[NTJ][2][3], half8v (&B)[NTJ]) {
 #pragma unroll
             for (int tj = 0; tj < NTJ; ++tj) {
                 half2v a, b, c, d;
-                weights_chunk<kMmMain>(W[tj][0], s2[tj], a, b);
-                weights_chunk<kMmMain>(W[tj][1], s2[tj], c, d);
+                if constexpr (F16T) {
+                    a = __builtin_bit_cast(half2v, W[tj][0][0]) * s2[tj];
+                    b = __builtin_bit_cast(half2v, W[tj][0][1]) * s2[tj];
+                    c = __builtin_bit_cast(half2v, W[tj][1][0]) * s2[tj];
+                    d = __builtin_bit_cast(half2v, W[tj][1][1]) * s2[tj];
+                } else {
+                    weights_chunk<kMmMain>(W[tj][0], s2[tj], a, b);
+                    weights_chunk<kMmMain>(W[tj][1], s2[tj], c, d);
+                }
                 B[tj][0] = a.x; B[tj][1] = a.y; B[tj][2] = b.x; B[tj][3] = b.y;
                 B[tj][4] = c.x; B[tj][5] = c.y; B[tj][6] = d.x; B[tj][7] = d.y;
             }
@@ -346,7 +370,7 @@ __device__ __forceinline__ void mm_half(const _Float16 *__restrict__ xb, const A
             }
             if (s8 < 7) {
                 constexpr int HM = NTI * NTJ / 2;                          // MFMAs per half of the step
-                constexpr int DV = (12 * NTJ + HM - 1) / HM;               // decode VALU per MFMA
+                constexpr int DV = ((F16T ? 4 : 12) * NTJ + HM - 1) / HM;  // decode VALU per MFMA
                 constexpr int RD = (NTI + 2 * NTJ + HM - 1) / HM;          // LDS reads per MFMA
 #pragma unroll
                 for (int i = 0; i < HM; ++i) {   // decode
@@ -388,14 +412,15 @@ template <int CM, int NTI>
 __global__ __launch_bounds__(64 * mm_waves()) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_mm(MmJob J) {
     constexpr int NWMAX = mm_nwmax(CM), NWAVES = mm_waves(), NTJ = mm_ntj(), kMmThreads = 64 * NWAVES;
-    constexpr int kMmRows = mm_rows(), TOK = mm_tok(NTI), TABW = mm_tab_words(CM);
-    __shared__ uint32_t tab[TABW];   // first: LDS address 0, replicated coset table (bytes offset by 128)
+    constexpr int kMmRows = mm_rows(), TOK = mm_tok(NTI), TABW = mm_tab_words(CM, NTI);
+    constexpr bool F16T = mm_f16_tab(CM, NTI);
+    __shared__ uint32_t tab[TABW];   // first: LDS address 0, replicated coset table (bytes offset by 128, or fp16)
     __shared__ __attribute__((aligned(16))) _Float16 xs0[TOK * 128];   // half 0 of a block
     __shared__ __attribute__((aligned(16))) _Float16 xs1[TOK * 128];   // half 1
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, kh = lane >> 5;
     // lane field of the table byte addresses: the lane's copy, at the 32-copy spacing (halved on read for 16 copies)
-    const uint32_t bankbytes = (uint32_t)((TABW == kTabWords ? j : (j & 15) << 1) << 2) * 0x01010101u;
+    const uint32_t bankbytes = (uint32_t)((TABW == kTabWords && !F16T ? j : (j & 15) << 1) << 2) * 0x01010101u;
 #ifdef P8X_TIMELINE
     const unsigned long long tl_start = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -424,7 +449,19 @@ void k_mm(MmJob J) {
     XStage<NWAVES, TOK> xq;
     mm_fetch<NWAVES, TOK>(J, xq, tok0, b0, 0, w, lane);
     mm_issue<CM>(J, raw, cl, g, b0, j, kh);
-    {
+    if constexpr (F16T) {
+        // 16-byte piece i = copies 2 (i % 8), 2 (i % 8) + 1 of entry (f, h) = (i / 16, (i / 8) % 2): the four int8
+        // A[f] + h c as fp16 (exact), lo pair then hi pair
+        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
+        for (int i = tid; i < TABW / 4; i += kMmThreads) {
+            const uint32_t v = J.a2[((i >> 3) & 1) * 256 + (i >> 4)];
+            half2v lo, hi;
+            lo.x = (_Float16)(float)(int8_t)(v & 0xFFu); lo.y = (_Float16)(float)(int8_t)((v >> 8) & 0xFFu);
+            hi.x = (_Float16)(float)(int8_t)((v >> 16) & 0xFFu); hi.y = (_Float16)(float)(int8_t)(v >> 24);
+            const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
+            t4[i] = make_uint4(l, h, l, h);
+        }
+    } else {
         // word (f, h, c) = A[f] + h c bytes (offset by 128) at f (TABW / 256) + h (TABW / 512) + c, c < TABW / 512
         constexpr int CPS = TABW / 512;   // copies
         uint4 *t4 = reinterpret_cast<uint4 *>(tab);
