@@ -162,9 +162,10 @@ def timed_steps(run, stream, warmup, steps):
     return e0.elapsed_ms(e1) / steps
 
 
-def measure_qwen14b_columns(stream, steps, col_list=(1, 2, 4, 8)):
+def measure_qwen14b_columns(stream, steps, col_list=(1, 2, 4, 8), kernel=p8x.GEMV_KERNEL_AUTO):
     """Qwen3-14B (40 layers, 280 linears, all class 3) streamed by one grouped launch per step at 1/2/4/8
-    activation columns sharing the weights: GB/s of the weight stream and columns (tokens) per second"""
+    activation columns sharing the weights: GB/s of the weight stream and columns (tokens) per second. kernel: the
+    fused launch's kernel for more than one column (the plan's choice by default; p8x_gemv_batch_create_ex)"""
     plan = [(r, K) for _ in range(40) for (_, r, K) in QWEN3_14B_LAYER]
     tensors = [p8x.Tensor(p8x.synth_random(1000 + i, r, K, nd=1), r, K) for i, (r, K) in enumerate(plan)]
     stream_bytes = sum(t.stream_bytes for t in tensors)
@@ -174,7 +175,7 @@ def measure_qwen14b_columns(stream, steps, col_list=(1, 2, 4, 8)):
     for n in col_list:
         xs = {K: p8x.DeviceBuffer.from_numpy(rng.standard_normal(n * K).astype(np.float32)) for K in sorted({t.K for t in tensors})}
         ys = [p8x.DeviceBuffer(4 * n * t.rows) for t in tensors]
-        batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ys, ncols=n)
+        batch = p8x.GemvBatch(tensors, [xs[t.K] for t in tensors], ys, ncols=n, kernel=kernel if n > 1 else p8x.GEMV_KERNEL_AUTO)
         ms = timed_steps(lambda: batch.run(stream), stream, 40, steps)
         out[f"batch_{n}"] = {"ms_per_step": round(ms, 4), "GB/s": round(stream_bytes / (ms * 1e-3) / 1e9, 1),
                              "tokens_per_s": round(n / (ms * 1e-3), 1)}
@@ -538,6 +539,8 @@ def main():
     ap.add_argument("--no-qwen", action="store_true", help="skip the Qwen3-14B multi-column and Qwen3-4B layer lines")
     ap.add_argument("--no-mix", action="store_true", help="skip the b4 class-mix line")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replays of the per-linear and dependent steps (the one-launch step still runs)")
+    ap.add_argument("--gemv-kernel", choices=("auto", "dot4", "mfma"), default="auto",
+                    help="the Qwen3-14B column runs' fused kernel from two columns on (default: the batch plan's choice)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -611,7 +614,8 @@ def main():
         batch.release()
         for t in tensors:
             t.release()
-        qwen14b = measure_qwen14b_columns(stream, max(10, args.steps // 4))
+        kern = {"auto": p8x.GEMV_KERNEL_AUTO, "dot4": p8x.GEMV_KERNEL_DOT4, "mfma": p8x.GEMV_KERNEL_MFMA}[args.gemv_kernel]
+        qwen14b = measure_qwen14b_columns(stream, max(10, args.steps // 4), kernel=kern)
         qwen4b = measure_qwen4b_layer(stream, max(10, args.steps // 4))
         quant4096 = measure_quantized_4096(stream, max(10, args.steps // 10))
     cpu = cpu_baseline(host0, args.cpu_seconds) if not args.no_cpu and host0 else None

@@ -221,6 +221,15 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
  * column's planes and then adds the clamp delta: p8x_mul_mat_vec_act's x16 values) */
 int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                               float *const *y, const size_t *ldy, int njobs, int ncols, int act, p8x_gemv_batch **out);
+/* No counterpart in the reference: the same with the fused launch's kernel chosen by the caller (for comparisons):
+ * P8X_GEMV_KERNEL_AUTO (the plan's choice, as p8x_gemv_batch_create_act), P8X_GEMV_KERNEL_DOT4 (v_dot4 products) or
+ * P8X_GEMV_KERNEL_MFMA (the matrix-core kernel: class-3 batches of 2..8 multiplied columns, else P8X_ERR_UNSUPPORTED).
+ * Both kernels give the same bits. */
+#define P8X_GEMV_KERNEL_AUTO 0
+#define P8X_GEMV_KERNEL_DOT4 1
+#define P8X_GEMV_KERNEL_MFMA 2
+int p8x_gemv_batch_create_ex(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                             float *const *y, const size_t *ldy, int njobs, int ncols, int act, int kernel, p8x_gemv_batch **out);
 int p8x_gemv_batch_run(const p8x_gemv_batch *b, void *stream);
 /* the launches of p8x_gemv_batch_run separately: stage 0 = activation prep, 1 = fused decode + GEMV (sorted-row
  * partials per K-chunk and column), 2 = partials to original rows with the clamp delta */
@@ -233,9 +242,8 @@ void p8x_gemv_batch_release(p8x_gemv_batch *b);
 /* The launch plan of a batch: work units (a 32-row group over a K-chunk), jobs cut along K, waves of the launch,
  * class_set (bit c: tile class c is decoded), small_launch = 1 when the batch had fewer whole-K units than two
  * rounds of the launch's waves and every job was cut into units of two or more blocks, matrix_cores = 1 when the
- * fused launch computes the tile products on the matrix cores (class-3 batches of 4..8 q8/128 columns or 2..4 x16
- * columns, whose planes count as two; the same bits as the v_dot4 kernel; the environment variable P8X_GEMV_MX, read
- * at creation, overrides the choice from 2 multiplied columns: 0 the v_dot4 kernel, 1 the matrix cores). */
+ * fused launch computes the tile products on the matrix cores (the plan's choice: class-3 batches of 4..8 q8/128
+ * columns or 2..4 x16 columns, whose planes count as two; p8x_gemv_batch_create_ex chooses explicitly). */
 typedef struct p8x_batch_info { int njobs, ncols, class_set, units, split_jobs, small_launch, waves, matrix_cores; } p8x_batch_info;
 int p8x_gemv_batch_info(const p8x_gemv_batch *b, p8x_batch_info *out);
 

@@ -17,7 +17,6 @@
 
 #include <algorithm>
 #include <atomic>
-#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -576,6 +575,13 @@ int p8x_gemv_batch_create(const p8x_tensor *const *tensors, const float *const *
 
 int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
                               float *const *y, const size_t *ldy, int njobs, int ncols, int act, p8x_gemv_batch **out) {
+    return p8x_gemv_batch_create_ex(tensors, x, ldx, y, ldy, njobs, ncols, act, P8X_GEMV_KERNEL_AUTO, out);
+}
+
+int p8x_gemv_batch_create_ex(const p8x_tensor *const *tensors, const float *const *x, const size_t *ldx,
+                             float *const *y, const size_t *ldy, int njobs, int ncols, int act, int kernel, p8x_gemv_batch **out) {
+    if (kernel != P8X_GEMV_KERNEL_AUTO && kernel != P8X_GEMV_KERNEL_DOT4 && kernel != P8X_GEMV_KERNEL_MFMA)
+        return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: kernel %d", kernel);
     if (!tensors || !x || !ldx || !y || !ldy || !out || njobs < 1) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: bad arguments");
     if (njobs >= (1 << 24)) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: %d jobs (at most %d)", njobs, (1 << 24) - 1);
     if (ncols < 1 || ncols > P8X_MAX_COLS) return set_error(P8X_ERR_ARG, "p8x_gemv_batch_create: ncols %d", ncols);
@@ -604,11 +610,11 @@ int p8x_gemv_batch_create_act(const p8x_tensor *const *tensors, const float *con
     int blk0 = 0;
     std::vector<uint32_t> ablk;   // activation prep: 256-block -> job
     const int cm = class_set(hist);
-    // class-3 batches of kMxMinCols..8 columns (x16: virtual columns, two per column) run on the matrix cores;
-    // P8X_GEMV_MX in the environment overrides the choice for 2..8 columns (0: the v_dot4 kernel, 1: the matrix
-    // cores; the same bits either way)
-    const char *mx_env = getenv("P8X_GEMV_MX");
-    const bool mx = wave_mx(cm, ncv) && (mx_env && (mx_env[0] == '0' || mx_env[0] == '1') ? mx_env[0] == '1' : ncv >= kMxMinCols);
+    // class-3 batches of kMxMinCols..8 columns (x16: virtual columns, two per column) run on the matrix cores unless
+    // the caller chose a kernel (the same bits either way)
+    if (kernel == P8X_GEMV_KERNEL_MFMA && !wave_mx(cm, ncv))
+        return set_error(P8X_ERR_UNSUPPORTED, "p8x_gemv_batch_create: the matrix-core kernel takes class-3 batches of 2..8 multiplied columns");
+    const bool mx = kernel == P8X_GEMV_KERNEL_MFMA || (kernel == P8X_GEMV_KERNEL_AUTO && wave_mx(cm, ncv) && ncv >= kMxMinCols);
     const int launch_waves = mx ? mx_wg_per_cu() * num_cus() * mx_waves() : wave_wg_per_cu(cm, ncv) * num_cus() * wave_waves(cm, ncv);
     // wave-independent units: (row group, whole K)
     std::vector<int> kcs(njobs);

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libp8x.so")
 P8X_OK, P8X_ERR_ARG, P8X_ERR_FORMAT, P8X_ERR_HIP, P8X_ERR_UNSUPPORTED, P8X_ERR_NOMEM = range(6)
 F32, F16, BF16, I16 = 0, 1, 2, 3
 ACT_Q8_128, ACT_Q8_1, ACT_X16 = 0, 1, 2
+GEMV_KERNEL_AUTO, GEMV_KERNEL_DOT4, GEMV_KERNEL_MFMA = 0, 1, 2   # p8x_gemv_batch_create_ex
 MAX_COLS = 8
 VR3_TAG = 0x56523300
 
@@ -28,7 +29,7 @@ EXPORTS = [
     "p8x_gemv_batch_release", "p8x_gemv_batch_info", "p8x_mul_mat_noalloc",
     "p8x_vr_open", "p8x_vr_count", "p8x_vr_find", "p8x_vr_describe", "p8x_vr_load", "p8x_vr_close", "p8x_vr3_rows",
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_mul_mat_vec_multi_act",
-    "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_graph_begin", "p8x_decode_tiles",
+    "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_gemv_batch_create_ex", "p8x_graph_begin", "p8x_decode_tiles",
     "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
     "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_run", "p8x_step_check", "p8x_step_info",
     "p8x_step_release",
@@ -138,6 +139,7 @@ def lib():
     L.p8x_step_release.argtypes = [vp]; L.p8x_step_release.restype = None
     L.p8x_gemv_batch_create.argtypes = [vp, vp, vp, vp, vp, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_create_act.argtypes = [vp, vp, vp, vp, vp, i, i, i, ctypes.POINTER(vp)]
+    L.p8x_gemv_batch_create_ex.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, ctypes.POINTER(vp)]
     L.p8x_gemv_batch_run.argtypes = [vp, vp]
     L.p8x_gemv_batch_run_stage.argtypes = [vp, i, vp]
     L.p8x_gemv_batch_run_stage_timed.argtypes = [vp, i, vp, vp, vp]
@@ -821,7 +823,7 @@ class GemvBatch:
 
     stages = 3   # activation prep, fused decode + GEMV, finishing (original rows, clamp delta)
 
-    def __init__(self, tensors, xs, ys, ncols=1, act=ACT_Q8_128):
+    def __init__(self, tensors, xs, ys, ncols=1, act=ACT_Q8_128, kernel=0):
         n = len(tensors)
         T = (ctypes.c_void_p * n)(*[t.h.value for t in tensors])
         X = (ctypes.c_void_p * n)(*[x.addr for x in xs])
@@ -829,7 +831,7 @@ class GemvBatch:
         LX = (ctypes.c_size_t * n)(*[t.K for t in tensors])
         LY = (ctypes.c_size_t * n)(*[t.rows for t in tensors])
         self.h = ctypes.c_void_p()
-        check(lib().p8x_gemv_batch_create_act(T, X, LX, Y, LY, n, ncols, act, ctypes.byref(self.h)), "p8x_gemv_batch_create")
+        check(lib().p8x_gemv_batch_create_ex(T, X, LX, Y, LY, n, ncols, act, kernel, ctypes.byref(self.h)), "p8x_gemv_batch_create")
         self._keep = (tensors, xs, ys)
 
     def info(self):

@@ -1,8 +1,6 @@
 """Grouped GEMV on the matrix cores (k_gemv_wave_mx: class-3 batches of 2..8 q8/128 columns, tile products as
 v_mfma_i32_32x32x32_i8) against the v_dot4 kernel of the same batch (bit for bit: the integer tile sums are exact
 and the float steps are the same) and against the fp64 oracle."""
-import os
-
 import numpy as np
 import pytest
 
@@ -20,17 +18,9 @@ def rel_l2(a, b):
 
 
 def run_batch(tensors, xs, rows, ncols, mx, act=p8x.ACT_Q8_128):
-    """one grouped launch with P8X_GEMV_MX set to 1 (mx) or 0 (the v_dot4 kernel) while the batch is created"""
+    """one grouped launch on the matrix-core kernel (mx) or the v_dot4 kernel, chosen at creation"""
     ys = [p8x.DeviceBuffer(4 * ncols * r) for r in rows]
-    old = os.environ.get("P8X_GEMV_MX")
-    os.environ["P8X_GEMV_MX"] = "1" if mx else "0"
-    try:
-        batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols, act=act)
-    finally:
-        if old is None:
-            os.environ.pop("P8X_GEMV_MX", None)
-        else:
-            os.environ["P8X_GEMV_MX"] = old
+    batch = p8x.GemvBatch(tensors, xs, ys, ncols=ncols, act=act, kernel=p8x.GEMV_KERNEL_MFMA if mx else p8x.GEMV_KERNEL_DOT4)
     info = batch.info()
     out = []
     for rep in range(2):   # twice: the unit counters are put back for the next launch
@@ -104,7 +94,6 @@ def test_mx_batch_x16_matches_dot4_and_oracle(ncols):
 def test_mx_plan_choice():
     """by default the matrix cores take class-3 batches of 4..8 multiplied columns (q8/128 columns, or x16 columns
     with their two planes); one to three, and non-class-3 sets, stay on the v_dot4 kernel"""
-    saved = os.environ.pop("P8X_GEMV_MX", None)
     rows, K = 256, 2048
     t3 = p8x.Tensor(p8x.synth_random(31, rows, K, class_p=C3, nd=1), rows, K)
     t6 = p8x.Tensor(p8x.synth_random(32, rows, K, class_p=(0, 0, 0, 0, 0, 0, 1, 0), nd=1), rows, K)
@@ -120,5 +109,22 @@ def test_mx_plan_choice():
     t6.release()
     x8.free()
     y8.free()
-    if saved is not None:
-        os.environ["P8X_GEMV_MX"] = saved
+
+
+def test_mx_kernel_choice_rejected_outside_its_set():
+    """asking for the matrix-core kernel where it does not apply (one multiplied column, a non-class-3 set) fails at
+    creation; an unknown kernel value too"""
+    rows, K = 256, 2048
+    t3 = p8x.Tensor(p8x.synth_random(33, rows, K, class_p=C3, nd=1), rows, K)
+    t6 = p8x.Tensor(p8x.synth_random(34, rows, K, class_p=(0, 0, 0, 0, 0, 0, 1, 0), nd=1), rows, K)
+    x = p8x.DeviceBuffer.from_numpy(np.ones((8, K), np.float32))
+    y = p8x.DeviceBuffer(4 * 8 * rows)
+    for ts, ncols in (([t3], 1), ([t6], 4)):
+        with pytest.raises(p8x.P8xError, match="matrix-core kernel"):
+            p8x.GemvBatch(ts, [x], [y], ncols=ncols, kernel=p8x.GEMV_KERNEL_MFMA)
+    with pytest.raises(p8x.P8xError, match="kernel 7"):
+        p8x.GemvBatch([t3], [x], [y], ncols=2, kernel=7)
+    t3.release()
+    t6.release()
+    x.free()
+    y.free()
