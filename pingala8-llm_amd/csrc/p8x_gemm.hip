@@ -79,7 +79,8 @@ struct MmJob {
     const _Float16 *xr;     // x' [N][K]
     float *y; unsigned ldy; // direct output (original rows = sorted rows, one K range)
     float *ws;              // sorted-row planes [nsplit][N][rows] otherwise
-    const uint32_t *a2;     // [2][256] coset table words (A[f] + h c), h-major
+    const uint32_t *a2;     // [2][256] coset table words (A[f] + h c), h-major, then the same as fp16: entry 2 f + h,
+                            // 4 halves
     int N, rows, K, nb, ng;
     int tiles_m, tiles_n, nsplit, kper, direct;
 #ifdef P8X_TIMELINE
@@ -449,27 +450,30 @@ void k_mm(MmJob J) {
     XStage<NWAVES, TOK> xq;
     mm_fetch<NWAVES, TOK>(J, xq, tok0, b0, 0, w, lane);
     mm_issue<CM>(J, raw, cl, g, b0, j, kh);
+    // the table build: every thread's loads first, then its stores (one memory round trip, not one per piece)
+    constexpr int TPT = TABW / 4 / kMmThreads;   // 16-byte pieces per thread
+    static_assert(TABW / 4 % kMmThreads == 0, "whole pieces per thread");
+    uint4 *t4 = reinterpret_cast<uint4 *>(tab);
     if constexpr (F16T) {
-        // 16-byte piece i = copies 2 (i % 8), 2 (i % 8) + 1 of entry (f, h) = (i / 16, (i / 8) % 2): the four int8
-        // A[f] + h c as fp16 (exact), lo pair then hi pair
-        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
-        for (int i = tid; i < TABW / 4; i += kMmThreads) {
-            const uint32_t v = J.a2[((i >> 3) & 1) * 256 + (i >> 4)];
-            half2v lo, hi;
-            lo.x = (_Float16)(float)(int8_t)(v & 0xFFu); lo.y = (_Float16)(float)(int8_t)((v >> 8) & 0xFFu);
-            hi.x = (_Float16)(float)(int8_t)((v >> 16) & 0xFFu); hi.y = (_Float16)(float)(int8_t)(v >> 24);
-            const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
-            t4[i] = make_uint4(l, h, l, h);
-        }
+        // 16-byte piece i = copies 2 (i % 8), 2 (i % 8) + 1 of entry 2 f + h = i / 8: the four A[f] + h c as fp16
+        // (the fp16 entries the tensor's tables carry after the words)
+        const uint2 *e16 = reinterpret_cast<const uint2 *>(J.a2 + 512);
+        uint2 v[TPT];
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) v[k] = e16[(tid + k * kMmThreads) >> 3];
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) t4[tid + k * kMmThreads] = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
     } else {
         // word (f, h, c) = A[f] + h c bytes (offset by 128) at f (TABW / 256) + h (TABW / 512) + c, c < TABW / 512
         constexpr int CPS = TABW / 512;   // copies
-        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
-        for (int i = tid; i < TABW / 4; i += kMmThreads) {
-            const int f = (4 * i) / (2 * CPS), h = ((4 * i) / CPS) & 1;
-            const uint32_t v = J.a2[h * 256 + f] ^ 0x80808080u;
-            t4[i] = make_uint4(v, v, v, v);
+        uint32_t v[TPT];
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) {
+            const int i = tid + k * kMmThreads, f = (4 * i) / (2 * CPS), h = ((4 * i) / CPS) & 1;
+            v[k] = J.a2[h * 256 + f] ^ 0x80808080u;
         }
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) t4[tid + k * kMmThreads] = make_uint4(v[k], v[k], v[k], v[k]);
     }
     mm_put<NWAVES, TOK>(xq, xs0, w, lane);
     mm_prepare<CM>(ls, cl, raw);

@@ -219,6 +219,16 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
         a2[f] = hdr[f];
         a2[256 + f] = add_bytes(hdr[f], hdr[512]);
     }
+    // the same entries as four fp16 each (exact: |v| <= 128), entry 2 f + h, behind the words in the device copy
+    // (the prompt GEMM's fp16 table replicates them)
+    std::vector<uint16_t> a2h(512 * 4);
+    for (int r = 0; r < 512; ++r)
+        for (int e = 0; e < 4; ++e) {
+            const int v = (int8_t)(a2[(r & 1) * 256 + (r >> 1)] >> (8 * e));
+            const unsigned a = (unsigned)(v < 0 ? -v : v);
+            const int ex = a ? 31 - __builtin_clz(a) : 0;
+            a2h[4 * r + e] = a ? (uint16_t)((v < 0 ? 0x8000u : 0u) | (unsigned)(ex + 15) << 10 | ((a << (10 - ex)) & 0x3FFu)) : 0;
+        }
     std::vector<float> ic(K);
     for (int k = 0; k < K; ++k) ic[k] = (float)sg[k & 255] / half_to_float(c16[k]);
     uint64_t ic_hash = 1469598103934665603ull;   // FNV-1a over the rotation's bytes (K included)
@@ -312,7 +322,7 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->Sg, 64 * nt, "regrouped scales"))) return fail(rc);
     hipLaunchKernelGGL(k_regroup_scales, dim3((unsigned)((32 * nt + 255) / 256)), dim3(256), 0, 0, t->S, t->Sg, nb, rows, 32 * nt);
     if ((rc = hip_check(hipGetLastError(), "p8x_prepare: regroup scales"))) return fail(rc);
-    if ((rc = alloc((void **)&t->a2, 512 * 4, "tables"))) return fail(rc);
+    if ((rc = alloc((void **)&t->a2, 512 * 4 + 512 * 8, "tables"))) return fail(rc);
     if ((rc = alloc((void **)&t->ic, 4 * (size_t)K, "ic"))) return fail(rc);
     if ((rc = alloc((void **)&t->cp, 4 * (size_t)(rows + 1), "delta rows"))) return fail(rc);
     if ((rc = alloc((void **)&t->cc, 2 * (size_t)nd, "delta cols"))) return fail(rc);
@@ -350,7 +360,8 @@ int p8x_prepare(const void *slot, size_t n, int rows, int K, int on_device, p8x_
     if ((rc = alloc((void **)&t->drows, 4 * std::max<size_t>(1, drows.size()), "delta row list"))) return fail(rc);
     if (!drows.empty() && (rc = hip_check(hipMemcpy(t->drows, drows.data(), 4 * drows.size(), hipMemcpyHostToDevice), "p8x_prepare: delta rows")))
         return fail(rc);
-    if ((rc = hip_check(hipMemcpy(t->a2, a2.data(), 512 * 4, hipMemcpyHostToDevice), "p8x_prepare: tables"))) return fail(rc);
+    if ((rc = hip_check(hipMemcpy(t->a2, a2.data(), 512 * 4, hipMemcpyHostToDevice), "p8x_prepare: tables")) ||
+        (rc = hip_check(hipMemcpy(t->a2 + 512, a2h.data(), 512 * 8, hipMemcpyHostToDevice), "p8x_prepare: tables"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->ic, ic.data(), 4 * (size_t)K, hipMemcpyHostToDevice), "p8x_prepare: ic"))) return fail(rc);
     if ((rc = hip_check(hipMemcpy(t->cp, cp.data(), 4 * (size_t)(rows + 1), hipMemcpyHostToDevice), "p8x_prepare: csr"))) return fail(rc);
     if (nd) {

@@ -33,7 +33,7 @@ struct p8x_tensor {
     uint16_t *prmd = nullptr;        // sorted row -> original row, bit 15 set when that row carries clamp-delta entries
     bool prm_identity = false;
     // device metadata built at prepare
-    uint32_t *a2 = nullptr;          // [2][256]: A[f] + h c (bytewise), h-major
+    uint32_t *a2 = nullptr;          // [2][256]: A[f] + h c (bytewise), h-major; then the same as fp16 [256][2][4]
     float *ic = nullptr;             // sg / c per column [K]
     int *cp = nullptr;               // delta CSR by original row [rows + 1]
     uint16_t *cc = nullptr;          // [nd]
