@@ -1171,8 +1171,8 @@ static int launch_gemv_wave_t(const GemvJob *jobs, const uint32_t *ujob, int uni
 // 2..8 columns of class-3 tiles in grouped launches. A tile's integer products form a small matrix product,
 // (32 rows x 128 K) x (128 K x columns) per 128-column half, which v_mfma_i32_32x32x32_i8 computes with the
 // looked-up codewords as the B operand (n = row = lane & 31) and the activations as A (m = column; rows of A past
-// the batch read a zero line): per tile 8 MFMAs replace 32 v_dot4 per column and lane. Lane (row j, half hs) looks up
-// its 32 codewords as the broadcast kernel does; one v_permlane32_swap per pair (chunk k, chunk k + 16) turns the
+// the batch are zeros): per tile 8 MFMAs replace 32 v_dot4 per column and lane. Lane (row j, half hs) looks up its
+// 32 codewords as the broadcast kernel does; one v_permlane32_swap per pair (chunk k, chunk k + 16) turns the
 // two halves' words into per-half operands (words 0..15: half 0, lanes 0..31 chunks 0..15 and lanes 32..63 chunks
 // 16..31; words 16..31 the same of half 1), so that MFMA i of half h reads words 16 h + 4 i .. + 3: K bytes
 // 16 i .. + 15 of the half in lanes 0..31 and 64 + 16 i .. in lanes 32..63. The activations come in a layout to
@@ -1189,12 +1189,12 @@ __host__ __device__ constexpr int mx_per_eu() { return 4; }
 __host__ __device__ constexpr int mx_wg_per_cu() { return 4 * mx_per_eu() / mx_waves(); }
 // activation bytes of a job: the records, then the scales
 __host__ __device__ constexpr size_t mx_act_bytes(int ncols, int nb) { return (size_t)ncols * nb * (kMxRecBytes + 8); }
-// a wave's LDS slot: the tile's records, its scales (8 columns' worth) and a zero line for the rows of A past the batch
+// a wave's LDS slot: the tile's records, then its scales (8 columns' worth)
 template <int NCOL>
 struct MxSlot {
     static constexpr int kRecWords = NCOL * kMxRecBytes / 4;
-    uint32_t w[kRecWords + 16 + 4];   // records | scales [8][2] | zero line
-    static constexpr int kScaleWord = kRecWords, kZeroWord = kRecWords + 16;
+    uint32_t w[kRecWords + 16];   // records | scales [8][2]
+    static constexpr int kScaleWord = kRecWords;
 };
 template <int NCOL>
 struct MxSmem {
@@ -1339,7 +1339,6 @@ void k_gemv_wave_mx(const GemvJob *__restrict__ jobs, const uint32_t *__restrict
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     build_coset_table<64 * WAVES>(sm.tab, a2, tid);
     MxSlot<NCOL> &slot = sm.slot[w];
-    if (lane < 4) slot.w[MxSlot<NCOL>::kZeroWord + lane] = 0u;
     __syncthreads();
     const int np = min(kWaveParts, (int)gridDim.x), part = blockIdx.x % np;
     const int nwp = (((int)gridDim.x - 1 - part) / np + 1) * WAVES;
