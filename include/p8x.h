@@ -189,6 +189,12 @@ int p8x_step_run(p8x_step *step, void *stream);
 int p8x_step_check(p8x_step *step);
 int p8x_step_info(const p8x_step *step, int *grid, int *stages, int *class_set);
 void p8x_step_release(p8x_step *step);
+/* The step with the activation mode chosen (the reference CPU path's modes, CPU.patch:1157-1160): P8X_ACT_Q8_128
+ * is p8x_step_create; P8X_ACT_Q8_1 and P8X_ACT_X16 make a step whose p8x_step_run enqueues each stage as its
+ * per-node call (p8x_mul_mat_vec_multi_act, or p8x_mul_mat_vec_glu_act for a swiglu pair) in stage order on the
+ * stream, the same bits as those calls; p8x_step_info reports grid 0 (no cooperative launch), and the step can be
+ * captured in a HIP graph. Same stage checks as p8x_step_create. */
+int p8x_step_create_act(const p8x_step_stage *stages, int n, int act, p8x_step **out);
 /* Prompt GEMM (ggml_cuda_f44_mul_mat_q8, CPU.patch:2303-2343): Y [N][ldy] = X [N][ldx] W^T in ORIGINAL rows,
  * X in P8X_F32 or P8X_BF16 (16-byte aligned, ldx % 8 == 0). The Hadamard rotation is applied to X (fp16 x'),
  * weight tiles are decoded from the LDS coset table straight into fp16 MFMA operands (v S), fp32 accumulation,

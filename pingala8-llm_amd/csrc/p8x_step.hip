@@ -399,6 +399,8 @@ struct p8x_step {
     const uint32_t *a2 = nullptr;
     int device = 0;
     std::vector<const void *> keep;      // tensors and buffers the stages point to (identity only)
+    int act = P8X_ACT_Q8_128;            // block_q8_1 / x16: the stages run as their per-node launches
+    std::vector<p8x_step_stage> host;    // the stages of that form
 };
 
 extern "C" {
@@ -459,8 +461,61 @@ int p8x_step_create(const p8x_step_stage *stages, int n, p8x_step **out) {
     return P8X_OK;
 }
 
+// block_q8_1 or x16 activations: each stage is the per-node call of its kind (p8x_mul_mat_vec_multi_act for one or
+// several tensors on one input, p8x_mul_mat_vec_glu_act for a swiglu pair), enqueued in stage order on the stream;
+// the cooperative launch quantizes its stages' inputs per 128 columns in the stage body and stays q8/128-only.
+int p8x_step_create_act(const p8x_step_stage *stages, int n, int act, p8x_step **out) {
+    if (act == P8X_ACT_Q8_128) return p8x_step_create(stages, n, out);
+    if (act != P8X_ACT_Q8_1 && act != P8X_ACT_X16) return set_error(P8X_ERR_ARG, "p8x_step_create_act: act %d", act);
+    if (!stages || n < 1 || !out) return set_error(P8X_ERR_ARG, "p8x_step_create_act: bad arguments");
+    *out = nullptr;
+    size_t hist[8] = {0};
+    bool in_order = true;
+    for (int s = 0; s < n; ++s) {
+        const p8x_step_stage &st = stages[s];
+        if (st.n < 1 || st.n > kRgMaxJobs) return set_error(P8X_ERR_ARG, "p8x_step_create_act: stage %d has %d tensors (1..%d)", s, st.n, kRgMaxJobs);
+        int rc = check_shared_input(st.tensors, st.n, st.x, st.x ? st.tensors[0]->K : 0, "p8x_step_create_act");
+        if (rc) return rc;
+        const bool glu = st.glu_out != nullptr;
+        if (glu && (st.n != 2 || st.tensors[0]->rows != st.tensors[1]->rows))
+            return set_error(P8X_ERR_ARG, "p8x_step_create_act: stage %d: swiglu needs a gate and an up tensor of the same rows", s);
+        for (int i = 0; i < st.n; ++i) {
+            if (!glu && !st.y[i]) return set_error(P8X_ERR_ARG, "p8x_step_create_act: stage %d output %d is null", s, i);
+            for (int c = 0; c < 8; ++c) hist[c] += st.tensors[i]->class_tiles[c];
+            in_order = in_order && st.tensors[i]->lin_words != 0;
+        }
+    }
+    p8x_step *sp = new p8x_step();
+    sp->nst = n;
+    sp->act = act;
+    sp->cm = class_set(hist, in_order) == kCmC3 ? kCmC3 : kCmAll;
+    (void)hipGetDevice(&sp->device);
+    sp->host.assign(stages, stages + n);
+    for (int s = 0; s < n; ++s)
+        for (int i = 0; i < stages[s].n; ++i) sp->keep.push_back(stages[s].tensors[i]);
+    *out = sp;
+    return P8X_OK;
+}
+
+static int run_per_node(const p8x_step *sp, void *stream) {
+    for (const p8x_step_stage &st : sp->host) {
+        const size_t K = (size_t)st.tensors[0]->K;
+        int rc;
+        if (st.glu_out) {
+            rc = p8x_mul_mat_vec_glu_act(st.tensors[0], st.tensors[1], sp->act, st.x, K, st.glu_out, stream);
+        } else {
+            size_t ldy[kRgMaxJobs];
+            for (int i = 0; i < st.n; ++i) ldy[i] = (size_t)st.tensors[i]->rows;
+            rc = p8x_mul_mat_vec_multi_act(st.tensors, st.n, sp->act, st.x, K, st.y, ldy, stream);
+        }
+        if (rc) return rc;
+    }
+    return P8X_OK;
+}
+
 int p8x_step_run(p8x_step *sp, void *stream) {
     if (!sp) return set_error(P8X_ERR_ARG, "p8x_step_run: null step");
+    if (sp->act != P8X_ACT_Q8_128) return run_per_node(sp, stream);
     if (sp->broken) return set_error(P8X_ERR_HIP, "p8x_step_run: a previous launch gave up waiting (see p8x_step_check)");
     const unsigned spin = 1u << 20;
     hipStream_t st = (hipStream_t)stream;
@@ -471,7 +526,7 @@ int p8x_step_run(p8x_step *sp, void *stream) {
 int p8x_step_check(p8x_step *sp) {
     if (!sp) return set_error(P8X_ERR_ARG, "p8x_step_check: null step");
     int rc = hip_check(hipDeviceSynchronize(), "p8x_step_check");
-    if (rc) return rc;
+    if (rc || !sp->words) return rc;   // the per-node form has no barrier words
     unsigned w[3] = {0, 0, 0};
     rc = hip_check(hipMemcpy(w, sp->words, sizeof w, hipMemcpyDeviceToHost), "p8x_step_check: read");
     if (rc) return rc;

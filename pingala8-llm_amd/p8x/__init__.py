@@ -31,7 +31,7 @@ EXPORTS = [
     "p8x_vr3_expand", "p8x_quantize_x16", "p8x_mul_mat_vec_multi", "p8x_mul_mat_vec_glu", "p8x_mul_mat_vec_multi_act",
     "p8x_mul_mat_vec_glu_act", "p8x_gemv_batch_create_act", "p8x_gemv_batch_create_ex", "p8x_graph_begin", "p8x_decode_tiles",
     "p8x_dequantize_rows", "p8x_vec_dot_rows", "p8x_encode_defaults", "p8x_encode_tensor", "p8x_encode_free",
-    "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_run", "p8x_step_check", "p8x_step_info",
+    "p8x_encode_factor", "p8x_encode_alloc", "p8x_step_create", "p8x_step_create_act", "p8x_step_run", "p8x_step_check", "p8x_step_info",
     "p8x_step_release",
 ]
 
@@ -133,6 +133,7 @@ def lib():
     L.p8x_encode_factor.argtypes = [vp, vp, vp, u64, i, ctypes.c_double, i, vp]
     L.p8x_encode_alloc.argtypes = [vp, i, ctypes.c_double, vp, vp, vp]
     L.p8x_step_create.argtypes = [ctypes.POINTER(StepStageC), i, ctypes.POINTER(vp)]
+    L.p8x_step_create_act.argtypes = [ctypes.POINTER(StepStageC), i, i, ctypes.POINTER(vp)]
     L.p8x_step_run.argtypes = [vp, vp]
     L.p8x_step_check.argtypes = [vp]
     L.p8x_step_info.argtypes = [vp, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)]
@@ -772,9 +773,10 @@ def mul_mat_vec_glu(gate, up, x, act=ACT_Q8_128):
 class Step:
     """A chain of linears in one launch (p8x_step_*). stages: list of (tensors, x, ys) or (tensors, x, None, glu_out)
     with device buffers; stage s may read an earlier stage's output. The step keeps the tensors and buffers alive
-    until release() (the library holds their addresses)."""
+    until release() (the library holds their addresses). act: ACT_Q8_128 (one cooperative launch), ACT_Q8_1 or
+    ACT_X16 (the stages enqueued as their per-node calls)."""
 
-    def __init__(self, stages):
+    def __init__(self, stages, act=ACT_Q8_128):
         self._keep = [list(st) for st in stages]
         arr = (StepStageC * len(stages))()
         for k, st in enumerate(stages):
@@ -789,7 +791,7 @@ class Step:
                     arr[k].y[i] = y.addr
             arr[k].glu_out = glu.addr if glu is not None else None
         self.h = ctypes.c_void_p()
-        check(lib().p8x_step_create(arr, len(stages), ctypes.byref(self.h)), "p8x_step_create")
+        check(lib().p8x_step_create_act(arr, len(stages), act, ctypes.byref(self.h)), "p8x_step_create")
 
     def run(self, stream=None):
         check(lib().p8x_step_run(self.h, stream.h if stream else None), "p8x_step_run")

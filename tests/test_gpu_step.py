@@ -182,3 +182,72 @@ def test_step_keeps_stage_order_for_aliased_outputs():
     for g, w in zip(got, want):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
     step.release()
+
+
+@pytest.mark.parametrize("act", [p8x.ACT_X16, p8x.ACT_Q8_1])
+def test_step_chain_act(act):
+    """x16 and block_q8_1 steps: every stage's output equals the per-node call of that mode bit for bit (poisoned
+    outputs, consecutive runs, HIP graph replays), and each stage is within 1e-5 of the oracle's GEMV of that mode on
+    the stage's input as the step wrote it"""
+    name = "x16" if act == p8x.ACT_X16 else "q8_1"
+    L, head, hosts, head_hosts = build(C3, layers=1, seed=300 + act)
+    rng = np.random.default_rng(10 + act)
+    x0h = rng.standard_normal(HIDDEN).astype(np.float32)
+    x0 = p8x.DeviceBuffer.from_numpy(x0h)
+    stages, outs = chain(L, head, x0)
+    for st in stages:   # the per-node calls of this mode
+        ts, x, ys = st[0], st[1], st[2]
+        if len(st) > 3:
+            p8x.mul_mat_vec_glu_dev(ts[0], ts[1], x, st[3], act=act)
+        else:
+            p8x.mul_mat_vec_multi_dev(ts, x, ys, act=act)
+    p8x.synchronize()
+    want = read(outs)
+    step = p8x.Step(stages, act=act)
+    info = step.info()
+    assert info["stages"] == len(stages) and info["grid"] == 0 and info["class_set"] == 8
+    st = p8x.Stream()
+    graph = p8x.Graph(lambda s: step.run(s), st)
+    for rep in range(3):
+        for b, _ in outs:
+            b.fill(0xFF)
+        if rep == 1:
+            graph.launch(st)
+            st.sync()
+        else:
+            step.run()
+            step.check()
+        got = read(outs)
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), (name, rep, i)
+    graph.release()
+    step.release()
+    orc = [O.Oracle(s, r, K) for s, (r, K) in hosts[0]]
+    orh = [O.Oracle(s, r, K) for s, (r, K) in head_hosts]
+    yq, yk, yv, yo, yg, yd = want[:6]
+    for y, o, nm in ((yq, orc[0], "q"), (yk, orc[1], "k"), (yv, orc[2], "v")):
+        assert rel(y, o.gemv_f64(x0h, act=name)) < 1e-5, (name, nm)
+    assert rel(yo, orc[3].gemv_f64(yq, act=name)) < 1e-5, (name, "o")
+    g, u = orc[4].gemv_f64(yo, act=name), orc[5].gemv_f64(yo, act=name)
+    assert rel(yg, g / (1.0 + np.exp(-g)) * u) < 1e-5, (name, "swiglu")
+    assert rel(yd, orc[6].gemv_f64(yg, act=name)) < 1e-5, (name, "down")
+    for i, o in enumerate(orh):
+        assert rel(want[6 + i], o.gemv_f64(yd, act=name)) < 1e-5, (name, "head", i)
+    for b, _ in outs:
+        b.free()
+    for t in [t for layer in L for t in layer] + head:
+        t.release()
+    x0.free()
+
+
+def test_step_act_rejects_unknown_mode():
+    L, head, _, _ = build(C3, layers=1, seed=400)
+    x0 = p8x.DeviceBuffer.from_numpy(np.ones(HIDDEN, np.float32))
+    stages, outs = chain(L, head, x0)
+    with pytest.raises(p8x.P8xError, match="act 5"):
+        p8x.Step(stages, act=5)
+    for b, _ in outs:
+        b.free()
+    for t in [t for layer in L for t in layer] + head:
+        t.release()
+    x0.free()
