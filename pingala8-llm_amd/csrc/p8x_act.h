@@ -123,4 +123,27 @@ __device__ __forceinline__ void quantize_block_q8_128(const float *__restrict__ 
     quantize_loaded_q8_128(in, lane, packed, dd, sum);
 }
 
+// ggml block_q8_1 of one rotated 256-block (quantize_row_q8_1_ref convention): lane l holds values 4l..4l+3, so the
+// eight lanes 8i..8i+7 form 32-block i: d = max|x'| / 127 over it, q = round-half-away(x' / d), s = d * sum(q).
+// dd and s are the float values the block stores as fp16.
+__device__ __forceinline__ void quantize_block_q8_1(const float *__restrict__ x, const float *__restrict__ ic, int lane, uint32_t &packed,
+                                                    float &dd, float &s) {
+    BlockLane in;
+    in.load(x, ic, lane);
+    float v[4];
+    rotate_block_lane(in, lane, v);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+    dd = div_rn(am, 127.f);
+    const float id = dd != 0.f ? div_rn(1.f, dd) : 0.f;
+    int qi[4], sum = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { qi[e] = (int)roundf(v[e] * id); sum += qi[e]; }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) sum += __shfl_xor(sum, m);
+    s = (float)sum * dd;
+    packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
+}
+
 }  // namespace p8x

@@ -460,6 +460,18 @@ void k_gemv(GemvJob job0, int total_tasks, const uint32_t *__restrict__ a2) {
                 }
                 scales_staged = true;
             }
+        } else if (ACT == P8X_ACT_Q8_1 && !PARTIALS && !J.q) {
+            // block_q8_1 of the chunk's blocks quantized here, one wave per (column, block); the scales staged are
+            // the fp16 values a block_q8_1 stores
+            for (int pi = w; pi < NCOL * c.nbl; pi += WAVES) {
+                const int n = pi / c.nbl, bl = pi % c.nbl;
+                uint32_t packed;
+                float dd, s;
+                quantize_block_q8_1(J.x + (size_t)n * J.ldx + 256 * (c.b0 + bl), J.ic + 256 * (c.b0 + bl), lane, packed, dd, s);
+                sm.xq[n * (kXBytes / 4 / NCOL) + bl * 64 + lane] = packed;
+                if ((lane & 7) == 0) sm.xd[n * NSC + 8 * bl + (lane >> 3)] = half_to_float(float_to_half(dd));
+            }
+            scales_staged = true;
         } else {
             for (int i = tid; i < NCOL * c.nbl * 64; i += NT) {
                 const int n = i / (c.nbl * 64), wi = i % (c.nbl * 64);

@@ -112,27 +112,12 @@ __global__ __launch_bounds__(256) void k_glu_rows(const float *__restrict__ g, c
 __global__ __launch_bounds__(64) void k_act_q8_1(const float *__restrict__ x, size_t ldx, const float *__restrict__ ic, int K,
                                                  uint8_t *__restrict__ blocks) {
     const int b = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    BlockLane in;
-    in.load(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane);
-    float v[4];
-    rotate_block_lane(in, lane, v);
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
-    const float dd = div_rn(am, 127.f);
-    const float id = dd != 0.f ? div_rn(1.f, dd) : 0.f;
-    int qi[4], s = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { qi[e] = (int)roundf(v[e] * id); s += qi[e]; }
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) s += __shfl_xor(s, m);
+    uint32_t packed;
+    float dd, s;
+    quantize_block_q8_1(x + (size_t)n * ldx + 256 * b, ic + 256 * b, lane, packed, dd, s);
     uint8_t *blk = blocks + ((size_t)n * (K / 32) + 8 * b + (lane >> 3)) * 36;
-    const uint32_t packed = (uint32_t)(uint8_t)qi[0] | ((uint32_t)(uint8_t)qi[1] << 8) | ((uint32_t)(uint8_t)qi[2] << 16) | ((uint32_t)(uint8_t)qi[3] << 24);
     reinterpret_cast<uint32_t *>(blk + 4)[lane & 7] = packed;
-    if ((lane & 7) == 0) {
-        const uint32_t ds = (uint32_t)float_to_half(dd) | ((uint32_t)float_to_half((float)s * dd) << 16);
-        *reinterpret_cast<uint32_t *>(blk) = ds;
-    }
+    if ((lane & 7) == 0) *reinterpret_cast<uint32_t *>(blk) = (uint32_t)float_to_half(dd) | ((uint32_t)float_to_half(s) << 16);
 }
 
 // K-split of a single-GEMV launch: about one task per workgroup slot, at least two tiles per wave, chunks no

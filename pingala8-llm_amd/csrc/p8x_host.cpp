@@ -468,12 +468,13 @@ int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols,
     int rc;
     if (act == P8X_ACT_Q8_128)   // one launch: every task quantizes its chunk of x itself (same arithmetic as the prep)
         return launch_gemv(t, act, nullptr, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
-    // x16 and block_q8_1 prepare x in a launch of their own; within a graph evaluation (p8x_graph_begin) a later call on
-    // the same input and rotation reuses the activation the previous call prepared (CPU.patch:1171-1180)
+    // x16 and, within a graph evaluation (p8x_graph_begin), block_q8_1 prepare x in a launch of their own, and a later
+    // call on the same input and rotation reuses the activation the previous call prepared (CPU.patch:1171-1180);
+    // outside one, block_q8_1 is quantized by the GEMV's tasks (one launch)
     bool have = false;
     if (act == P8X_ACT_Q8_1) {
         uint8_t *blk = act_reuse(t, act, x, ncols, ldx, (size_t)36 * ncols * (t->K / 32), st, &have);
-        if (!blk) blk = t->wq81;
+        if (!blk) return launch_gemv(t, act, nullptr, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
         if (!have && (rc = launch_act_q8_1(t, x, ncols, ldx, blk, st))) return rc;
         return launch_gemv(t, act, blk, nullptr, ncols, x, ldx, y, ldy, nullptr, st);
     }
