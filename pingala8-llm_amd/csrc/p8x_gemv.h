@@ -1395,7 +1395,8 @@ static int launch_gemv_wave_mx_t(const GemvJob *jobs, const uint32_t *ujob, int 
 
 // defined in the instantiation units
 int launch_gemv_q8(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
-int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
+// block_q8_1: one column of a class-3 tensor has its own instantiation (cm kCmC3), every other case the generic one
+int launch_gemv_q81(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st);
 int launch_gemv_partials(int act, const GemvJob &job0, const uint32_t *a2, hipStream_t st);
 int launch_gemv_rg(int ncols, int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);
 int launch_gemv_rg_multi(int cm, const RgJobs &jobs, int ng, const uint32_t *a2, hipStream_t st);

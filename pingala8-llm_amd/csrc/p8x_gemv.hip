@@ -145,9 +145,13 @@ int rg_plan(const p8x_tensor *t, int ncols, int *kc) {
     return (t->nb + *kc - 1) / *kc;
 }
 
+static int q81_cm(const p8x_tensor *t, int ncols) {
+    return ncols == 1 && class_set(t->class_tiles, t->lin_words != 0) == kCmC3 ? kCmC3 : kCmAll;
+}
+
 GemvPlan gemv_plan(const p8x_tensor *t, int ncols, int act, bool partials) {
     GemvPlan p;
-    const int cm = partials || act != P8X_ACT_Q8_128 ? kCmAll : class_set(t->class_tiles, t->lin_words != 0);
+    const int cm = partials || act == P8X_ACT_X16 ? kCmAll : act == P8X_ACT_Q8_1 ? q81_cm(t, ncols) : class_set(t->class_tiles, t->lin_words != 0);
     p.gpt = gemv_waves(ncols, act, partials, cm);
     const int octets = (t->ng + p.gpt - 1) / p.gpt;
     const int slots = gemv_wg_per_cu(ncols, act, partials, cm) * num_cus();
@@ -221,7 +225,7 @@ int launch_gemv_range(const p8x_tensor *t, int act, const void *q, const float *
     job0.g0 = g0; job0.gend = g0 + ng;
     job0.ntasks = ((ng + p.gpt - 1) / p.gpt) * p.nks;
     if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, job0, job0.ntasks, t->a2, st);
-    return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
+    return launch_gemv_q81(ncols, q81_cm(t, ncols), job0, job0.ntasks, t->a2, st);
 }
 
 int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int ncols, const float *x, size_t ldx,
@@ -246,7 +250,7 @@ int launch_gemv(const p8x_tensor *t, int act, const void *q, const float *d, int
     GemvJob job0;
     fill_job(job0, t, q, d, x, ldx, y, ldy, nullptr, p.nks, p.bpk, p.gpt, 0);
     if (act == P8X_ACT_Q8_128) return launch_gemv_q8(ncols, cm, job0, job0.ntasks, t->a2, st);
-    return launch_gemv_q81(ncols, job0, job0.ntasks, t->a2, st);
+    return launch_gemv_q81(ncols, q81_cm(t, ncols), job0, job0.ntasks, t->a2, st);
 }
 
 // The row-group plan of several linears on the same activations (out == nullptr), or of a gate / up pair with the

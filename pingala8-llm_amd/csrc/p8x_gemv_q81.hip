@@ -3,7 +3,8 @@
 
 namespace p8x {
 
-int launch_gemv_q81(int ncols, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
+int launch_gemv_q81(int ncols, int cm, const GemvJob &job0, int tasks, const uint32_t *a2, hipStream_t st) {
+    if (ncols == 1 && cm == kCmC3) return launch_gemv_t<1, P8X_ACT_Q8_1, false, kCmC3>(job0, tasks, a2, st);
     switch (ncols) {
         case 1: return launch_gemv_t<1, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
         case 2: return launch_gemv_t<2, P8X_ACT_Q8_1, false, kCmAll>(job0, tasks, a2, st);
