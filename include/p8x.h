@@ -132,7 +132,8 @@ int p8x_vec_dot_rows(const p8x_tensor *t, int act, const void *q, const float *d
  * in the tensor's handle: calls on one tensor from different streams must not overlap (on one stream they are
  * ordered); counters and slots are put back by each call. Records kernel launches only (capture-safe). */
 int p8x_mul_mat_vec(const p8x_tensor *t, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
-/* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1, or P8X_ACT_X16 (1..4
+/* the same with the activation mode chosen: P8X_ACT_Q8_128 (as p8x_mul_mat_vec), P8X_ACT_Q8_1 (ggml block_q8_1 of x',
+ * quantized inside the GEMV's launch, or by a prep launch within a graph evaluation, below), or P8X_ACT_X16 (1..4
  * columns: both planes of each column through one GEMV, summed, then the clamp delta; the reference's CPU default) */
 int p8x_mul_mat_vec_act(const p8x_tensor *t, int act, const float *x, int ncols, size_t ldx, float *y, size_t ldy, void *stream);
 /* Marks the start of a graph evaluation (ggml_vr_cpu_graph_begin, CPU.patch:1148). After the first call, a
