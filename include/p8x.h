@@ -158,10 +158,10 @@ int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *
 int p8x_mul_mat_vec_glu(const p8x_tensor *gate, const p8x_tensor *up, const float *x, size_t ldx, float *out, void *stream);
 /* The two calls above with the activation mode chosen, as p8x_mul_mat_vec_act (the reference's CPU path defaults to
  * x16, CPU.patch:1157-1160, and prepares the activation once for consecutive mul_mats on the same input and c,
- * CPU.patch:1142-1143, :1171-1180): P8X_ACT_Q8_128 runs the one-launch forms above; P8X_ACT_Q8_1 and P8X_ACT_X16
- * prepare x once in tensor 0's (the gate's) workspace and run each tensor's GEMV on it (X16: both planes as two
- * columns, summed, then the clamp delta), then for the GLU silu(gate) * up. Same values as p8x_mul_mat_vec_act per
- * tensor. Calls sharing a tensor are ordered on one stream. */
+ * CPU.patch:1142-1143, :1171-1180): P8X_ACT_Q8_128 runs the one-launch forms above; P8X_ACT_X16 prepares x once in
+ * tensor 0's (the gate's) workspace and runs each tensor's GEMV on it (both planes as two columns, summed, then the
+ * clamp delta); P8X_ACT_Q8_1 runs each tensor's block_q8_1 GEMV with x quantized in its launch; then for the GLU
+ * silu(gate) * up. Same values as p8x_mul_mat_vec_act per tensor. Calls sharing a tensor are ordered on one stream. */
 int p8x_mul_mat_vec_multi_act(const p8x_tensor *const *tensors, int n, int act, const float *x, size_t ldx, float *const *y,
                               const size_t *ldy, void *stream);
 int p8x_mul_mat_vec_glu_act(const p8x_tensor *gate, const p8x_tensor *up, int act, const float *x, size_t ldx, float *out, void *stream);

@@ -808,16 +808,16 @@ int p8x_mul_mat_vec_multi(const p8x_tensor *const *tensors, int n, const float *
     return launch_gemv_multi(tensors, n, x, ldx, y, ldy, nullptr, (hipStream_t)stream);
 }
 
-// The shared-input calls with another activation mode: the activations are prepared once (in tensor 0's workspace:
-// every tensor rotates its input the same way) and each tensor multiplies them; Q8_1: block_q8_1 then the Q8_1 GEMV;
-// X16: both planes as two columns into the tensor's plane rows, then its combine (planes summed, then the delta).
+// The shared-input calls with another activation mode. Q8_1: each tensor's block_q8_1 GEMV quantizes x in its own
+// launch (every tensor rotates its input the same way, so the blocks are the same); X16: the planes are prepared once
+// (in tensor 0's workspace) and each tensor multiplies them as two columns into its plane rows, then its combine
+// (planes summed, then the delta).
 static int multi_act(const p8x_tensor *const *ts, int n, int act, const float *x, size_t ldx, float *const *y, const size_t *ldy, hipStream_t st) {
     const p8x_tensor *t0 = ts[0];
     int rc;
-    if (act == P8X_ACT_Q8_1) {
-        if ((rc = launch_act_q8_1(t0, x, 1, ldx, t0->wq81, st))) return rc;
+    if (act == P8X_ACT_Q8_1) {   // each GEMV's tasks quantize their chunks (the tensors share the rotation)
         for (int i = 0; i < n; ++i)
-            if ((rc = launch_gemv(ts[i], P8X_ACT_Q8_1, t0->wq81, nullptr, 1, x, ldx, y[i], ldy[i], nullptr, st))) return rc;
+            if ((rc = launch_gemv(ts[i], P8X_ACT_Q8_1, nullptr, nullptr, 1, x, ldx, y[i], ldy[i], nullptr, st))) return rc;
         return P8X_OK;
     }
     if ((rc = launch_act_x16(t0, x, 1, ldx, t0->wq, t0->wd, nullptr, t0->wq + t0->K, t0->wd + t0->nsl, nullptr, 2 * t0->K, st))) return rc;
